@@ -1,0 +1,352 @@
+#!/usr/bin/env python3
+"""Benchmark of the burn-rocket MI355X op surface on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu-baseline]
+
+A step is one pass of the headline workload: the Q8_0/W8A8 MLP GEMMs at
+M=3633 tokens — up-projection K=1024→N=3072 and down-projection K=3072→N=1024
+— on per-token int8 activations and Q8_0 weights that are resident in HBM
+when the timed region starts. `value` is int8 tera-ops per second over the K
+timed steps (2·M·K·N per GEMM), measured with HIP events on the library
+stream. `roofline` is the up-projection kernel's own average launch time
+(events around each launch inside the timed region) against the MI355X dense
+int8 MFMA peak. `extras` times the other four workloads the same way;
+`cpu_baseline` times the CPU restatement of the reference's W8A8 path on the
+host cores over a bounded sample of rows.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "burn-rocket_amd"))
+
+import numpy as np  # noqa: E402
+
+import burn_rocket as rk  # noqa: E402
+from burn_rocket import synth  # noqa: E402
+
+METRIC = "GEMM & GQA-attn TFLOP/s + % MFMA peak on 1 MI355X vs host-CPU Burn path"
+PEAK_FP16 = 2516.6  # TFLOP/s dense
+PEAK_INT8 = 5033.2  # TOP/s dense
+PEAK_HBM = 8000.0   # GB/s
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def dev(a):
+    return rk.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+def call(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what}: {rk.lib().rk_last_error().decode()}")
+
+
+def time_launches(fn, iters, warmup=3):
+    """Average ms per call of fn() measured with events on the library stream."""
+    for _ in range(warmup):
+        fn()
+    rk.synchronize()
+    e0, e1 = rk.Event(), rk.Event()
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    rk.synchronize()
+    return e0.elapsed_ms(e1) / iters
+
+
+# ------------------------------------------------------------ config 2 ----
+def setup_w8a8():
+    c = synth.W8A8
+    s1, s2, s3 = synth.SEEDS["w8a8"]
+    m, h, i = c["m"], c["hidden"], c["inter"]
+    lib = rk.lib()
+    layers = []
+    for name, k, n, sx, sw in (("up", h, i, s1, s2), ("down", i, h, s1 + 1000, s3)):
+        x = synth.normal_f32(sx, (m, k))
+        w = synth.normal_f32(sw, (n, k), 0.02)
+        wid = rk.pack_q8_0_f32(w)
+        dx = dev(x)
+        dq, ds = rk.DeviceBuffer(m * k), rk.DeviceBuffer(m * 4)
+        call(lib.rk_quantize_rows_dev(dx.ptr, m, k, k, dq.ptr, ds.ptr, None), "quantize")
+        dc = rk.DeviceBuffer(m * n * 4)
+        layers.append(dict(name=name, m=m, k=k, n=n, wid=wid, dx=dx, dq=dq, ds=ds, dc=dc,
+                           sha_x=synth.sha256(x), sha_w=synth.sha256(w)))
+    rk.synchronize()
+    return layers
+
+
+def gemm_w8a8(L):
+    call(rk.lib().rk_matmul_w8a8_dev(int(L["wid"]), L["dq"].ptr, L["ds"].ptr, L["k"], L["m"], L["k"],
+                                     L["dc"].ptr, None), "w8a8")
+
+
+def run_headline(layers, steps, warmup):
+    up, down = layers
+    for _ in range(warmup):
+        gemm_w8a8(up)
+        gemm_w8a8(down)
+    rk.synchronize()
+    ev_a = [rk.Event() for _ in range(steps)]
+    ev_b = [rk.Event() for _ in range(steps)]
+    e0, e1 = rk.Event(), rk.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    for s in range(steps):
+        ev_a[s].record()
+        gemm_w8a8(up)
+        ev_b[s].record()
+        gemm_w8a8(down)
+    e1.record()
+    rk.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1) / steps
+    up_ms = float(np.mean([a.elapsed_ms(b) for a, b in zip(ev_a, ev_b)]))
+    return ms, up_ms, wall
+
+
+def load_traffic(kernel_key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        return json.load(open(path)).get(kernel_key, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+# -------------------------------------------------------------- extras ----
+def extra_gemm_f16(iters):
+    c = synth.GEMM_F16
+    s1, s2 = synth.SEEDS["gemm_f16"]
+    m, k, n = c["m"], c["k"], c["n"]
+    a = synth.normal_f16(s1, (m, k))
+    b = synth.normal_f16(s2, (n, k), 0.02)
+    lib = rk.lib()
+    wid = rk.pack(b)
+    da, dc = dev(a.view(np.uint16)), rk.DeviceBuffer(m * n * 2)
+    ms = time_launches(lambda: call(lib.rk_matmul_f16_dev(int(wid), da.ptr, m, k, dc.ptr, None), "f16"), iters)
+    flop = 2.0 * m * n * k
+    # Rotating copies of A and B (> 256 MB) so the operands come from HBM, not the MALL.
+    reps = 40
+    wids = [rk.pack(b) for _ in range(reps)]
+    das = [dev(a.view(np.uint16)) for _ in range(reps)]
+    state = {"i": 0}
+
+    def rot():
+        j = state["i"] % reps
+        state["i"] += 1
+        call(lib.rk_matmul_f16_dev(int(wids[j]), das[j].ptr, m, k, dc.ptr, None), "f16")
+
+    ms_rot = time_launches(rot, reps * 5)
+    return {"shape": f"{m}x{k}x{n}", "ms": ms, "tflops": flop / ms / 1e9, "frac_fp16_peak": flop / ms / 1e9 / PEAK_FP16,
+            "ms_rotating": ms_rot, "tflops_rotating": flop / ms_rot / 1e9}
+
+
+def attn_flops(s_q, s_k, h, d, causal):
+    if causal:
+        return 2.0 * d * h * s_q * (s_q + 1)  # unmasked (q, k) pairs, QKᵀ and PV
+    return 4.0 * s_q * s_k * d * h
+
+
+def time_attention(s, h, kv, d, causal, seeds, iters):
+    q = synth.normal_f16(seeds[0], (s, h * d))
+    k = synth.normal_f16(seeds[1], (s, kv * d))
+    v = synth.normal_f16(seeds[2], (s, kv * d))
+    dq, dk, dv = dev(q.view(np.uint16)), dev(k.view(np.uint16)), dev(v.view(np.uint16))
+    do = rk.DeviceBuffer(s * h * d * 2)
+    lib = rk.lib()
+    mode = 1 if causal else 0
+    ms = time_launches(lambda: call(lib.rk_attention_dev(dq.ptr, dk.ptr, dv.ptr, s, s, h, kv, d, d ** -0.5, 0.0,
+                                                         mode, -1, 0, 0, do.ptr, None), "attn"), iters)
+    fl = attn_flops(s, s, h, d, causal)
+    return {"shape": f"S={s} H={h} KV={kv} D={d} {'causal' if causal else 'bidirectional'}", "ms": ms,
+            "tflops": fl / ms / 1e9, "frac_fp16_peak": fl / ms / 1e9 / PEAK_FP16}
+
+
+def extra_vision(iters):
+    c = synth.VISION
+    s, hid, h, d, mlp = c["s"], c["hidden"], c["n_head"], c["d"], c["mlp"]
+    seeds = synth.SEEDS["vision"]
+    lib = rk.lib()
+    x = synth.normal_f16(seeds[0], (s, max(hid, mlp)))
+    dx = dev(x.view(np.uint16))
+    out = {}
+    total_ms, total_fl = 0.0, 0.0
+    for i, (name, n, k) in enumerate((("qkv", 3 * hid, hid), ("out", hid, hid), ("fc1", mlp, hid), ("fc2", hid, mlp))):
+        w = synth.normal_f16(seeds[1 + i], (n, k), 0.02)
+        wid = rk.pack(w)
+        xa = dev(x[:, :k].copy().view(np.uint16))
+        dc = rk.DeviceBuffer(s * n * 2)
+        ms = time_launches(lambda: call(lib.rk_matmul_f16_dev(int(wid), xa.ptr, s, k, dc.ptr, None), "f16"), iters)
+        fl = 2.0 * s * n * k
+        out[name] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp16_peak": fl / ms / 1e9 / PEAK_FP16}
+        total_ms += ms
+        total_fl += fl
+    att = time_attention(s, h, h, d, False, seeds[6:9], iters)
+    out["attention"] = att
+    total_ms += att["ms"]
+    total_fl += attn_flops(s, s, h, d, False)
+    out["layer"] = {"ms": total_ms, "tflops": total_fl / total_ms / 1e9}
+    return out
+
+
+def extra_moe(iters):
+    c = synth.MOE
+    S, H, E, K, I = c["s"], c["hidden"], c["experts"], c["top_k"], c["inter"]
+    seeds = synth.SEEDS["moe"]
+    log("generating MoE expert weights")
+    gate = synth.normal_f32(seeds[2], (E, I, H), 0.02)
+    up = synth.normal_f32(seeds[3], (E, I, H), 0.02)
+    down = synth.normal_f32(seeds[4], (E, H, I), 0.02)
+    wid = rk.pack_moe_f32(gate, up, down)
+    del gate, up, down
+    x = synth.normal_f32(seeds[0], (S, H))
+    ids, wts = rk.moe_route(synth.normal_f32(seeds[1], (S, E)), K)
+    lib = rk.lib()
+    import ctypes
+    plan = ctypes.c_void_p()
+    ids_c, wts_c = np.ascontiguousarray(ids), np.ascontiguousarray(wts)
+    call(lib.rk_moe_plan_create(int(wid), S, K, ids_c.ctypes.data, wts_c.ctypes.data, ctypes.byref(plan)), "plan")
+    dx, dy = dev(x), rk.DeviceBuffer(S * H * 4)
+    ms = time_launches(lambda: call(lib.rk_moe_experts_planned_dev(int(wid), plan, dx.ptr, dy.ptr, None), "moe"),
+                       iters)
+    call(lib.rk_moe_plan_destroy(plan), "plan")
+    ops = 2.0 * S * K * (2 * I * H + H * I)
+    weight_bytes = E * (2 * I * H + H * I) * 34 / 32  # Q8_0 codes + f16 scales
+    act_bytes = 23.1e6
+    att = time_attention(S, c["attn_heads"], c["attn_kv"], c["attn_d"], True, seeds[6:9], iters)
+    return {"experts": {"ms": ms, "tops": ops / ms / 1e9, "frac_int8_peak": ops / ms / 1e9 / PEAK_INT8,
+                        "gbps_algorithmic": (weight_bytes + act_bytes) / ms / 1e6,
+                        "frac_hbm": (weight_bytes + act_bytes) / ms / 1e6 / PEAK_HBM},
+            "attention": att}
+
+
+# --------------------------------------------------------- CPU baseline ----
+def cpu_baseline(layers, budget_s):
+    """The reference's W8A8 formula (emu_matmul_gw) on the host cores."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    threads = os.cpu_count() or 1
+    c = synth.W8A8
+    s1, s2, s3 = synth.SEEDS["w8a8"]
+    rows = 64
+    data = []
+    for (k, n, sx, sw) in ((c["hidden"], c["inter"], s1, s2), (c["inter"], c["hidden"], s1 + 1000, s3)):
+        x = synth.normal_f32(sx, (c["m"], k))
+        w = synth.normal_f32(sw, (n, k), 0.02)
+        wq, wd = oracle.q8_0_quantize(w)
+        data.append((x, wq, wd.view(np.float16).astype(np.float32), k))
+    # grow the row sample until one up+down pass takes a measurable time
+    ops_done, t_done, samples = 0.0, 0.0, []
+    r0 = 0
+    while t_done < budget_s and r0 < c["m"]:
+        r1 = min(c["m"], r0 + rows)
+        t = time.perf_counter()
+        ops = 0.0
+        for x, wq, ws, k in data:
+            aq, a_s = oracle.quantize_rows(x[r0:r1], k, threads)
+            oracle.emu_matmul_gw(aq, a_s, k, wq, ws, 32, threads)
+            ops += 2.0 * (r1 - r0) * k * wq.shape[0]
+        dt = time.perf_counter() - t
+        samples.append(ops / dt / 1e12)
+        ops_done += ops
+        t_done += dt
+        r0 = r1
+        rows = min(rows * 2, 1024)
+    return {"value": ops_done / t_done / 1e12, "unit": "TOP/s", "cores": threads, "kind": "port",
+            "sample": f"rows 0..{r0} of the M=3633 up- and down-projection (per-token quantize + "
+                      f"emu_matmul_gw formula, OpenMP over rows), {t_done:.1f} s of CPU time",
+            "best": max(samples), "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported on this single-GPU build "
+              "(the multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(2)
+
+    rk.init(0)
+    name, cus, clk = rk.device_info()
+    log(f"device {name}, {cus} CUs, {clk / 1e3:.0f} MHz")
+    layers = setup_w8a8()
+    log("W8A8 config ready; timing")
+    ms, up_ms, wall = run_headline(layers, a.steps, a.warmup)
+    m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]
+    ops_gemm = 2.0 * m * h * i
+    value = 2 * ops_gemm / ms / 1e9
+    achieved = ops_gemm / up_ms / 1e9
+    log(f"step {ms:.4f} ms, up-proj {up_ms:.4f} ms, {value:.1f} TOP/s")
+
+    extras = {}
+    if not a.no_extras:
+        for key, fn in (("gemm_f16_512x1024x3072", lambda: extra_gemm_f16(200)),
+                        ("gqa_causal_3633", lambda: time_attention(
+                            synth.GQA_CAUSAL["s"], synth.GQA_CAUSAL["n_head"], synth.GQA_CAUSAL["n_kv"],
+                            synth.GQA_CAUSAL["d"], True, synth.SEEDS["gqa"], 50)),
+                        ("vision_layer_2394", lambda: extra_vision(50)),
+                        ("moe_30b_a3b_1024", lambda: extra_moe(20))):
+            log(f"extra {key}")
+            extras[key] = fn()
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        log("CPU baseline")
+        cpu = cpu_baseline(layers, a.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: splitmix64 + Box-Muller normals, seeds " + str(synth.SEEDS["w8a8"]),
+        "config": {"workload": "Q8_0/W8A8 MLP GEMMs, M=3633 tokens: up K=1024->N=3072 + down K=3072->N=1024, "
+                               "per-token int8 activations, Q8_0 (32-value block) weights, f32 out",
+                   "ops_per_step": 2 * ops_gemm, "sha256_x_up": layers[0]["sha_x"][:16],
+                   "sha256_w_up": layers[0]["sha_w"][:16], "wall_s": round(wall, 4)},
+        "roofline": {"bound": "mfma", "kernel": "gemm_i8_kernel (up-projection, PER_TOKEN)",
+                     "achieved": round(achieved, 2), "peak": PEAK_INT8, "unit": "TOP/s",
+                     "frac": round(achieved / PEAK_INT8, 4),
+                     "frac_of_fp16_peak": round(achieved / PEAK_FP16, 4),
+                     "avg_launch_ms": round(up_ms, 5), "algorithmic_ops_per_launch": ops_gemm,
+                     "traffic": load_traffic("w8a8_up")},
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,467 @@
+"""Python binding of the burn-rocket MI355X op surface (libburn_rocket_amd.so).
+
+The functions mirror the helper API of crates/burn-rocket/src/ext.rs
+(`init`, `pack`, `pack2`, `pack3`, `pack_i8`, `pack_qat`, `matmul`,
+`attention*`, `stats`, `mem_stats`, `trim_scratch_to`, `clear_scratch`,
+ext.rs:171-308, ext.rs:561-580, ext.rs:1382-1425, ext.rs:1864-2137) over
+numpy arrays, plus device-buffer plumbing for callers that keep tensors in HBM.
+Every call goes through the C ABI declared in include/burn_rocket_amd.h; there
+is no CPU fallback — a missing library or device raises.
+
+Errors: a non-zero status from the library raises `RocketError` carrying the
+op name and the status code (-1 shape … -7 io), as `burn_rocket::Error`
+(lib.rs:119-156) does; `OpFailure` adds the m/k/n of the call (lib.rs:160-167).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libburn_rocket_amd.so")
+
+RK_OK = 0
+RK_E_SHAPE, RK_E_TILING, RK_E_NOMEM, RK_E_DEVICE = -1, -2, -3, -4
+RK_E_UNSUPPORTED, RK_E_RANGE, RK_E_IO = -5, -6, -7
+RK_WEIGHT_F16, RK_WEIGHT_I8, RK_WEIGHT_QAT = 1, 2, 3
+MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_CAUSAL_WINDOW = 0, 1, 2, 3
+
+# Every entry point of include/burn_rocket_amd.h with its ctypes signature.
+_c = ctypes
+_p, _i, _i64, _u64, _f, _sz = _c.c_void_p, _c.c_int, _c.c_int64, _c.c_uint64, _c.c_float, _c.c_size_t
+SIGNATURES = {
+    "rk_init": (_i, [_i]),
+    "rk_last_error": (_c.c_char_p, []),
+    "rk_is_fallback": (_i, [_i]),
+    "rk_stats": (_i, [_p]),
+    "rk_stats_reset": (_i, []),
+    "rk_mem_stats": (_i, [_p]),
+    "rk_trim_scratch_to": (_i, [_u64]),
+    "rk_clear_scratch": (_i, []),
+    "rk_pack": (_i, [_p, _i64, _i64, _p]),
+    "rk_pack_f16": (_i, [_p, _i64, _i64, _p]),
+    "rk_pack_seg": (_i, [_p, _p, _i, _i64, _p]),
+    "rk_pack_i8": (_i, [_p, _i64, _i64, _i64, _p]),
+    "rk_pack_i8_codes": (_i, [_p, _p, _i64, _i64, _i64, _p]),
+    "rk_rewrite_i8": (_i, [_u64, _p, _p]),
+    "rk_pack_q8_0": (_i, [_p, _i64, _i64, _p]),
+    "rk_pack_q8_0_f32": (_i, [_p, _i64, _i64, _p]),
+    "rk_pack_qat": (_i, [_p, _p, _i64, _i64, _f, _f, _p]),
+    "rk_weight_info": (_i, [_u64, _p, _p, _p, _p]),
+    "rk_matmul": (_i, [_u64, _p, _i64, _i64, _p]),
+    "rk_matmul_f16_dev": (_i, [_u64, _p, _i64, _i64, _p, _p]),
+    "rk_quantize_rows_dev": (_i, [_p, _i64, _i64, _i64, _p, _p, _p]),
+    "rk_matmul_w8a8_dev": (_i, [_u64, _p, _p, _i64, _i64, _i64, _p, _p]),
+    "rk_matmul_w8a8_f16out_dev": (_i, [_u64, _p, _p, _i64, _i64, _i64, _p, _p]),
+    "rk_matmul_i8_raw_dev": (_i, [_u64, _p, _i64, _i64, _p, _p]),
+    "rk_matmul_i8_partials_dev": (_i, [_u64, _p, _i64, _i64, _p, _p]),
+    "rk_attention": (_i, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p]),
+    "rk_attention_dev": (_i, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p]),
+    "rk_flash_attn_f16": (_i, [_i64, _i64, _i, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "rk_moe_route": (_i, [_p, _i64, _i, _i, _i, _p, _p]),
+    "rk_pack_moe_q8_0": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
+    "rk_pack_moe_f32": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
+    "rk_moe_experts_dev": (_i, [_u64, _p, _i64, _i, _p, _p, _p, _p]),
+    "rk_moe_plan_create": (_i, [_u64, _i64, _i, _p, _p, _p]),
+    "rk_moe_experts_planned_dev": (_i, [_u64, _p, _p, _p, _p]),
+    "rk_moe_plan_destroy": (_i, [_p]),
+    "rk_device_alloc": (_i, [_sz, _p]),
+    "rk_device_free": (_i, [_p]),
+    "rk_memcpy_htod": (_i, [_p, _p, _sz]),
+    "rk_memcpy_dtoh": (_i, [_p, _p, _sz]),
+    "rk_memset_dev": (_i, [_p, _i, _sz]),
+    "rk_stream_get": (_i, [_p]),
+    "rk_stream_sync": (_i, [_p]),
+    "rk_event_create": (_i, [_p]),
+    "rk_event_destroy": (_i, [_p]),
+    "rk_event_record": (_i, [_p, _p]),
+    "rk_event_elapsed_ms": (_i, [_p, _p, _p]),
+    "rk_device_info": (_i, [_c.c_char_p, _sz, _p, _p]),
+}
+
+
+class RocketError(RuntimeError):
+    """A failed op: `op` name and status code `rc` (lib.rs:119-156)."""
+
+    def __init__(self, op, rc, message):
+        super().__init__(message)
+        self.op, self.rc = op, rc
+
+    def is_fallback(self):
+        return self.rc == RK_E_TILING
+
+
+class OpFailure(RocketError):
+    """A failed matmul/attention with the shape of the call (lib.rs:160-167)."""
+
+    def __init__(self, op, rc, message, m=0, k=0, n=0):
+        super().__init__(op, rc, message)
+        self.m, self.k, self.n = m, k, n
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    """Load the C-ABI library (no initialisation, no device access)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RocketError("load", RK_E_IO, f"{path} is missing: run burn-rocket_amd/build.py")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    _lib = lib
+    return lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def _check(rc, op, m=0, k=0, n=0):
+    if rc != RK_OK:
+        msg = _lib.rk_last_error().decode()
+        raise OpFailure(op, rc, msg or f"{op} failed (rc={rc})", m, k, n)
+
+
+def init(device=0):
+    """Create the global engine (`burn_rocket::init`, ext.rs:561-580)."""
+    lib = load_library()
+    _check(lib.rk_init(device), "rk_init")
+
+
+class WeightId(int):
+    """Registry id of a resident weight (`WeightId`, ext.rs:39-51)."""
+
+    def id(self):
+        return int(self)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def pack(w):
+    """Resident fp16 weight from an [N, K] f32/f16 array (`pack`, ext.rs:1866)."""
+    w = np.asarray(w)
+    assert w.ndim == 2, "weights are [N, K]"
+    n, k = w.shape
+    out = ctypes.c_uint64()
+    if w.dtype == np.float16:
+        w16 = np.ascontiguousarray(w).view(np.uint16)
+        _check(_lib.rk_pack_f16(_ptr(w16), n, k, ctypes.byref(out)), "rocket_weights_pack", 0, k, n)
+    else:
+        wf = _f32(w)
+        _check(_lib.rk_pack(_ptr(wf), n, k, ctypes.byref(out)), "rocket_weights_pack", 0, k, n)
+    return WeightId(out.value)
+
+
+def _pack_many(parts):
+    parts = [_f32(p) for p in parts]
+    k = parts[0].shape[1]
+    assert all(p.ndim == 2 and p.shape[1] == k for p in parts), "all parts must share K"
+    ptrs = (ctypes.c_void_p * len(parts))(*[p.ctypes.data for p in parts])
+    ns = (ctypes.c_int64 * len(parts))(*[p.shape[0] for p in parts])
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_seg(ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(ns, ctypes.c_void_p),
+                            len(parts), k, ctypes.byref(out)), "rocket_weights_pack_seg")
+    return WeightId(out.value)
+
+
+def pack2(a, b):
+    """Two weights sharing one input, concatenated along N (ext.rs:1870)."""
+    return _pack_many([a, b])
+
+
+def pack3(a, b, c):
+    """Three weights sharing one input, concatenated along N (ext.rs:1879)."""
+    return _pack_many([a, b, c])
+
+
+def pack_i8(w, group):
+    """Resident group-wise int8 weight (`pack_i8`, ext.rs:1892)."""
+    wf = _f32(w)
+    n, k = wf.shape
+    assert group > 0 and group % 32 == 0 and k % group == 0, \
+        f"int8 group {group} must be a positive multiple of 32 dividing K={k}"
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_i8(_ptr(wf), n, k, group, ctypes.byref(out)), "rocket_i8_weights_pack_gw", 0, k, n)
+    return WeightId(out.value)
+
+
+def pack_i8_codes(codes, scales, group):
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    scales = _f32(scales)
+    n, k = codes.shape
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_i8_codes(_ptr(codes), _ptr(scales), n, k, group, ctypes.byref(out)),
+           "rocket_i8_weights_pack_gw", 0, k, n)
+    return WeightId(out.value)
+
+
+def rewrite_i8(wid, codes, scales):
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    scales = _f32(scales)
+    _check(_lib.rk_rewrite_i8(int(wid), _ptr(codes), _ptr(scales)), "rocket_i8_rewrite_gw")
+
+
+def pack_q8_0(blocks, n, k):
+    """Resident weight from GGUF Q8_0 blocks (34 bytes per 32 values)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    assert blocks.size == n * (k // 32) * 34, "Q8_0 blob size"
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_q8_0(_ptr(blocks), n, k, ctypes.byref(out)), "rocket_q8_0_pack", 0, k, n)
+    return WeightId(out.value)
+
+
+def pack_q8_0_f32(w):
+    """Resident Q8_0 weight quantized on the device from f32 [N, K]."""
+    wf = _f32(w)
+    n, k = wf.shape
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_q8_0_f32(_ptr(wf), n, k, ctypes.byref(out)), "rocket_q8_0_pack", 0, k, n)
+    return WeightId(out.value)
+
+
+def pack_qat(codes, w_scale, n, k, in_scale, out_scale):
+    """Per-channel QAT weight (`pack_qat`, ext.rs:1382-1425)."""
+    codes = np.ascontiguousarray(codes, dtype=np.int8).reshape(n, k)
+    w_scale = _f32(w_scale)
+    assert w_scale.size == n, "one weight scale per output channel"
+    assert in_scale >= 0.0, "QAT input scale must not be negative"
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_qat(_ptr(codes), _ptr(w_scale), n, k, in_scale, out_scale, ctypes.byref(out)),
+           "rocket_i8_weights_pack", 0, k, n)
+    return WeightId(out.value)
+
+
+def weight_info(wid):
+    kind, n, k, g = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    _check(_lib.rk_weight_info(int(wid), ctypes.byref(kind), ctypes.byref(n), ctypes.byref(k), ctypes.byref(g)),
+           "weight_info")
+    return kind.value, n.value, k.value, g.value
+
+
+def matmul(x, wid):
+    """`x[.., M, K] @ W[N, K]ᵀ -> [.., M, N]` (`matmul`, ext.rs:1900); f32 in/out."""
+    x = np.asarray(x)
+    assert x.ndim >= 2, "matmul needs at least [M, K]"
+    k = x.shape[-1]
+    m = int(np.prod(x.shape[:-1]))
+    _, n, wk, _ = weight_info(wid)
+    assert wk == k, f"activation K mismatch for weight id {int(wid)}"
+    xf = _f32(x).reshape(m, k)
+    y = np.empty((m, n), dtype=np.float32)
+    _check(_lib.rk_matmul(int(wid), _ptr(xf), m, k, _ptr(y)), "rocket_matmul", m, k, n)
+    return y.reshape(*x.shape[:-1], n).astype(x.dtype if x.dtype in (np.float16, np.float32) else np.float32)
+
+
+def _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, mode, window, q0, k0):
+    q, k, v = np.asarray(q), np.asarray(k), np.asarray(v)
+    assert q.ndim == 3 and q.shape[0] == 1, "attention input must be [1, S, H*D] (batch 1)"
+    assert q.shape[2] == n_head * head_dim, "q width must be n_head * head_dim"
+    n, n_k = q.shape[1], k.shape[1]
+    assert k.shape == (1, n_k, n_kv_heads * head_dim), "k must be [1, S, KV*D]"
+    assert v.shape == (1, n_k, n_kv_heads * head_dim), "v must be [1, S, KV*D]"
+    out = np.empty((n, n_head * head_dim), dtype=np.float32)
+    qf, kf, vf = _f32(q[0]), _f32(k[0]), _f32(v[0])
+    _check(_lib.rk_attention(_ptr(qf), _ptr(kf), _ptr(vf), n, n_k, n_head, n_kv_heads, head_dim,
+                             float(scale), float(softcap or 0.0), mode, window, q0, k0, _ptr(out)),
+           "rocket_flash_attn_fp16_ctx", n, n_k, head_dim)
+    return out.reshape(1, n, n_head * head_dim).astype(q.dtype if q.dtype == np.float16 else np.float32)
+
+
+def attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap=None, is_causal=False):
+    """Masked GQA attention (`attention`, ext.rs:1910)."""
+    mode = MASK_CAUSAL if is_causal else MASK_NONE
+    return _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, mode, -1, 0, 0)
+
+
+def attention_window(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, window):
+    """|t - j| <= window, window < 0 = no mask (ext.rs:1938)."""
+    return _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, MASK_WINDOW, window, 0, 0)
+
+
+def attention_causal_window(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, window):
+    """t - window < j <= t, window < 0 = causal (ext.rs:1966)."""
+    return _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, MASK_CAUSAL_WINDOW, window, 0, 0)
+
+
+def attention_window_block(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, window, q_start, kv_start):
+    """Band over a query chunk at absolute offsets (ext.rs:1996)."""
+    return _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, MASK_WINDOW, window, q_start,
+                      kv_start)
+
+
+def attention_causal_block(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, q_start, kv_start):
+    """Causal over a query chunk at absolute offsets (ext.rs:2034)."""
+    return _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, MASK_CAUSAL, -1, q_start,
+                      kv_start)
+
+
+def attention_causal_block_window(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, window, q_start,
+                                  kv_start):
+    """Causal sliding window over a query chunk (ext.rs:2068)."""
+    return _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, MASK_CAUSAL_WINDOW, window,
+                      q_start, kv_start)
+
+
+def flash_attn_f16(q, k, v, n_q, n_kv, head_dim, n_head, n_kv_heads, scale, softcap=0.0, mode=MASK_NONE,
+                   window=-1, q0=0, k0=0):
+    """Head-major fp16 attention (`RocketFaCtx::flash_attn` layout, lib.rs:294-323):
+    q [H][n_q][D], k [KV][n_kv][D], v [KV][D][n_kv] → out [H][n_q][D] (fp16)."""
+    q16 = np.ascontiguousarray(q, dtype=np.float16).view(np.uint16)
+    k16 = np.ascontiguousarray(k, dtype=np.float16).view(np.uint16)
+    v16 = np.ascontiguousarray(v, dtype=np.float16).view(np.uint16)
+    out = np.empty(n_head * n_q * head_dim, dtype=np.uint16)
+    _check(_lib.rk_flash_attn_f16(n_q, n_kv, head_dim, head_dim, n_head, n_kv_heads, float(scale),
+                                  float(softcap), mode, window, q0, k0, _ptr(q16), _ptr(k16), _ptr(v16),
+                                  _ptr(out)), "rocket_flash_attn_fp16_ctx", n_q, n_kv, head_dim)
+    return out.view(np.float16).reshape(n_head, n_q, head_dim)
+
+
+def moe_route(logits, top_k, norm_topk=True):
+    """Router top-k (`route`, src/clef/model.rs:462-489): ids [s, k], weights [s, k]."""
+    logits = _f32(logits)
+    s, e = logits.shape
+    ids = np.empty((s, top_k), dtype=np.uint32)
+    wts = np.empty((s, top_k), dtype=np.float32)
+    _check(_lib.rk_moe_route(_ptr(logits), s, e, top_k, int(norm_topk), _ptr(ids), _ptr(wts)), "route")
+    return ids, wts
+
+
+def pack_moe_q8_0(gate_blocks, up_blocks, down_blocks, n_experts, hidden, inter):
+    g = np.ascontiguousarray(gate_blocks, dtype=np.uint8)
+    u = np.ascontiguousarray(up_blocks, dtype=np.uint8)
+    d = np.ascontiguousarray(down_blocks, dtype=np.uint8)
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_moe_q8_0(_ptr(g), _ptr(u), _ptr(d), n_experts, hidden, inter, ctypes.byref(out)),
+           "pack_moe")
+    return WeightId(out.value)
+
+
+def pack_moe_f32(gate, up, down):
+    """Expert stack from f32 gate/up [E, I, H] and down [E, H, I], Q8_0 on device."""
+    g, u, d = _f32(gate), _f32(up), _f32(down)
+    E, I, H = g.shape
+    assert u.shape == (E, I, H) and d.shape == (E, H, I)
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_moe_f32(_ptr(g), _ptr(u), _ptr(d), E, H, I, ctypes.byref(out)), "pack_moe")
+    return WeightId(out.value)
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [("convert_s", ctypes.c_double), ("npu_s", ctypes.c_double), ("calls", ctypes.c_uint64)]
+
+
+class MemStats(ctypes.Structure):
+    _fields_ = [("weights_bytes", ctypes.c_uint64), ("scratch_bytes", ctypes.c_uint64),
+                ("n_weights", ctypes.c_uint64)]
+
+
+def stats():
+    s = Stats()
+    _check(_lib.rk_stats(ctypes.byref(s)), "stats")
+    return s
+
+
+def stats_reset():
+    _check(_lib.rk_stats_reset(), "stats_reset")
+
+
+def mem_stats():
+    s = MemStats()
+    _check(_lib.rk_mem_stats(ctypes.byref(s)), "mem_stats")
+    return s
+
+
+def trim_scratch_to(budget):
+    _check(_lib.rk_trim_scratch_to(int(budget)), "trim_scratch_to")
+
+
+def clear_scratch():
+    _check(_lib.rk_clear_scratch(), "clear_scratch")
+
+
+# ------------------------------------------------------------- device buffers
+class DeviceBuffer:
+    """Device memory owned through the library (no torch, one HIP runtime)."""
+
+    def __init__(self, nbytes):
+        p = ctypes.c_void_p()
+        _check(_lib.rk_device_alloc(int(nbytes), ctypes.byref(p)), "device_alloc")
+        self.ptr, self.nbytes = p.value, int(nbytes)
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        _check(_lib.rk_memcpy_htod(ctypes.c_void_p(self.ptr), _ptr(a), a.nbytes), "memcpy_htod")
+
+    def download(self, shape, dtype):
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        _check(_lib.rk_memcpy_dtoh(_ptr(out), ctypes.c_void_p(self.ptr), out.nbytes), "memcpy_dtoh")
+        return out
+
+    def zero(self):
+        _check(_lib.rk_memset_dev(ctypes.c_void_p(self.ptr), 0, self.nbytes), "memset")
+
+    def free(self):
+        if self.ptr:
+            _check(_lib.rk_device_free(ctypes.c_void_p(self.ptr)), "device_free")
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.rk_device_free(ctypes.c_void_p(self.ptr))
+        except Exception:
+            pass
+
+
+def stream():
+    s = ctypes.c_void_p()
+    _check(_lib.rk_stream_get(ctypes.byref(s)), "stream_get")
+    return s.value
+
+
+def synchronize(st=None):
+    _check(_lib.rk_stream_sync(ctypes.c_void_p(st) if st else None), "stream_sync")
+
+
+class Event:
+    def __init__(self):
+        e = ctypes.c_void_p()
+        _check(_lib.rk_event_create(ctypes.byref(e)), "event_create")
+        self.ptr = e.value
+
+    def record(self, st=None):
+        _check(_lib.rk_event_record(ctypes.c_void_p(self.ptr), ctypes.c_void_p(st) if st else None),
+               "event_record")
+
+    def elapsed_ms(self, end):
+        ms = ctypes.c_float()
+        _check(_lib.rk_event_elapsed_ms(ctypes.c_void_p(self.ptr), ctypes.c_void_p(end.ptr),
+                                        ctypes.byref(ms)), "event_elapsed")
+        return ms.value
+
+
+def device_info():
+    name = ctypes.create_string_buffer(256)
+    cus, clk = ctypes.c_int(), ctypes.c_int()
+    _check(_lib.rk_device_info(name, 256, ctypes.byref(cus), ctypes.byref(clk)), "device_info")
+    return name.value.decode(), cus.value, clk.value
+
+
+def lib():
+    return load_library()

@@ -1,0 +1,62 @@
+// Shared definitions for the gfx950 kernels and the engine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/burn_rocket_amd.h"
+
+typedef _Float16 f16;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_ __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int uintx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int uintx2 __attribute__((ext_vector_type(2)));
+
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
+
+// s_waitcnt immediates for gfx9: vmcnt[3:0] in bits 3:0, expcnt in 6:4,
+// lgkmcnt in 11:8, vmcnt[5:4] in 15:14. A field at its maximum means "do not
+// wait on this counter".
+#define WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt((((n)&15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
+#define WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0x0f | (7 << 4) | (0 << 8) | (3 << 14))
+#define WAIT_ALL0() __builtin_amdgcn_s_waitcnt(0)
+
+// Workgroup barrier without a memory fence. The kernels wait on the exact
+// counters they need (WAIT_VMCNT / WAIT_LGKMCNT0) before it; the empty asm
+// statements keep the compiler from moving memory operations across it.
+#define BARRIER()                          \
+  do {                                     \
+    asm volatile("" ::: "memory");         \
+    __builtin_amdgcn_s_barrier();          \
+    asm volatile("" ::: "memory");         \
+  } while (0)
+
+// 64 zero bytes: the source of global→LDS copies that fall past the end of K,
+// so a ragged K tail contributes nothing. One copy per translation unit.
+static __device__ __attribute__((aligned(16))) uint8_t g_zero_chunk[64];
+
+// Asynchronous 16-byte global→LDS copy (global_load_lds_dwordx4). The LDS
+// destination of lane i is lds_base + 16·i; lds_base must be wave-uniform.
+__device__ __forceinline__ void dma16(const void *gsrc, void *lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, LDS_PTR(lds_base), 16, 0, 0);
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// Logical→physical block index so that consecutive logical tiles land on the
+// same XCD (the dispatcher assigns workgroup b to XCD b % 8). Tiles that share
+// operands then share that XCD's L2.
+__device__ __forceinline__ int xcd_swizzle(int b, int nblocks) {
+  const int nx = 8;
+  if (nblocks % nx != 0) return b;
+  return (b % nx) * (nblocks / nx) + b / nx;
+}
+
+static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+static inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }

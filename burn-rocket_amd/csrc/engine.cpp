@@ -1,0 +1,1269 @@
+// C-ABI engine: process-global device context, resident weight registry,
+// per-shape scratch and the op entry points declared in burn_rocket_amd.h.
+//
+// Mirrors the reference extension's engine (crates/burn-rocket/src/ext.rs:
+// Engine ext.rs:518-535, init ext.rs:561-580, weight kinds ext.rs:1156-1181,
+// matmul_impl ext.rs:1208-1232, attention_impl ext.rs:1669-1858) with the
+// NPU driver calls replaced by HIP kernel launches on one stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/burn_rocket_amd.h"
+#include "kernels.hpp"
+
+static inline int64_t round_up_i(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+
+namespace {
+
+thread_local std::string g_last_error;
+
+const char *status_text(int rc) {
+  switch (rc) {
+    case RK_E_SHAPE: return "unsupported shape";
+    case RK_E_TILING: return "shape not tileable";
+    case RK_E_NOMEM: return "allocation failed";
+    case RK_E_DEVICE: return "device/driver failure";
+    case RK_E_UNSUPPORTED: return "unsupported feature";
+    case RK_E_RANGE: return "value out of range";
+    case RK_E_IO: return "i/o failure";
+  }
+  return "unknown error";
+}
+
+int fail(int rc, const char *op, const std::string &detail) {
+  g_last_error = std::string(op) + " failed: " + status_text(rc) + " (rc=" + std::to_string(rc) +
+                 ")" + (detail.empty() ? "" : ": " + detail);
+  return rc;
+}
+
+int hip_fail(hipError_t e, const char *op) {
+  const int rc = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? RK_E_NOMEM
+                                                                             : RK_E_DEVICE;
+  return fail(rc, op, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, op)                         \
+  do {                                            \
+    hipError_t e_ = (expr);                       \
+    if (e_ != hipSuccess) return hip_fail(e_, op); \
+  } while (0)
+
+#define RK_TRY(expr)          \
+  do {                        \
+    int rc_ = (expr);         \
+    if (rc_ != RK_OK) return rc_; \
+  } while (0)
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+};
+
+struct Weight {
+  int kind = 0;
+  int64_t n = 0, k = 0, group = 0;
+  void *codes = nullptr;     // fp16 [N,K] or int8 [N,K]
+  float *scales = nullptr;   // I8: [N, ws_stride] per 32-block; QAT: [N]
+  int ws_stride = 0;
+  float in_scale = 0.f, out_scale = 0.f;
+  size_t bytes = 0;
+  // MoE expert stack (kind 0, moe = true)
+  bool moe = false;
+  int n_experts = 0;
+  int64_t hidden = 0, inter = 0;
+  int8_t *gu_codes = nullptr, *dn_codes = nullptr;
+  float *gu_scales = nullptr, *dn_scales = nullptr;
+  int gu_ws_stride = 0, dn_ws_stride = 0;
+};
+
+struct Engine {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int num_cus = 256;
+  std::unordered_map<uint64_t, Weight> weights;
+  uint64_t next_id = 1;
+  std::unordered_map<std::string, DevBuf> scratch;
+  double convert_s = 0, device_s = 0;
+  uint64_t calls = 0;
+};
+
+std::mutex g_mu;
+Engine *g_eng = nullptr;
+
+using Clock = std::chrono::steady_clock;
+double secs(Clock::time_point a, Clock::time_point b) {
+  return std::chrono::duration<double>(b - a).count();
+}
+
+int ensure(const char *op) {
+  if (!g_eng) return fail(RK_E_DEVICE, op, "rk_init() has not been called");
+  HIP_TRY(hipSetDevice(g_eng->device), op);
+  return RK_OK;
+}
+
+// Grow-only named device scratch.
+int scratch(const char *name, size_t bytes, void **out) {
+  DevBuf &b = g_eng->scratch[name];
+  if (b.bytes < bytes) {
+    if (b.p) {
+      HIP_TRY(hipStreamSynchronize(g_eng->stream), "scratch");
+      HIP_TRY(hipFree(b.p), "scratch");
+    }
+    b.p = nullptr;
+    b.bytes = 0;
+    const size_t want = std::max<size_t>(bytes, 256);
+    HIP_TRY(hipMalloc(&b.p, want), "scratch");
+    b.bytes = want;
+  }
+  *out = b.p;
+  return RK_OK;
+}
+
+hipStream_t pick(rk_stream s) { return s ? (hipStream_t)s : g_eng->stream; }
+
+Weight *find(uint64_t id) {
+  auto it = g_eng->weights.find(id);
+  return it == g_eng->weights.end() ? nullptr : &it->second;
+}
+
+uint64_t insert(Weight w) {
+  const uint64_t id = g_eng->next_id++;
+  g_eng->weights.emplace(id, w);
+  return id;
+}
+
+int ws_stride_for(int64_t k) { return (int)round_up_i(k / 32, 4); }
+
+}  // namespace
+
+namespace {
+
+// Upload per-block scales [n][kb] (kb = K/32 values per row) into a padded
+// [n][ws_stride] device array.
+int upload_block_scales(const std::vector<float> &blk, int64_t n, int64_t kb, float **dev,
+                        int *stride_out, const char *op) {
+  const int stride = ws_stride_for(kb * 32);
+  std::vector<float> pad((size_t)n * stride, 0.f);
+  for (int64_t r = 0; r < n; ++r)
+    std::memcpy(&pad[(size_t)r * stride], &blk[(size_t)r * kb], sizeof(float) * kb);
+  HIP_TRY(hipMalloc((void **)dev, pad.size() * sizeof(float)), op);
+  HIP_TRY(hipMemcpy(*dev, pad.data(), pad.size() * sizeof(float), hipMemcpyHostToDevice), op);
+  *stride_out = stride;
+  return RK_OK;
+}
+
+float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+  const uint32_t exp = (h >> 10) & 0x1f;
+  uint32_t man = h & 0x3ff;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else {  // subnormal: renormalise
+      int e = -1;
+      do {
+        ++e;
+        man <<= 1;
+      } while ((man & 0x400) == 0);
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3ff) << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+// Parse [n][k/32] GGUF Q8_0 blocks into codes [n][k] and scales [n][k/32].
+void parse_q8_0(const uint8_t *blocks, int64_t n, int64_t k, int8_t *codes, float *scales) {
+  const int64_t kb = k / 32;
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t b = 0; b < kb; ++b) {
+      const uint8_t *blk = blocks + (r * kb + b) * 34;
+      const uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
+      scales[r * kb + b] = f16_bits_to_f32(d);
+      std::memcpy(codes + r * k + b * 32, blk + 2, 32);
+    }
+}
+
+int pack_f16_dev(const void *src_f16_dev, int64_t n, int64_t k, uint64_t *id) {
+  Weight w;
+  w.kind = RK_WEIGHT_F16;
+  w.n = n;
+  w.k = k;
+  w.bytes = (size_t)n * k * 2;
+  HIP_TRY(hipMalloc(&w.codes, w.bytes), "rk_pack");
+  HIP_TRY(hipMemcpyAsync(w.codes, src_f16_dev, w.bytes, hipMemcpyDeviceToDevice, g_eng->stream),
+          "rk_pack");
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack");
+  *id = insert(w);
+  return RK_OK;
+}
+
+int check_f16_shape(int64_t n, int64_t k, const char *op) {
+  if (n <= 0 || k <= 0) return fail(RK_E_SHAPE, op, "empty weight");
+  if (k % 8 != 0) return fail(RK_E_SHAPE, op, "K must be a multiple of 8 (16-byte rows)");
+  if (n > INT32_MAX || k > INT32_MAX) return fail(RK_E_SHAPE, op, "dimension too large");
+  return RK_OK;
+}
+
+int check_i8_shape(int64_t n, int64_t k, int64_t group, const char *op) {
+  if (n <= 0 || k <= 0) return fail(RK_E_SHAPE, op, "empty weight");
+  if (group <= 0 || group % 32 != 0 || k % group != 0)
+    return fail(RK_E_SHAPE, op, "group must be a positive multiple of 32 dividing K");
+  return RK_OK;
+}
+
+}  // namespace
+
+// =========================================================================
+// Engine
+// =========================================================================
+extern "C" int rk_init(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_eng) return RK_OK;
+  int count = 0;
+  HIP_TRY(hipGetDeviceCount(&count), "rk_init");
+  if (device < 0 || device >= count)
+    return fail(RK_E_DEVICE, "rk_init", "no HIP device " + std::to_string(device));
+  HIP_TRY(hipSetDevice(device), "rk_init");
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device), "rk_init");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(RK_E_UNSUPPORTED, "rk_init",
+                std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
+  Engine *e = new Engine();
+  e->device = device;
+  e->num_cus = prop.multiProcessorCount;
+  hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+  if (err != hipSuccess) {
+    delete e;
+    return hip_fail(err, "rk_init");
+  }
+  g_eng = e;
+  return RK_OK;
+}
+
+extern "C" const char *rk_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int rk_is_fallback(int rc) { return rc == RK_E_TILING ? 1 : 0; }
+
+extern "C" int rk_stats(rk_stats_t *out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_stats"));
+  out->convert_s = g_eng->convert_s;
+  out->device_s = g_eng->device_s;
+  out->calls = g_eng->calls;
+  return RK_OK;
+}
+
+extern "C" int rk_stats_reset(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_stats_reset"));
+  g_eng->convert_s = g_eng->device_s = 0;
+  g_eng->calls = 0;
+  return RK_OK;
+}
+
+extern "C" int rk_mem_stats(rk_mem_stats_t *out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_mem_stats"));
+  out->weights_bytes = 0;
+  out->scratch_bytes = 0;
+  out->n_weights = g_eng->weights.size();
+  for (auto &kv : g_eng->weights) out->weights_bytes += kv.second.bytes;
+  for (auto &kv : g_eng->scratch) out->scratch_bytes += kv.second.bytes;
+  return RK_OK;
+}
+
+extern "C" int rk_trim_scratch_to(uint64_t budget) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_trim_scratch_to"));
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_trim_scratch_to");
+  // Largest buffers go first until the rest fits the budget.
+  std::vector<std::pair<size_t, std::string>> order;
+  uint64_t total = 0;
+  for (auto &kv : g_eng->scratch) {
+    order.push_back({kv.second.bytes, kv.first});
+    total += kv.second.bytes;
+  }
+  std::sort(order.rbegin(), order.rend());
+  for (auto &o : order) {
+    if (total <= budget) break;
+    DevBuf &b = g_eng->scratch[o.second];
+    HIP_TRY(hipFree(b.p), "rk_trim_scratch_to");
+    total -= b.bytes;
+    g_eng->scratch.erase(o.second);
+  }
+  return RK_OK;
+}
+
+extern "C" int rk_clear_scratch(void) { return rk_trim_scratch_to(0); }
+
+// =========================================================================
+// Weights
+// =========================================================================
+extern "C" int rk_pack(const float *w, int64_t n, int64_t k, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack"));
+  RK_TRY(check_f16_shape(n, k, "rk_pack"));
+  void *x32, *x16;
+  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch("pack_f16", (size_t)n * k * 2, &x16));
+  HIP_TRY(hipMemcpyAsync(x32, w, (size_t)n * k * 4, hipMemcpyHostToDevice, g_eng->stream), "rk_pack");
+  HIP_TRY(rk_launch_f32_to_f16((const float *)x32, x16, n * k, g_eng->stream), "rk_pack");
+  return pack_f16_dev(x16, n, k, id);
+}
+
+extern "C" int rk_pack_f16(const uint16_t *w, int64_t n, int64_t k, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_f16"));
+  RK_TRY(check_f16_shape(n, k, "rk_pack_f16"));
+  void *x16;
+  RK_TRY(scratch("pack_f16", (size_t)n * k * 2, &x16));
+  HIP_TRY(hipMemcpyAsync(x16, w, (size_t)n * k * 2, hipMemcpyHostToDevice, g_eng->stream),
+          "rk_pack_f16");
+  return pack_f16_dev(x16, n, k, id);
+}
+
+extern "C" int rk_pack_seg(const float *const *parts, const int64_t *ns, int nparts, int64_t k,
+                           rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_seg"));
+  if (nparts <= 0) return fail(RK_E_SHAPE, "rk_pack_seg", "no parts");
+  int64_t n = 0;
+  for (int i = 0; i < nparts; ++i) {
+    if (ns[i] <= 0) return fail(RK_E_SHAPE, "rk_pack_seg", "empty part");
+    n += ns[i];
+  }
+  RK_TRY(check_f16_shape(n, k, "rk_pack_seg"));
+  void *x32, *x16;
+  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch("pack_f16", (size_t)n * k * 2, &x16));
+  int64_t off = 0;
+  for (int i = 0; i < nparts; ++i) {
+    HIP_TRY(hipMemcpyAsync((char *)x32 + off * k * 4, parts[i], (size_t)ns[i] * k * 4,
+                           hipMemcpyHostToDevice, g_eng->stream),
+            "rk_pack_seg");
+    off += ns[i];
+  }
+  HIP_TRY(rk_launch_f32_to_f16((const float *)x32, x16, n * k, g_eng->stream), "rk_pack_seg");
+  return pack_f16_dev(x16, n, k, id);
+}
+
+namespace {
+int pack_i8_host(const int8_t *codes, const std::vector<float> &block_scales, int64_t n,
+                 int64_t k, int64_t group, rk_weight_id *id, const char *op) {
+  Weight w;
+  w.kind = RK_WEIGHT_I8;
+  w.n = n;
+  w.k = k;
+  w.group = group;
+  HIP_TRY(hipMalloc(&w.codes, (size_t)n * k), op);
+  HIP_TRY(hipMemcpy(w.codes, codes, (size_t)n * k, hipMemcpyHostToDevice), op);
+  RK_TRY(upload_block_scales(block_scales, n, k / 32, &w.scales, &w.ws_stride, op));
+  w.bytes = (size_t)n * k + (size_t)n * w.ws_stride * 4;
+  *id = insert(w);
+  return RK_OK;
+}
+
+std::vector<float> expand_group_scales(const float *scales, int64_t n, int64_t k, int64_t group) {
+  const int64_t kb = k / 32, ng = k / group, gb = group / 32;
+  std::vector<float> blk((size_t)n * kb);
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t b = 0; b < kb; ++b) blk[r * kb + b] = scales[r * ng + b / gb];
+  return blk;
+}
+}  // namespace
+
+extern "C" int rk_pack_i8(const float *w, int64_t n, int64_t k, int64_t group, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_i8"));
+  RK_TRY(check_i8_shape(n, k, group, "rk_pack_i8"));
+  // Quantize on the device with the activation quantizer (same formula as
+  // quantize_i8_weight, ext.rs:1001-1012), then keep codes and scales.
+  void *x32, *q, *s;
+  const int64_t ng = k / group;
+  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch("pack_q", (size_t)n * k, &q));
+  RK_TRY(scratch("pack_s", (size_t)n * ng * 4, &s));
+  HIP_TRY(hipMemcpyAsync(x32, w, (size_t)n * k * 4, hipMemcpyHostToDevice, g_eng->stream),
+          "rk_pack_i8");
+  HIP_TRY(rk_launch_quantize_rows((const float *)x32, n, k, group, (int8_t *)q, (float *)s,
+                                  g_eng->stream),
+          "rk_pack_i8");
+  std::vector<int8_t> codes((size_t)n * k);
+  std::vector<float> scales((size_t)n * ng);
+  HIP_TRY(hipMemcpyAsync(codes.data(), q, codes.size(), hipMemcpyDeviceToHost, g_eng->stream),
+          "rk_pack_i8");
+  HIP_TRY(hipMemcpyAsync(scales.data(), s, scales.size() * 4, hipMemcpyDeviceToHost,
+                         g_eng->stream),
+          "rk_pack_i8");
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack_i8");
+  return pack_i8_host(codes.data(), expand_group_scales(scales.data(), n, k, group), n, k, group,
+                      id, "rk_pack_i8");
+}
+
+extern "C" int rk_pack_i8_codes(const int8_t *codes, const float *scales, int64_t n, int64_t k,
+                                int64_t group, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_i8_codes"));
+  RK_TRY(check_i8_shape(n, k, group, "rk_pack_i8_codes"));
+  return pack_i8_host(codes, expand_group_scales(scales, n, k, group), n, k, group, id,
+                      "rk_pack_i8_codes");
+}
+
+extern "C" int rk_rewrite_i8(rk_weight_id id, const int8_t *codes, const float *scales) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_rewrite_i8"));
+  Weight *w = find(id);
+  if (!w || w->kind != RK_WEIGHT_I8)
+    return fail(RK_E_RANGE, "rk_rewrite_i8", "id is not a resident int8 weight");
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_rewrite_i8");
+  HIP_TRY(hipMemcpy(w->codes, codes, (size_t)w->n * w->k, hipMemcpyHostToDevice), "rk_rewrite_i8");
+  std::vector<float> blk = expand_group_scales(scales, w->n, w->k, w->group);
+  const int64_t kb = w->k / 32;
+  std::vector<float> pad((size_t)w->n * w->ws_stride, 0.f);
+  for (int64_t r = 0; r < w->n; ++r)
+    std::memcpy(&pad[(size_t)r * w->ws_stride], &blk[(size_t)r * kb], sizeof(float) * kb);
+  HIP_TRY(hipMemcpy(w->scales, pad.data(), pad.size() * 4, hipMemcpyHostToDevice), "rk_rewrite_i8");
+  return RK_OK;
+}
+
+extern "C" int rk_pack_q8_0(const uint8_t *blocks, int64_t n, int64_t k, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_q8_0"));
+  RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0"));
+  std::vector<int8_t> codes((size_t)n * k);
+  std::vector<float> scales((size_t)n * (k / 32));
+  parse_q8_0(blocks, n, k, codes.data(), scales.data());
+  return pack_i8_host(codes.data(), scales, n, k, 32, id, "rk_pack_q8_0");
+}
+
+extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_q8_0_f32"));
+  RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_f32"));
+  Weight wt;
+  wt.kind = RK_WEIGHT_I8;
+  wt.n = n;
+  wt.k = k;
+  wt.group = 32;
+  wt.ws_stride = ws_stride_for(k);
+  void *x32;
+  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
+  HIP_TRY(hipMalloc(&wt.codes, (size_t)n * k), "rk_pack_q8_0_f32");
+  HIP_TRY(hipMalloc((void **)&wt.scales, (size_t)n * wt.ws_stride * 4), "rk_pack_q8_0_f32");
+  HIP_TRY(hipMemsetAsync(wt.scales, 0, (size_t)n * wt.ws_stride * 4, g_eng->stream), "rk_pack_q8_0_f32");
+  HIP_TRY(hipMemcpyAsync(x32, w, (size_t)n * k * 4, hipMemcpyHostToDevice, g_eng->stream),
+          "rk_pack_q8_0_f32");
+  HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, n, k, 32, 0, (int8_t *)wt.codes, wt.scales,
+                                  wt.ws_stride, g_eng->stream),
+          "rk_pack_q8_0_f32");
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack_q8_0_f32");
+  wt.bytes = (size_t)n * k + (size_t)n * wt.ws_stride * 4;
+  *id = insert(wt);
+  return RK_OK;
+}
+
+extern "C" int rk_pack_qat(const int8_t *codes, const float *w_scale, int64_t n, int64_t k,
+                           float in_scale, float out_scale, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_qat"));
+  if (n <= 0 || k <= 0 || k % 32 != 0)
+    return fail(RK_E_SHAPE, "rk_pack_qat", "the int8 path needs K % 32 == 0");
+  if (!(in_scale >= 0.f)) return fail(RK_E_RANGE, "rk_pack_qat", "input scale must not be negative");
+  Weight w;
+  w.kind = RK_WEIGHT_QAT;
+  w.n = n;
+  w.k = k;
+  w.group = k;
+  w.in_scale = in_scale;
+  w.out_scale = out_scale;
+  HIP_TRY(hipMalloc(&w.codes, (size_t)n * k), "rk_pack_qat");
+  HIP_TRY(hipMemcpy(w.codes, codes, (size_t)n * k, hipMemcpyHostToDevice), "rk_pack_qat");
+  HIP_TRY(hipMalloc((void **)&w.scales, (size_t)n * 4), "rk_pack_qat");
+  HIP_TRY(hipMemcpy(w.scales, w_scale, (size_t)n * 4, hipMemcpyHostToDevice), "rk_pack_qat");
+  w.bytes = (size_t)n * k + (size_t)n * 4;
+  *id = insert(w);
+  return RK_OK;
+}
+
+extern "C" int rk_weight_info(rk_weight_id id, int *kind, int64_t *n, int64_t *k,
+                              int64_t *group) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_weight_info"));
+  Weight *w = find(id);
+  if (!w) return fail(RK_E_RANGE, "rk_weight_info", "weight id is not packed");
+  *kind = w->moe ? 0 : w->kind;
+  *n = w->n;
+  *k = w->k;
+  *group = w->group;
+  return RK_OK;
+}
+
+// =========================================================================
+// Matmul
+// =========================================================================
+namespace {
+int launch_i8(const Weight &w, const int8_t *a, const float *as, int as_stride, int a_gb,
+              int mode, bool out_f16, int64_t m, void *c, hipStream_t st, const char *op) {
+  I8GemmArgs g;
+  g.A = a;
+  g.AS = as;
+  g.as_stride = as_stride;
+  g.a_gb = a_gb;
+  g.W = (const int8_t *)w.codes;
+  g.WS = w.scales;
+  g.ws_stride = w.ws_stride;
+  g.gb = (int)(w.group / 32);
+  g.C = c;
+  g.M = (int)m;
+  g.N = (int)w.n;
+  g.K = (int)w.k;
+  g.mode = mode;
+  g.out_f16 = out_f16;
+  g.num_cus = g_eng->num_cus;
+  HIP_TRY(rk_launch_gemm_i8(g, st), op);
+  return RK_OK;
+}
+
+int check_m(int64_t m, int64_t k, const Weight *w, const char *op) {
+  if (!w) return fail(RK_E_RANGE, op, "weight id is not packed");
+  if (m <= 0) return fail(RK_E_SHAPE, op, "M must be positive");
+  if (m > INT32_MAX) return fail(RK_E_SHAPE, op, "M too large");
+  if (k != w->k)
+    return fail(RK_E_SHAPE, op, "activation K " + std::to_string(k) + " != weight K " +
+                                    std::to_string(w->k));
+  return RK_OK;
+}
+}  // namespace
+
+extern "C" int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, float *y) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_matmul"));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, "rk_matmul"));
+  if (w->moe) return fail(RK_E_UNSUPPORTED, "rk_matmul", "an expert stack is not a matmul weight");
+  const auto t0 = Clock::now();
+  hipStream_t st = g_eng->stream;
+  const int64_t n = w->n;
+  void *x32, *y32;
+  RK_TRY(scratch("mm_x32", (size_t)m * k * 4, &x32));
+  RK_TRY(scratch("mm_y32", (size_t)m * n * 4, &y32));
+  HIP_TRY(hipMemcpyAsync(x32, x, (size_t)m * k * 4, hipMemcpyHostToDevice, st), "rk_matmul");
+  if (w->kind == RK_WEIGHT_F16) {
+    void *a16, *c16;
+    RK_TRY(scratch("mm_a16", (size_t)m * k * 2, &a16));
+    RK_TRY(scratch("mm_c16", (size_t)m * n * 2, &c16));
+    HIP_TRY(rk_launch_f32_to_f16((const float *)x32, a16, m * k, st), "rk_matmul");
+    HIP_TRY(rk_launch_gemm_f16(a16, w->codes, c16, (int)m, (int)n, (int)k, g_eng->num_cus, st),
+            "rk_matmul_fp16");
+    HIP_TRY(rk_launch_f16_to_f32(c16, (float *)y32, m * n, st), "rk_matmul");
+  } else if (w->kind == RK_WEIGHT_I8) {
+    void *q, *s;
+    const int64_t ng = k / w->group;
+    RK_TRY(scratch("mm_q", (size_t)m * k, &q));
+    RK_TRY(scratch("mm_s", (size_t)m * ng * 4, &s));
+    HIP_TRY(rk_launch_quantize_rows((const float *)x32, m, k, w->group, (int8_t *)q, (float *)s, st),
+            "rk_matmul");
+    RK_TRY(launch_i8(*w, (const int8_t *)q, (const float *)s, (int)ng, (int)(w->group / 32),
+                     I8_PER_GROUP, false, m, y32, st, "rk_matmul_int8_gw"));
+  } else {  // QAT
+    void *q, *rs, *acc;
+    RK_TRY(scratch("mm_q", (size_t)m * k, &q));
+    RK_TRY(scratch("mm_rs", (size_t)m * 4, &rs));
+    RK_TRY(scratch("mm_acc", (size_t)m * n * 4, &acc));
+    HIP_TRY(rk_launch_quantize_static((const float *)x32, m, k, w->in_scale, (int8_t *)q,
+                                      (float *)rs, st),
+            "rk_matmul");
+    RK_TRY(launch_i8(*w, (const int8_t *)q, nullptr, 0, 1, I8_RAW, false, m, acc, st,
+                     "rk_matmul_int8_qat"));
+    HIP_TRY(rk_launch_qat_epilogue((const int32_t *)acc, (const float *)rs, w->scales, m, n,
+                                   w->out_scale, (float *)y32, st),
+            "rk_matmul");
+  }
+  HIP_TRY(hipMemcpyAsync(y, y32, (size_t)m * n * 4, hipMemcpyDeviceToHost, st), "rk_matmul");
+  HIP_TRY(hipStreamSynchronize(st), "rk_matmul");
+  g_eng->device_s += secs(t0, Clock::now());
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_matmul_f16_dev(rk_weight_id id, const void *a, int64_t m, int64_t k, void *c,
+                                 rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_matmul_f16_dev"));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, "rk_matmul_f16_dev"));
+  if (w->kind != RK_WEIGHT_F16 || w->moe)
+    return fail(RK_E_UNSUPPORTED, "rk_matmul_f16_dev", "weight is not fp16");
+  HIP_TRY(rk_launch_gemm_f16(a, w->codes, c, (int)m, (int)w->n, (int)k, g_eng->num_cus,
+                             pick(stream)),
+          "rk_matmul_f16_dev");
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_quantize_rows_dev(const float *x, int64_t m, int64_t k, int64_t group, int8_t *q,
+                                    float *scale, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_quantize_rows_dev"));
+  if (m < 0 || k <= 0 || group <= 0 || k % group != 0)
+    return fail(RK_E_SHAPE, "rk_quantize_rows_dev", "group must divide K");
+  if (k / group > 1024) return fail(RK_E_SHAPE, "rk_quantize_rows_dev", "more than 1024 groups per row");
+  HIP_TRY(rk_launch_quantize_rows(x, m, k, group, q, scale, pick(stream)), "rk_quantize_rows_dev");
+  return RK_OK;
+}
+
+namespace {
+int w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale, int64_t a_group, int64_t m,
+             int64_t k, void *c, bool out_f16, rk_stream stream, const char *op) {
+  RK_TRY(ensure(op));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, op));
+  if (w->kind != RK_WEIGHT_I8 || w->moe) return fail(RK_E_UNSUPPORTED, op, "weight is not group-wise int8");
+  int mode;
+  if (a_group == k)
+    mode = I8_PER_TOKEN;
+  else if (a_group == w->group)
+    mode = I8_PER_GROUP;
+  else
+    return fail(RK_E_SHAPE, op, "activation group must be K (per token) or the weight group");
+  RK_TRY(launch_i8(*w, a, a_scale, (int)(k / a_group), (int)(a_group / 32), mode, out_f16, m, c,
+                   pick(stream), op));
+  g_eng->calls++;
+  return RK_OK;
+}
+}  // namespace
+
+extern "C" int rk_matmul_w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale,
+                                  int64_t a_group, int64_t m, int64_t k, float *c,
+                                  rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return w8a8_dev(id, a, a_scale, a_group, m, k, c, false, stream, "rk_matmul_w8a8_dev");
+}
+
+extern "C" int rk_matmul_w8a8_f16out_dev(rk_weight_id id, const int8_t *a, const float *a_scale,
+                                         int64_t a_group, int64_t m, int64_t k, void *c,
+                                         rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return w8a8_dev(id, a, a_scale, a_group, m, k, c, true, stream, "rk_matmul_w8a8_f16out_dev");
+}
+
+extern "C" int rk_matmul_i8_raw_dev(rk_weight_id id, const int8_t *a, int64_t m, int64_t k,
+                                    int32_t *c, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_matmul_i8_raw_dev"));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, "rk_matmul_i8_raw_dev"));
+  if ((w->kind != RK_WEIGHT_I8 && w->kind != RK_WEIGHT_QAT) || w->moe)
+    return fail(RK_E_UNSUPPORTED, "rk_matmul_i8_raw_dev", "weight is not int8");
+  RK_TRY(launch_i8(*w, a, nullptr, 0, 1, I8_RAW, false, m, c, pick(stream), "rk_matmul_i8_raw_dev"));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_matmul_i8_partials_dev(rk_weight_id id, const int8_t *a, int64_t m, int64_t k,
+                                         int32_t *p, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_matmul_i8_partials_dev"));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, "rk_matmul_i8_partials_dev"));
+  if ((w->kind != RK_WEIGHT_I8 && w->kind != RK_WEIGHT_QAT) || w->moe)
+    return fail(RK_E_UNSUPPORTED, "rk_matmul_i8_partials_dev", "weight is not int8");
+  RK_TRY(launch_i8(*w, a, nullptr, 0, 1, I8_PARTIALS, false, m, p, pick(stream),
+                   "rk_matmul_i8_partials_dev"));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+// =========================================================================
+// Attention
+// =========================================================================
+hipError_t rk_launch_v_transpose_strided(const void *v, int64_t tok_stride, int64_t head_stride,
+                                         int64_t d_stride, int n_kv, int n_kv_pad,
+                                         int n_kv_heads, int head_dim, int dv_pad, void *vt,
+                                         hipStream_t st);
+namespace {
+int attn_check(int64_t n_q, int64_t n_kv, int n_head, int n_kv_heads, int head_dim, int *mode,
+               int64_t window, const char *op) {
+  if (n_q <= 0 || n_kv <= 0) return fail(RK_E_SHAPE, op, "empty query or key axis");
+  if (n_q > INT32_MAX || n_kv > INT32_MAX) return fail(RK_E_SHAPE, op, "sequence too long");
+  if (n_head <= 0 || n_kv_heads <= 0 || n_head % n_kv_heads != 0)
+    return fail(RK_E_SHAPE, op, "n_head must be a positive multiple of n_kv_heads");
+  if (n_head / n_kv_heads > 128) return fail(RK_E_SHAPE, op, "GQA group above 128");
+  switch (head_dim) {
+    case 64: case 72: case 80: case 96: case 112: case 128: break;
+    default:
+      return fail(RK_E_UNSUPPORTED, op, "head_dim " + std::to_string(head_dim) +
+                                            " (supported: 64, 72, 80, 96, 112, 128)");
+  }
+  if (*mode < RK_MASK_NONE || *mode > RK_MASK_CAUSAL_WINDOW)
+    return fail(RK_E_SHAPE, op, "unknown mask mode");
+  // window < 0 disables the window (ext.rs:99-126).
+  if (*mode == RK_MASK_WINDOW && window < 0) *mode = RK_MASK_NONE;
+  if (*mode == RK_MASK_CAUSAL_WINDOW && window < 0) *mode = RK_MASK_CAUSAL;
+  return RK_OK;
+}
+
+int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_q, int64_t n_kv,
+             int64_t n_kv_pad, int n_head, int n_kv_heads, int head_dim, float scale, float softcap,
+             int mode, int64_t window, int64_t q0, int64_t k0, bool head_major, hipStream_t st,
+             const char *op) {
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.vt = vt;
+  a.out = out;
+  if (head_major) {
+    a.q_tok_stride = head_dim;
+    a.q_head_stride = n_q * head_dim;
+    a.k_tok_stride = head_dim;
+    a.k_head_stride = n_kv * head_dim;
+    a.o_tok_stride = head_dim;
+    a.o_head_stride = n_q * head_dim;
+  } else {
+    a.q_tok_stride = (int64_t)n_head * head_dim;
+    a.q_head_stride = head_dim;
+    a.k_tok_stride = (int64_t)n_kv_heads * head_dim;
+    a.k_head_stride = head_dim;
+    a.o_tok_stride = (int64_t)n_head * head_dim;
+    a.o_head_stride = head_dim;
+  }
+  a.n_q = (int)n_q;
+  a.n_kv = (int)n_kv;
+  a.n_kv_pad = (int)n_kv_pad;
+  a.n_head = n_head;
+  a.n_kv_heads = n_kv_heads;
+  a.head_dim = head_dim;
+  a.scale = scale;
+  a.softcap = softcap;
+  a.mask_mode = mode;
+  a.window = window;
+  a.q0 = q0;
+  a.k0 = k0;
+  a.num_cus = g_eng->num_cus;
+  HIP_TRY(rk_launch_attention(a, st), op);
+  return RK_OK;
+}
+
+int attn_dev_impl(const void *q, const void *k, const void *v, int64_t n_q, int64_t n_kv, int n_head,
+                  int n_kv_heads, int head_dim, float scale, float softcap, int mode,
+                  int64_t window, int64_t q0, int64_t k0, void *out, hipStream_t st,
+                  const char *op) {
+  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, op));
+  const int dvp = rk_attn_dv_pad(head_dim);
+  const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
+  void *vt;
+  RK_TRY(scratch("attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
+  HIP_TRY(rk_launch_v_transpose(v, (int64_t)n_kv_heads * head_dim, head_dim, (int)n_kv,
+                                (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
+          op);
+  return attn_run(q, k, vt, out, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale, softcap,
+                  mode, window, q0, k0, false, st, op);
+}
+}  // namespace
+
+extern "C" int rk_attention_dev(const void *q, const void *k, const void *v, int64_t n_q,
+                                int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
+                                float scale, float softcap, int mask_mode, int64_t window,
+                                int64_t q0, int64_t k0, void *out, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_attention_dev"));
+  RK_TRY(attn_dev_impl(q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap, mask_mode,
+                       window, q0, k0, out, pick(stream), "rk_attention_dev"));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_attention(const float *q, const float *k, const float *v, int64_t n_q,
+                            int64_t n_kv, int n_head, int n_kv_heads, int head_dim, float scale,
+                            float softcap, int mask_mode, int64_t window, int64_t q0, int64_t k0,
+                            float *out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_attention"));
+  int mode = mask_mode;
+  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, "rk_attention"));
+  const auto t0 = Clock::now();
+  hipStream_t st = g_eng->stream;
+  const size_t nq_el = (size_t)n_q * n_head * head_dim;
+  const size_t nk_el = (size_t)n_kv * n_kv_heads * head_dim;
+  void *f32buf, *q16, *k16, *v16, *o16;
+  RK_TRY(scratch("at_f32", std::max(nq_el, nk_el) * 4, &f32buf));
+  RK_TRY(scratch("at_q16", nq_el * 2, &q16));
+  RK_TRY(scratch("at_k16", nk_el * 2, &k16));
+  RK_TRY(scratch("at_v16", nk_el * 2, &v16));
+  RK_TRY(scratch("at_o16", nq_el * 2, &o16));
+  const float *srcs[3] = {q, k, v};
+  void *dsts[3] = {q16, k16, v16};
+  const size_t els[3] = {nq_el, nk_el, nk_el};
+  for (int i = 0; i < 3; ++i) {
+    HIP_TRY(hipMemcpyAsync(f32buf, srcs[i], els[i] * 4, hipMemcpyHostToDevice, st), "rk_attention");
+    HIP_TRY(rk_launch_f32_to_f16((const float *)f32buf, dsts[i], (int64_t)els[i], st), "rk_attention");
+  }
+  RK_TRY(attn_dev_impl(q16, k16, v16, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap, mode,
+                       window, q0, k0, o16, st, "rk_attention"));
+  HIP_TRY(rk_launch_f16_to_f32(o16, (float *)f32buf, (int64_t)nq_el, st), "rk_attention");
+  HIP_TRY(hipMemcpyAsync(out, f32buf, nq_el * 4, hipMemcpyDeviceToHost, st), "rk_attention");
+  HIP_TRY(hipStreamSynchronize(st), "rk_attention");
+  g_eng->device_s += secs(t0, Clock::now());
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv, int n_head,
+                                 int n_kv_heads, float scale, float softcap, int mask_mode,
+                                 int64_t window, int64_t q0, int64_t k0, const uint16_t *q,
+                                 const uint16_t *k, const uint16_t *v, uint16_t *out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_flash_attn_f16"));
+  if (dv != head_dim) return fail(RK_E_UNSUPPORTED, "rk_flash_attn_f16", "dv must equal head_dim");
+  int mode = mask_mode;
+  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, "rk_flash_attn_f16"));
+  const auto t0 = Clock::now();
+  hipStream_t st = g_eng->stream;
+  const size_t nq_el = (size_t)n_q * n_head * head_dim;
+  const size_t nk_el = (size_t)n_kv * n_kv_heads * head_dim;
+  const int dvp = rk_attn_dv_pad(head_dim);
+  const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
+  void *q16, *k16, *v16, *o16, *vt;
+  RK_TRY(scratch("at_q16", nq_el * 2, &q16));
+  RK_TRY(scratch("at_k16", nk_el * 2, &k16));
+  RK_TRY(scratch("at_v16", nk_el * 2, &v16));
+  RK_TRY(scratch("at_o16", nq_el * 2, &o16));
+  RK_TRY(scratch("attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
+  HIP_TRY(hipMemcpyAsync(q16, q, nq_el * 2, hipMemcpyHostToDevice, st), "rk_flash_attn_f16");
+  HIP_TRY(hipMemcpyAsync(k16, k, nk_el * 2, hipMemcpyHostToDevice, st), "rk_flash_attn_f16");
+  HIP_TRY(hipMemcpyAsync(v16, v, nk_el * 2, hipMemcpyHostToDevice, st), "rk_flash_attn_f16");
+  // v is [KV][dv][n_kv]: element (key, head, d) at head·dv·n_kv + d·n_kv + key.
+  HIP_TRY(rk_launch_v_transpose_strided(v16, 1, (int64_t)head_dim * n_kv, n_kv, (int)n_kv,
+                                        (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
+          "rk_flash_attn_f16");
+  RK_TRY(attn_run(q16, k16, vt, o16, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale,
+                  softcap, mode, window, q0, k0, true, st, "rk_flash_attn_f16"));
+  HIP_TRY(hipMemcpyAsync(out, o16, nq_el * 2, hipMemcpyDeviceToHost, st), "rk_flash_attn_f16");
+  HIP_TRY(hipStreamSynchronize(st), "rk_flash_attn_f16");
+  g_eng->device_s += secs(t0, Clock::now());
+  g_eng->calls++;
+  return RK_OK;
+}
+
+// =========================================================================
+// MoE
+// =========================================================================
+extern "C" int rk_moe_route(const float *logits, int64_t s, int n_experts, int top_k,
+                            int norm_topk, uint32_t *ids, float *wts) {
+  if (s < 0 || n_experts <= 0 || top_k <= 0 || top_k > n_experts)
+    return fail(RK_E_SHAPE, "rk_moe_route", "need 0 < top_k <= n_experts");
+  std::vector<float> p(n_experts);
+  std::vector<int> order(n_experts);
+  for (int64_t t = 0; t < s; ++t) {
+    const float *l = logits + t * n_experts;
+    // softmax_row (src/clef/math.rs:138-148): max, exp(v - max), sum, divide.
+    float mx = -INFINITY;
+    for (int e = 0; e < n_experts; ++e) mx = std::max(mx, l[e]);
+    float sum = 0.f;
+    for (int e = 0; e < n_experts; ++e) {
+      p[e] = std::exp(l[e] - mx);
+      sum += p[e];
+    }
+    for (int e = 0; e < n_experts; ++e) p[e] /= sum;
+    for (int e = 0; e < n_experts; ++e) order[e] = e;
+    // Descending probability, ties to the lower id (model.rs:475).
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+      if (p[a] != p[b]) return p[a] > p[b];
+      return a < b;
+    });
+    float sel = 0.f;
+    for (int j = 0; j < top_k; ++j) sel += p[order[j]];
+    for (int j = 0; j < top_k; ++j) {
+      ids[t * top_k + j] = (uint32_t)order[j];
+      wts[t * top_k + j] = norm_topk ? p[order[j]] / sel : p[order[j]];
+    }
+  }
+  return RK_OK;
+}
+
+extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                                int n_experts, int64_t hidden, int64_t inter, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_moe_q8_0"));
+  if (n_experts <= 0 || hidden <= 0 || inter <= 0 || hidden % 32 || inter % 32)
+    return fail(RK_E_SHAPE, "rk_pack_moe_q8_0", "hidden and inter must be multiples of 32");
+  const int64_t H = hidden, I = inter, E = n_experts;
+  Weight w;
+  w.moe = true;
+  w.n_experts = n_experts;
+  w.hidden = H;
+  w.inter = I;
+  w.n = H;
+  w.k = H;
+  w.group = 32;
+  w.gu_ws_stride = ws_stride_for(H);
+  w.dn_ws_stride = ws_stride_for(I);
+  const size_t gu_codes = (size_t)E * 2 * I * H, dn_codes = (size_t)E * H * I;
+  const size_t gu_sc = (size_t)E * 2 * I * w.gu_ws_stride, dn_sc = (size_t)E * H * w.dn_ws_stride;
+  HIP_TRY(hipMalloc((void **)&w.gu_codes, gu_codes), "rk_pack_moe_q8_0");
+  HIP_TRY(hipMalloc((void **)&w.dn_codes, dn_codes), "rk_pack_moe_q8_0");
+  HIP_TRY(hipMalloc((void **)&w.gu_scales, gu_sc * 4), "rk_pack_moe_q8_0");
+  HIP_TRY(hipMalloc((void **)&w.dn_scales, dn_sc * 4), "rk_pack_moe_q8_0");
+  w.bytes = gu_codes + dn_codes + (gu_sc + dn_sc) * 4;
+  // Per expert: parse gate/up/down, interleave gate|up per 32-row slice.
+  std::vector<int8_t> gc(I * H), uc(I * H), dc(H * I), guc(2 * I * H);
+  std::vector<float> gs(I * (H / 32)), us(I * (H / 32)), ds(H * (I / 32));
+  std::vector<float> gus((size_t)2 * I * w.gu_ws_stride), dss((size_t)H * w.dn_ws_stride);
+  const size_t gblk = (size_t)I * (H / 32) * 34, dblk = (size_t)H * (I / 32) * 34;
+  for (int64_t e = 0; e < E; ++e) {
+    parse_q8_0(gate + e * gblk, I, H, gc.data(), gs.data());
+    parse_q8_0(up + e * gblk, I, H, uc.data(), us.data());
+    parse_q8_0(down + e * dblk, H, I, dc.data(), ds.data());
+    std::fill(gus.begin(), gus.end(), 0.f);
+    std::fill(dss.begin(), dss.end(), 0.f);
+    for (int64_t r = 0; r < I; ++r) {
+      const int64_t t = r / 32, j = r % 32;
+      const int64_t rg = 64 * t + j, ru = 64 * t + 32 + j;
+      std::memcpy(&guc[rg * H], &gc[r * H], H);
+      std::memcpy(&guc[ru * H], &uc[r * H], H);
+      std::memcpy(&gus[rg * w.gu_ws_stride], &gs[r * (H / 32)], 4 * (H / 32));
+      std::memcpy(&gus[ru * w.gu_ws_stride], &us[r * (H / 32)], 4 * (H / 32));
+    }
+    for (int64_t r = 0; r < H; ++r)
+      std::memcpy(&dss[r * w.dn_ws_stride], &ds[r * (I / 32)], 4 * (I / 32));
+    HIP_TRY(hipMemcpy(w.gu_codes + e * 2 * I * H, guc.data(), guc.size(), hipMemcpyHostToDevice),
+            "rk_pack_moe_q8_0");
+    HIP_TRY(hipMemcpy(w.dn_codes + e * H * I, dc.data(), dc.size(), hipMemcpyHostToDevice),
+            "rk_pack_moe_q8_0");
+    HIP_TRY(hipMemcpy(w.gu_scales + e * 2 * I * w.gu_ws_stride, gus.data(), gus.size() * 4,
+                      hipMemcpyHostToDevice),
+            "rk_pack_moe_q8_0");
+    HIP_TRY(hipMemcpy(w.dn_scales + e * H * w.dn_ws_stride, dss.data(), dss.size() * 4,
+                      hipMemcpyHostToDevice),
+            "rk_pack_moe_q8_0");
+  }
+  *id = insert(w);
+  return RK_OK;
+}
+
+namespace {
+int moe_alloc(Weight &w, int n_experts, int64_t H, int64_t I, const char *op) {
+  w.moe = true;
+  w.n_experts = n_experts;
+  w.hidden = H;
+  w.inter = I;
+  w.n = H;
+  w.k = H;
+  w.group = 32;
+  w.gu_ws_stride = ws_stride_for(H);
+  w.dn_ws_stride = ws_stride_for(I);
+  const int64_t E = n_experts;
+  const size_t gu_codes = (size_t)E * 2 * I * H, dn_codes = (size_t)E * H * I;
+  const size_t gu_sc = (size_t)E * 2 * I * w.gu_ws_stride, dn_sc = (size_t)E * H * w.dn_ws_stride;
+  HIP_TRY(hipMalloc((void **)&w.gu_codes, gu_codes), op);
+  HIP_TRY(hipMalloc((void **)&w.dn_codes, dn_codes), op);
+  HIP_TRY(hipMalloc((void **)&w.gu_scales, gu_sc * 4), op);
+  HIP_TRY(hipMalloc((void **)&w.dn_scales, dn_sc * 4), op);
+  HIP_TRY(hipMemset(w.gu_scales, 0, gu_sc * 4), op);
+  HIP_TRY(hipMemset(w.dn_scales, 0, dn_sc * 4), op);
+  w.bytes = gu_codes + dn_codes + (gu_sc + dn_sc) * 4;
+  return RK_OK;
+}
+}  // namespace
+
+extern "C" int rk_pack_moe_f32(const float *gate, const float *up, const float *down, int n_experts,
+                               int64_t hidden, int64_t inter, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_moe_f32"));
+  if (n_experts <= 0 || hidden <= 0 || inter <= 0 || hidden % 32 || inter % 32)
+    return fail(RK_E_SHAPE, "rk_pack_moe_f32", "hidden and inter must be multiples of 32");
+  const int64_t H = hidden, I = inter, E = n_experts;
+  Weight w;
+  RK_TRY(moe_alloc(w, n_experts, H, I, "rk_pack_moe_f32"));
+  void *x32;
+  RK_TRY(scratch("pack_f32", (size_t)I * H * 4, &x32));
+  hipStream_t st = g_eng->stream;
+  for (int64_t e = 0; e < E; ++e) {
+    int8_t *guc = w.gu_codes + e * 2 * I * H;
+    float *gus = w.gu_scales + e * 2 * I * w.gu_ws_stride;
+    const float *src[3] = {gate + e * I * H, up + e * I * H, down + e * H * I};
+    for (int part = 0; part < 3; ++part) {
+      HIP_TRY(hipMemcpyAsync(x32, src[part], (size_t)I * H * 4, hipMemcpyHostToDevice, st),
+              "rk_pack_moe_f32");
+      if (part < 2)
+        HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, I, H, 64, 32 * part, guc, gus,
+                                        w.gu_ws_stride, st),
+                "rk_pack_moe_f32");
+      else
+        HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, H, I, 32, 0, w.dn_codes + e * H * I,
+                                        w.dn_scales + e * H * w.dn_ws_stride, w.dn_ws_stride, st),
+                "rk_pack_moe_f32");
+    }
+  }
+  HIP_TRY(hipStreamSynchronize(st), "rk_pack_moe_f32");
+  *id = insert(w);
+  return RK_OK;
+}
+
+namespace {
+// Device-resident routing lists of one MoE call.
+struct MoePlan {
+  int64_t s = 0;
+  int top_k = 0;
+  int64_t rows = 0;
+  int n_tiles = 0;
+  int32_t *tok = nullptr;     // [rows] token of each bucket row
+  float *roww = nullptr;      // [rows] router weight of each bucket row
+  int32_t *slot = nullptr;    // [s, top_k] bucket rows of a token, ascending expert id
+  MoeTile *tiles = nullptr;   // [n_tiles]
+  uint64_t weight = 0;        // expert stack the plan was made for
+};
+
+void plan_free(MoePlan *p) {
+  if (!p) return;
+  hipFree(p->tok);
+  hipFree(p->roww);
+  hipFree(p->slot);
+  hipFree(p->tiles);
+  delete p;
+}
+
+// Bucket the (token, slot) pairs per expert in ascending token order
+// (engine.rs:292-305), list ≤128-row tiles, and sort each token's slot rows by
+// expert id for the combine; the lists are copied into the plan's buffers.
+int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const float *wts,
+             MoePlan *plan, hipStream_t st) {
+  const char *op = "rk_moe_plan";
+  const int E = w.n_experts;
+  std::vector<int64_t> count(E, 0);
+  for (int64_t i = 0; i < s * top_k; ++i) {
+    if (ids[i] >= (uint32_t)E) return fail(RK_E_RANGE, op, "expert id out of range");
+    count[ids[i]]++;
+  }
+  std::vector<int64_t> off(E + 1, 0);
+  for (int e = 0; e < E; ++e) off[e + 1] = off[e] + count[e];
+  const int64_t R = off[E];
+  std::vector<int32_t> tok(R), slot(s * top_k);
+  std::vector<float> roww(R);
+  std::vector<int64_t> fill(off.begin(), off.end() - 1);
+  for (int64_t t = 0; t < s; ++t)
+    for (int j = 0; j < top_k; ++j) {
+      const int e = (int)ids[t * top_k + j];
+      const int64_t row = fill[e]++;
+      tok[row] = (int32_t)t;
+      roww[row] = wts[t * top_k + j];
+      slot[t * top_k + j] = (int32_t)row;
+    }
+  // Rows of one expert are contiguous and expert-major, so ordering a token's
+  // slots by row is ordering them by expert id.
+  for (int64_t t = 0; t < s; ++t) std::sort(slot.begin() + t * top_k, slot.begin() + (t + 1) * top_k);
+  std::vector<MoeTile> tiles;
+  for (int e = 0; e < E; ++e)
+    for (int64_t r = off[e]; r < off[e + 1]; r += 128)
+      tiles.push_back(MoeTile{e, (int)r, (int)std::min<int64_t>(128, off[e + 1] - r)});
+  HIP_TRY(hipMalloc((void **)&plan->tok, std::max<size_t>(R, 1) * 4), op);
+  HIP_TRY(hipMalloc((void **)&plan->roww, std::max<size_t>(R, 1) * 4), op);
+  HIP_TRY(hipMalloc((void **)&plan->slot, std::max<size_t>(slot.size(), 1) * 4), op);
+  HIP_TRY(hipMalloc((void **)&plan->tiles, std::max<size_t>(tiles.size(), 1) * sizeof(MoeTile)), op);
+  if (R) {
+    HIP_TRY(hipMemcpyAsync(plan->tok, tok.data(), R * 4, hipMemcpyHostToDevice, st), op);
+    HIP_TRY(hipMemcpyAsync(plan->roww, roww.data(), R * 4, hipMemcpyHostToDevice, st), op);
+    HIP_TRY(hipMemcpyAsync(plan->tiles, tiles.data(), tiles.size() * sizeof(MoeTile),
+                           hipMemcpyHostToDevice, st),
+            op);
+  }
+  if (!slot.empty())
+    HIP_TRY(hipMemcpyAsync(plan->slot, slot.data(), slot.size() * 4, hipMemcpyHostToDevice, st), op);
+  // The host vectors die at return: finish the copies first.
+  HIP_TRY(hipStreamSynchronize(st), op);
+  plan->s = s;
+  plan->top_k = top_k;
+  plan->rows = R;
+  plan->n_tiles = (int)tiles.size();
+  return RK_OK;
+}
+
+int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipStream_t st) {
+  const int64_t H = w.hidden, I = w.inter, S = plan.s, R = plan.rows;
+  void *xq, *xs, *act, *aq, *as, *yb;
+  RK_TRY(scratch("moe_xq", (size_t)S * H, &xq));
+  RK_TRY(scratch("moe_xs", (size_t)S * 4, &xs));
+  RK_TRY(scratch("moe_act", (size_t)std::max<int64_t>(R, 1) * I * 4, &act));
+  RK_TRY(scratch("moe_aq", (size_t)std::max<int64_t>(R, 1) * I, &aq));
+  RK_TRY(scratch("moe_as", (size_t)std::max<int64_t>(R, 1) * 4, &as));
+  RK_TRY(scratch("moe_yb", (size_t)std::max<int64_t>(R, 1) * H * 4, &yb));
+  const char *op = "rk_moe_experts_dev";
+  HIP_TRY(rk_launch_quantize_rows(x, S, H, H, (int8_t *)xq, (float *)xs, st), op);
+  HIP_TRY(rk_launch_moe_gemm_gu((const int8_t *)xq, (const float *)xs, plan.tok, plan.tiles,
+                                plan.n_tiles, w.gu_codes, w.gu_scales, 2 * I * H,
+                                2 * I * w.gu_ws_stride, w.gu_ws_stride, (int)(2 * I), (int)H,
+                                (float *)act, g_eng->num_cus, st),
+          op);
+  HIP_TRY(rk_launch_quantize_rows((const float *)act, R, I, I, (int8_t *)aq, (float *)as, st), op);
+  HIP_TRY(rk_launch_moe_gemm_down((const int8_t *)aq, (const float *)as, plan.tiles, plan.n_tiles,
+                                  w.dn_codes, w.dn_scales, H * I, H * w.dn_ws_stride,
+                                  w.dn_ws_stride, (int)H, (int)I, plan.roww, (float *)yb,
+                                  g_eng->num_cus, st),
+          op);
+  HIP_TRY(rk_launch_moe_combine((const float *)yb, plan.slot, S, plan.top_k, H, y, st), op);
+  return RK_OK;
+}
+
+int moe_check(uint64_t id, int64_t s, int top_k, Weight **w, const char *op) {
+  *w = find(id);
+  if (!*w || !(*w)->moe) return fail(RK_E_RANGE, op, "id is not an expert stack");
+  if (s <= 0 || top_k <= 0 || top_k > (*w)->n_experts)
+    return fail(RK_E_SHAPE, op, "need s > 0 and 0 < top_k <= n_experts");
+  return RK_OK;
+}
+}  // namespace
+
+extern "C" int rk_moe_experts_dev(rk_weight_id id, const float *x, int64_t s, int top_k,
+                                  const uint32_t *ids, const float *wts, float *y,
+                                  rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_moe_experts_dev"));
+  Weight *w;
+  RK_TRY(moe_check(id, s, top_k, &w, "rk_moe_experts_dev"));
+  hipStream_t st = pick(stream);
+  MoePlan *plan = new MoePlan();
+  int rc = moe_plan(*w, s, top_k, ids, wts, plan, st);
+  if (rc == RK_OK) rc = moe_run(*w, *plan, x, y, st);
+  // The plan's lists must outlive the kernels that read them.
+  hipError_t e = hipStreamSynchronize(st);
+  plan_free(plan);
+  if (rc != RK_OK) return rc;
+  HIP_TRY(e, "rk_moe_experts_dev");
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_moe_plan_create(rk_weight_id id, int64_t s, int top_k, const uint32_t *ids,
+                                  const float *wts, void **plan) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_moe_plan_create"));
+  Weight *w;
+  RK_TRY(moe_check(id, s, top_k, &w, "rk_moe_plan_create"));
+  MoePlan *p = new MoePlan();
+  const int rc = moe_plan(*w, s, top_k, ids, wts, p, g_eng->stream);
+  if (rc != RK_OK) {
+    plan_free(p);
+    return rc;
+  }
+  p->weight = id;
+  *plan = p;
+  return RK_OK;
+}
+
+extern "C" int rk_moe_experts_planned_dev(rk_weight_id id, const void *plan, const float *x,
+                                          float *y, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_moe_experts_planned_dev"));
+  const MoePlan *p = (const MoePlan *)plan;
+  if (!p) return fail(RK_E_SHAPE, "rk_moe_experts_planned_dev", "null plan");
+  Weight *w;
+  RK_TRY(moe_check(id, p->s, p->top_k, &w, "rk_moe_experts_planned_dev"));
+  if (p->weight != id)
+    return fail(RK_E_SHAPE, "rk_moe_experts_planned_dev", "plan was made for another expert stack");
+  RK_TRY(moe_run(*w, *p, x, y, pick(stream)));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_moe_plan_destroy(void *plan) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_moe_plan_destroy"));
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_moe_plan_destroy");
+  plan_free((MoePlan *)plan);
+  return RK_OK;
+}
+
+// =========================================================================
+// Device plumbing
+// =========================================================================
+extern "C" int rk_device_alloc(size_t bytes, void **ptr) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_device_alloc"));
+  HIP_TRY(hipMalloc(ptr, std::max<size_t>(bytes, 1)), "rk_device_alloc");
+  return RK_OK;
+}
+extern "C" int rk_device_free(void *ptr) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_device_free"));
+  HIP_TRY(hipFree(ptr), "rk_device_free");
+  return RK_OK;
+}
+extern "C" int rk_memcpy_htod(void *dst, const void *src, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_memcpy_htod"));
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "rk_memcpy_htod");
+  return RK_OK;
+}
+extern "C" int rk_memcpy_dtoh(void *dst, const void *src, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_memcpy_dtoh"));
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_memcpy_dtoh");
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "rk_memcpy_dtoh");
+  return RK_OK;
+}
+extern "C" int rk_memset_dev(void *dst, int value, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_memset_dev"));
+  HIP_TRY(hipMemset(dst, value, bytes), "rk_memset_dev");
+  return RK_OK;
+}
+extern "C" int rk_stream_get(rk_stream *stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_stream_get"));
+  *stream = (rk_stream)g_eng->stream;
+  return RK_OK;
+}
+extern "C" int rk_stream_sync(rk_stream stream) {
+  RK_TRY(ensure("rk_stream_sync"));
+  HIP_TRY(hipStreamSynchronize(stream ? (hipStream_t)stream : g_eng->stream), "rk_stream_sync");
+  return RK_OK;
+}
+extern "C" int rk_event_create(void **event) {
+  RK_TRY(ensure("rk_event_create"));
+  HIP_TRY(hipEventCreate((hipEvent_t *)event), "rk_event_create");
+  return RK_OK;
+}
+extern "C" int rk_event_destroy(void *event) {
+  HIP_TRY(hipEventDestroy((hipEvent_t)event), "rk_event_destroy");
+  return RK_OK;
+}
+extern "C" int rk_event_record(void *event, rk_stream stream) {
+  RK_TRY(ensure("rk_event_record"));
+  HIP_TRY(hipEventRecord((hipEvent_t)event, stream ? (hipStream_t)stream : g_eng->stream),
+          "rk_event_record");
+  return RK_OK;
+}
+extern "C" int rk_event_elapsed_ms(void *start, void *stop, float *ms) {
+  HIP_TRY(hipEventSynchronize((hipEvent_t)stop), "rk_event_elapsed_ms");
+  HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop), "rk_event_elapsed_ms");
+  return RK_OK;
+}
+extern "C" int rk_device_info(char *name, size_t name_len, int *cus, int *clock_khz) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_device_info"));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, g_eng->device), "rk_device_info");
+  if (name && name_len) {
+    std::snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (cus) *cus = prop.multiProcessorCount;
+  if (clock_khz) *clock_khz = prop.clockRate;
+  return RK_OK;
+}

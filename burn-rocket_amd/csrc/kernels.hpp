@@ -1,0 +1,93 @@
+// Host-callable launchers of the gfx950 kernels (defined in the .hip files).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// fp16 GEMM, C[M,N] = A[M,K]·B[N,K]ᵀ, K % 8 == 0.
+hipError_t rk_launch_gemm_f16(const void *A, const void *B, void *C, int M, int N, int K,
+                              int num_cus, hipStream_t st);
+
+enum I8Mode { I8_PER_TOKEN = 0, I8_PER_GROUP = 1, I8_RAW = 2, I8_PARTIALS = 3 };
+
+struct I8GemmArgs {
+  const int8_t *A;     // [M, K]
+  const float *AS;     // activation scales [M, as_stride] (PER_TOKEN: [M, 1])
+  int as_stride;       // K / a_group
+  int a_gb;            // a_group / 32 (PER_GROUP)
+  const int8_t *W;     // [N, K]
+  const float *WS;     // weight scale per 32-block [N, ws_stride]
+  int ws_stride;       // K/32 rounded up to a multiple of 4
+  int gb;              // weight group / 32
+  void *C;             // f32 / fp16 [M, N], int32 [M, N] (RAW), int32 [M, N, K/32] (PARTIALS)
+  int M, N, K;
+  int mode;            // I8Mode
+  bool out_f16;
+  int num_cus;
+};
+hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st);
+
+// Element-wise conversions.
+hipError_t rk_launch_f32_to_f16(const float *x, void *y, int64_t n, hipStream_t st);
+hipError_t rk_launch_f16_to_f32(const void *x, float *y, int64_t n, hipStream_t st);
+
+// Per-row symmetric quantizer (scale = max(amax/127, 1e-12), codes
+// round-half-away(x·(1/scale)) clamped to ±127), `group` values per scale.
+hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,
+                                   int8_t *q, float *scale, hipStream_t st);
+// Static / dynamic per-row quantizer of the QAT path (ties-to-even, [-128,127]).
+hipError_t rk_launch_quantize_static(const float *x, int64_t m, int64_t k, float in_scale,
+                                     int8_t *q, float *row_scale, hipStream_t st);
+// GGUF Q8_0 quantization of f32 rows into codes + per-block f32 scales, with
+// rows remapped as (r/32)·grp_stride + grp_off + r%32.
+hipError_t rk_launch_q8_0_quantize(const float *w, int64_t n, int64_t k, int grp_stride,
+                                   int grp_off, int8_t *codes, float *scales, int ws_stride,
+                                   hipStream_t st);
+// QAT epilogue: y = acc·(row_scale[m]·w_scale[n]), optionally rounded to the
+// out_scale grid.
+hipError_t rk_launch_qat_epilogue(const int32_t *acc, const float *row_scale,
+                                  const float *w_scale, int64_t m, int64_t n, float out_scale,
+                                  float *y, hipStream_t st);
+
+// Attention.
+struct AttnArgs {
+  const void *q;   // fp16, row (token) stride q_stride, head h at column h·D
+  const void *k;   // fp16 [n_kv, k_stride], kv head g at column g·D
+  const void *vt;  // fp16 V transposed and key-permuted: [KV][Dv_pad][n_kv_pad]
+  void *out;       // fp16, same layout as q (o_stride)
+  int64_t q_stride, k_stride, o_stride;  // in elements
+  int64_t q_head_stride, k_head_stride, o_head_stride;  // elements between heads
+  int64_t q_tok_stride, k_tok_stride, o_tok_stride;     // elements between tokens
+  int n_q, n_kv, n_kv_pad;
+  int n_head, n_kv_heads, head_dim;
+  float scale, softcap;
+  int mask_mode;
+  int64_t window, q0, k0;
+  int num_cus;
+};
+// V [n_kv, tok stride] (kv head g at column g·D) → Vt [KV][Dv_pad][n_kv_pad].
+hipError_t rk_launch_v_transpose(const void *v, int64_t v_tok_stride, int64_t v_head_stride,
+                                 int n_kv, int n_kv_pad, int n_kv_heads, int head_dim,
+                                 int dv_pad, void *vt, hipStream_t st);
+int rk_attn_dv_pad(int head_dim);
+int rk_attn_kv_tile();
+hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st);
+
+// MoE helpers.
+struct MoeTile {
+  int expert;   // expert id
+  int row0;     // first bucket row of the tile
+  int rows;     // rows in the tile
+};
+hipError_t rk_launch_moe_gemm_gu(const int8_t *xq, const float *xs, const int32_t *tok,
+                                 const MoeTile *tiles, int n_tiles, const int8_t *w,
+                                 const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
+                                 int ws_stride, int N, int K, float *act, int num_cus,
+                                 hipStream_t st);
+hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, const MoeTile *tiles,
+                                   int n_tiles, const int8_t *w, const float *ws,
+                                   int64_t w_stride_e, int64_t ws_stride_e, int ws_stride,
+                                   int N, int K, const float *row_w, float *yb, int num_cus,
+                                   hipStream_t st);
+hipError_t rk_launch_moe_combine(const float *yb, const int32_t *slot_rows, int64_t s, int top_k,
+                                 int64_t h, float *y, hipStream_t st);

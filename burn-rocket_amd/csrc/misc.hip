@@ -1,0 +1,190 @@
+// Format conversions and activation quantizers on the GPU.
+//
+// These are the host-side steps around every call in the reference
+// (f32_to_f16_par / f16_to_f32_par ext.rs:2144-2170, quantize_i8_rows
+// ext.rs:1017-1029 with quantize_row_groups host.rs:77-90, the QAT static
+// quantizer and epilogue ext.rs:1236-1373), moved next to the data.
+#include "common.hpp"
+#include "kernels.hpp"
+
+__global__ void f32_to_f16_kernel(const float *__restrict__ x, f16 *__restrict__ y, int64_t n) {
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    floatx4 v = *(const floatx4 *)(x + i);
+    half4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    *(half4 *)(y + i) = h;
+  } else {
+    for (; i < n; ++i) y[i] = (f16)x[i];
+  }
+}
+
+__global__ void f16_to_f32_kernel(const f16 *__restrict__ x, float *__restrict__ y, int64_t n) {
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    half4 h = *(const half4 *)(x + i);
+    *(floatx4 *)(y + i) = floatx4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  } else {
+    for (; i < n; ++i) y[i] = (float)x[i];
+  }
+}
+
+hipError_t rk_launch_f32_to_f16(const float *x, void *y, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  // Vector path needs 16-byte aligned rows of 4; callers pass whole buffers.
+  int64_t threads = (n + 3) / 4;
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, x, (f16 *)y, n);
+  return hipGetLastError();
+}
+
+hipError_t rk_launch_f16_to_f32(const void *x, float *y, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  int64_t threads = (n + 3) / 4;
+  hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, (const f16 *)x, y, n);
+  return hipGetLastError();
+}
+
+// One workgroup per row. Group maxima are reduced with LDS atomics on the
+// f32 bit pattern (all values are >= 0, so integer order is float order).
+constexpr int QROW_THREADS = 256;
+constexpr int QROW_MAX_GROUPS = 1024;
+
+__global__ __launch_bounds__(QROW_THREADS) void quantize_rows_kernel(
+    const float *__restrict__ x, int64_t k, int64_t group, int8_t *__restrict__ q,
+    float *__restrict__ scale) {
+  __shared__ unsigned int amax[QROW_MAX_GROUPS];
+  __shared__ float inv[QROW_MAX_GROUPS];
+  const int64_t row = blockIdx.x;
+  const int ng = (int)(k / group);
+  const float *xr = x + row * k;
+  for (int g = threadIdx.x; g < ng; g += QROW_THREADS) amax[g] = 0u;
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < k; i += QROW_THREADS) {
+    float a = fabsf(xr[i]);
+    atomicMax(&amax[i / group], __float_as_uint(a));
+  }
+  __syncthreads();
+  for (int g = threadIdx.x; g < ng; g += QROW_THREADS) {
+    float s = fmaxf(__uint_as_float(amax[g]) / 127.0f, 1e-12f);
+    scale[row * ng + g] = s;
+    inv[g] = 1.0f / s;
+  }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < k; i += QROW_THREADS) {
+    float v = roundf(xr[i] * inv[i / group]);
+    v = fminf(fmaxf(v, -127.0f), 127.0f);
+    q[row * k + i] = (int8_t)(int)v;
+  }
+}
+
+hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,
+                                   int8_t *q, float *scale, hipStream_t st) {
+  if (m <= 0) return hipSuccess;
+  if (k / group > QROW_MAX_GROUPS) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)m), dim3(QROW_THREADS), 0, st, x, k,
+                     group, q, scale);
+  return hipGetLastError();
+}
+
+// QAT activation grid: ties-to-even, clamped to [-128, 127]. in_scale == 0
+// selects the per-row dynamic scale max(amax/127, 1e-12).
+__global__ __launch_bounds__(QROW_THREADS) void quantize_static_kernel(
+    const float *__restrict__ x, int64_t k, float in_scale, int8_t *__restrict__ q,
+    float *__restrict__ row_scale) {
+  __shared__ unsigned int amax;
+  __shared__ float inv_s;
+  const int64_t row = blockIdx.x;
+  const float *xr = x + row * k;
+  if (threadIdx.x == 0) amax = 0u;
+  __syncthreads();
+  if (in_scale == 0.0f) {
+    for (int64_t i = threadIdx.x; i < k; i += QROW_THREADS)
+      atomicMax(&amax, __float_as_uint(fabsf(xr[i])));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float rs = in_scale;
+    if (in_scale == 0.0f) rs = fmaxf(__uint_as_float(amax) / 127.0f, 1e-12f);
+    row_scale[row] = rs;
+    inv_s = 1.0f / rs;
+  }
+  __syncthreads();
+  const float inv = inv_s;
+  for (int64_t i = threadIdx.x; i < k; i += QROW_THREADS) {
+    float v = rintf(xr[i] * inv);
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    q[row * k + i] = (int8_t)(int)v;
+  }
+}
+
+hipError_t rk_launch_quantize_static(const float *x, int64_t m, int64_t k, float in_scale,
+                                     int8_t *q, float *row_scale, hipStream_t st) {
+  if (m <= 0) return hipSuccess;
+  hipLaunchKernelGGL(quantize_static_kernel, dim3((unsigned)m), dim3(QROW_THREADS), 0, st, x, k,
+                     in_scale, q, row_scale);
+  return hipGetLastError();
+}
+
+__global__ void qat_epilogue_kernel(const int32_t *__restrict__ acc,
+                                    const float *__restrict__ row_scale,
+                                    const float *__restrict__ w_scale, int64_t m, int64_t n,
+                                    float out_scale, float *__restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= m * n) return;
+  const int64_t r = i / n, c = i % n;
+  float v = (float)acc[i] * (row_scale[r] * w_scale[c]);
+  if (out_scale != 0.0f) {
+    const float out_inv = 1.0f / out_scale;
+    float code = fminf(fmaxf(rintf(v * out_inv), -128.0f), 127.0f);
+    v = code * out_scale;
+  }
+  y[i] = v;
+}
+
+hipError_t rk_launch_qat_epilogue(const int32_t *acc, const float *row_scale,
+                                  const float *w_scale, int64_t m, int64_t n, float out_scale,
+                                  float *y, hipStream_t st) {
+  if (m * n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(qat_epilogue_kernel, dim3((unsigned)((m * n + 255) / 256)), dim3(256), 0,
+                     st, acc, row_scale, w_scale, m, n, out_scale, y);
+  return hipGetLastError();
+}
+
+// GGUF Q8_0 quantizer (llama.cpp rule, crates/rocket-npu/src/bin/q8_bench.rs:
+// 200-220): per 32-value block d = f16(amax/127); codes are quantized against
+// the stored f32(d) with inv = d > 0 ? 1/d : 0, round-half-away, clamp ±127.
+// One thread per block. Source row r of block column b goes to destination
+// row (r / 32)·grp_stride + grp_off + r % 32, which lets the gate and up
+// projections of an expert interleave per 32-row slice.
+__global__ void q8_0_quantize_kernel(const float *__restrict__ w, int64_t n, int64_t k,
+                                     int grp_stride, int grp_off, int8_t *__restrict__ codes,
+                                     float *__restrict__ scales, int ws_stride) {
+  const int64_t nb = k / 32;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * nb) return;
+  const int64_t r = i / nb, b = i % nb;
+  const float *src = w + r * k + b * 32;
+  float amax = 0.f;
+  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(src[j]));
+  const float scale = (float)(f16)(amax / 127.0f);
+  const float inv = scale > 0.f ? 1.0f / scale : 0.f;
+  const int64_t dr = (r / 32) * grp_stride + grp_off + (r % 32);
+  int8_t *dst = codes + dr * k + b * 32;
+  for (int j = 0; j < 32; ++j) {
+    float v = roundf(src[j] * inv);
+    v = fminf(fmaxf(v, -127.0f), 127.0f);
+    dst[j] = (int8_t)(int)v;
+  }
+  scales[dr * ws_stride + b] = scale;
+}
+
+hipError_t rk_launch_q8_0_quantize(const float *w, int64_t n, int64_t k, int grp_stride,
+                                   int grp_off, int8_t *codes, float *scales, int ws_stride,
+                                   hipStream_t st) {
+  const int64_t total = n * (k / 32);
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(q8_0_quantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                     w, n, k, grp_stride, grp_off, codes, scales, ws_stride);
+  return hipGetLastError();
+}

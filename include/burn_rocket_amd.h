@@ -1,0 +1,304 @@
+/*
+ * burn_rocket_amd.h — C ABI of the MI355X (gfx950) accelerator op surface.
+ *
+ * This is the boundary a Burn backend extension binds over FFI. It replaces the
+ * `rocket-npu` driver calls that `crates/burn-rocket` makes today and keeps the
+ * same op surface: resident fp16 weights and their matmul, resident W8A8 / GGUF
+ * Q8_0 int8 weights and their matmul, masked grouped-query flash attention, and
+ * the MoE expert pipeline. Each entry point cites the reference item it stands
+ * in for (paths relative to the royalcat/burn-rocket tree).
+ *
+ * Conventions
+ *   - Every entry returns RK_OK (0) or a negative status code with the meaning
+ *     of `crates/rocket-npu/src/error.rs:11-51`; `rk_last_error()` returns the
+ *     message of the last failure on the calling thread.
+ *   - Calls are serialised by one engine mutex (`ext.rs:543-556`); work inside a
+ *     call runs on the library's HIP stream (or the stream passed to a `_dev`
+ *     entry) and is stream-ordered.
+ *   - Host entries (`rk_matmul`, `rk_attention`, ...) take and return host f32
+ *     buffers, as Burn's flex tensors do; conversion to fp16 / int8 happens on
+ *     the GPU. `_dev` entries take device pointers that are already resident in
+ *     HBM and do no host<->device copies.
+ *   - Weight handles are u64 ids that stay valid for the process lifetime
+ *     (`ext.rs:39-43`).
+ *   - Matrices are row-major. A weight is [N, K] (HF `[out, in]`), an activation
+ *     is [M, K], the product is [M, N] = x · Wᵀ.
+ */
+#ifndef BURN_ROCKET_AMD_H
+#define BURN_ROCKET_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: crates/rocket-npu/src/error.rs:11-51 ------------------ */
+#define RK_OK 0
+#define RK_E_SHAPE (-1)       /* unsupported shape or bad argument */
+#define RK_E_TILING (-2)      /* shape not tileable (caller may fall back) */
+#define RK_E_NOMEM (-3)       /* device or host allocation failed */
+#define RK_E_DEVICE (-4)      /* HIP runtime / device failure */
+#define RK_E_UNSUPPORTED (-5) /* feature not supported */
+#define RK_E_RANGE (-6)       /* value out of range (fp16 overflow, id unknown) */
+#define RK_E_IO (-7)          /* I/O failure */
+
+/* ---- weight kinds (ext.rs:1156-1161 `WeightKind`) ------------------------ */
+#define RK_WEIGHT_F16 1 /* resident fp16 [N, K] */
+#define RK_WEIGHT_I8 2  /* resident int8 codes [N, K] + f32 scales [N, K/group] */
+#define RK_WEIGHT_QAT 3 /* resident per-channel int8 codes + w_scale [N] */
+
+/* ---- attention mask modes (ext.rs:1643-1666 `MaskMode`) ------------------ *
+ * With absolute query position t = q0 + i and key position j = k0 + jj:
+ *   RK_MASK_NONE           every key visible
+ *   RK_MASK_CAUSAL         j <= t
+ *   RK_MASK_WINDOW         |t - j| <= window
+ *   RK_MASK_CAUSAL_WINDOW  t - window < j <= t
+ * q0 = k0 = 0 with n_q == n_kv is the full-sequence form; other offsets are the
+ * query-chunk block forms (`masks.rs:44-114`). Masks are evaluated as
+ * predicates inside the kernel; no mask tensor is built.                      */
+#define RK_MASK_NONE 0
+#define RK_MASK_CAUSAL 1
+#define RK_MASK_WINDOW 2
+#define RK_MASK_CAUSAL_WINDOW 3
+
+typedef uint64_t rk_weight_id;
+typedef void *rk_stream; /* a hipStream_t; NULL selects the library stream */
+
+/* ======================================================================== *
+ * Engine                                                                    *
+ * ======================================================================== */
+
+/* Create the process-global engine on HIP device `device`. Later calls are
+ * no-ops. Replaces `burn_rocket::init(threads)` (ext.rs:561-580). */
+int rk_init(int device);
+
+/* Message of the last failure on this thread ("" if none). Mirrors
+ * `burn_rocket::Error`'s Display (lib.rs:125-140). */
+const char *rk_last_error(void);
+
+/* 1 when `rc` asks the caller to fall back to another path (RK_E_TILING),
+ * as `burn_rocket::Error::is_fallback` (lib.rs:142-147). */
+int rk_is_fallback(int rc);
+
+/* Op wall-time counters: `burn_rocket::stats()` / `stats_reset()`
+ * (ext.rs:171-200). convert_s covers host<->device copies and format
+ * conversion, device_s the kernels, calls counts op invocations. */
+typedef struct {
+  double convert_s;
+  double device_s;
+  uint64_t calls;
+} rk_stats_t;
+int rk_stats(rk_stats_t *out);
+int rk_stats_reset(void);
+
+/* Live memory held by the engine: `burn_rocket::mem_stats()` (ext.rs:206-252).*/
+typedef struct {
+  uint64_t weights_bytes; /* resident weights */
+  uint64_t scratch_bytes; /* per-shape device scratch */
+  uint64_t n_weights;
+} rk_mem_stats_t;
+int rk_mem_stats(rk_mem_stats_t *out);
+/* Drop scratch above `budget` bytes / all scratch: `trim_scratch_to`,
+ * `clear_scratch` (ext.rs:256-308). */
+int rk_trim_scratch_to(uint64_t budget);
+int rk_clear_scratch(void);
+
+/* ======================================================================== *
+ * Resident weights                                                          *
+ * ======================================================================== */
+
+/* fp16 weight from f32 [N, K] (RNE), `pack` (ext.rs:1866, pack_one ext.rs:869,
+ * to_host ext.rs:758-776). */
+int rk_pack(const float *w, int64_t n, int64_t k, rk_weight_id *id);
+/* fp16 weight from fp16 bits [N, K] (the F16 arm of to_host, ext.rs:770). */
+int rk_pack_f16(const uint16_t *w, int64_t n, int64_t k, rk_weight_id *id);
+/* Segmented fp16 weight: `nparts` f32 parts [ns[i], K] concatenated along N
+ * (`pack2`/`pack3` → pack_seg, ext.rs:836-855, ext.rs:1870-1885). */
+int rk_pack_seg(const float *const *parts, const int64_t *ns, int nparts,
+                int64_t k, rk_weight_id *id);
+
+/* Group-wise int8 weight from f32 [N, K]: per (n, K-group) scale
+ * max(amax/127, 1e-12), codes round-half-away(x * (1/scale)) clamped to ±127
+ * (`pack_i8` → quantize_i8_weight → quantize_row_groups, ext.rs:939-1012,
+ * host.rs:77-90). group % 32 == 0 and K % group == 0. */
+int rk_pack_i8(const float *w, int64_t n, int64_t k, int64_t group,
+               rk_weight_id *id);
+/* Pre-quantized group-wise weight: codes [N, K], scales [N, K/group]
+ * (`RocketI8Ctx::pack_weight_gw`, lib.rs:363; int8.rs:458). */
+int rk_pack_i8_codes(const int8_t *codes, const float *scales, int64_t n,
+                     int64_t k, int64_t group, rk_weight_id *id);
+/* Replace the codes/scales of a resident group-wise weight in place
+ * (`I8Context::rewrite_weight_gw`, int8.rs:521). */
+int rk_rewrite_i8(rk_weight_id id, const int8_t *codes, const float *scales);
+/* GGUF Q8_0 weight: [N, K/32] blocks of 34 bytes {f16 d, int8 q[32]}
+ * (src/util/gguf.rs:125-200). Stored as codes + f32(d), group 32. */
+int rk_pack_q8_0(const uint8_t *blocks, int64_t n, int64_t k, rk_weight_id *id);
+/* GGUF Q8_0 weight quantized on the device from f32 [N, K] with llama.cpp's
+ * rule (crates/rocket-npu/src/bin/q8_bench.rs:200-220): per 32 values
+ * d = f16(amax/127), codes round-half-away(x / f32(d)) clamped to ±127.
+ * K % 32 == 0. The resident form equals rk_pack_q8_0 of the same blocks. */
+int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_id *id);
+/* Per-channel QAT weight (`pack_qat`, ext.rs:1382-1425): codes [N, K],
+ * w_scale [N], static activation scale in_scale (0 = per-row dynamic
+ * amax/127), output grid out_scale (0 = none). */
+int rk_pack_qat(const int8_t *codes, const float *w_scale, int64_t n, int64_t k,
+                float in_scale, float out_scale, rk_weight_id *id);
+
+/* Kind (RK_WEIGHT_*), N, K and group of a resident weight. */
+int rk_weight_info(rk_weight_id id, int *kind, int64_t *n, int64_t *k,
+                   int64_t *group);
+
+/* ======================================================================== *
+ * Matmul                                                                    *
+ * ======================================================================== */
+
+/* y[M, N] = x[M, K] · Wᵀ for any resident weight, host f32 in and out
+ * (`rocket_matmul` → matmul_impl, ext.rs:627, ext.rs:1208-1232):
+ *   F16: x → fp16 (RNE), fp16 GEMM with f32 accumulation, fp16 result widened
+ *        to f32 (matmul_f16, ext.rs:1437-1499);
+ *   I8 : x quantized per row per weight group (quantize_i8_rows, ext.rs:1017),
+ *        C = Σ_g (a_s[m,g]·w_s[n,g])·P_g with exact int32 P_g (matmul_i8,
+ *        ext.rs:1505; detile_accum_i8_scaled, layout.rs:504-540);
+ *   QAT: x quantized with the static scale (ties-to-even, [-128,127]) or per
+ *        row dynamically, exact int32 C, epilogue acc·(in_scale·w_scale[n])
+ *        and optional output-grid rounding (matmul_qat, ext.rs:1236-1373). */
+int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, float *y);
+
+/* fp16 GEMM on device buffers: a fp16 [M, K], c fp16 [M, N]
+ * (`RocketCtx::matmul_prepacked`, lib.rs:244-254). K % 8 == 0. */
+int rk_matmul_f16_dev(rk_weight_id id, const void *a, int64_t m, int64_t k,
+                      void *c, rk_stream stream);
+
+/* Per-row activation quantizer on device (`quantize_i8_rows`, ext.rs:1017;
+ * quantize_row_groups, host.rs:77-90): x f32 [M, K] → q int8 [M, K] and
+ * scale f32 [M, K/group]. group == K is per-token quantization. */
+int rk_quantize_rows_dev(const float *x, int64_t m, int64_t k, int64_t group,
+                         int8_t *q, float *scale, rk_stream stream);
+
+/* W8A8 GEMM on device buffers against a resident I8 weight
+ * (`I8Context::matmul_gw`, int8.rs:644-676): a int8 [M, K] with scales
+ * a_scale [M, K/a_group]; a_group is the weight's group (reference formula
+ * Σ_g (a_s·w_s)·P_g) or K (per-token: a_s[m]·Σ_g w_s[n,g]·P_g).
+ * c f32 [M, N]. */
+int rk_matmul_w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale,
+                       int64_t a_group, int64_t m, int64_t k, float *c,
+                       rk_stream stream);
+/* Same, fp16 output. */
+int rk_matmul_w8a8_f16out_dev(rk_weight_id id, const int8_t *a,
+                              const float *a_scale, int64_t a_group, int64_t m,
+                              int64_t k, void *c, rk_stream stream);
+
+/* Raw integer product of int8 activations and a resident I8/QAT weight's
+ * codes: c int32 [M, N] = Σ_k a[m,k]·w[n,k], exact (`I8Context::matmul`,
+ * int8.rs:606-640). */
+int rk_matmul_i8_raw_dev(rk_weight_id id, const int8_t *a, int64_t m, int64_t k,
+                         int32_t *c, rk_stream stream);
+
+/* Per-block int32 partials of the same product: p int32 [M, N, K/32],
+ * p[m,n,b] = Σ_{k in block b} a[m,k]·w[n,k] over 32-value blocks. Exposes
+ * the accumulators the scaled W8A8 kernel folds, for exactness checks (the
+ * per-K-tile partials of `drain`, int8.rs:708-746). */
+int rk_matmul_i8_partials_dev(rk_weight_id id, const int8_t *a, int64_t m,
+                              int64_t k, int32_t *p, rk_stream stream);
+
+/* ======================================================================== *
+ * Attention                                                                 *
+ * ======================================================================== */
+
+/* Masked grouped-query attention, token-major host f32 buffers as Burn passes
+ * them (`rocket_attention*` → attention_impl, ext.rs:631-755,
+ * ext.rs:1669-1858): q [n_q, n_head·head_dim], k/v [n_kv, n_kv_heads·head_dim],
+ * out [n_q, n_head·head_dim]. Query head h reads kv head h / (n_head /
+ * n_kv_heads). Score = scale·q·k (softcap·tanh(score/softcap) when softcap !=
+ * 0), f32 online softmax over the visible keys, fp16 operands, fp16 result
+ * widened to f32. A query row with no visible key averages V uniformly over
+ * the n_kv keys (flash_attn_ref, attn/oneshot.rs:118-127). window < 0 turns
+ * the window modes into NONE / CAUSAL (ext.rs:99-126). */
+int rk_attention(const float *q, const float *k, const float *v, int64_t n_q,
+                 int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
+                 float scale, float softcap, int mask_mode, int64_t window,
+                 int64_t q0, int64_t k0, float *out);
+
+/* The same on fp16 device buffers in the token-major layout. */
+int rk_attention_dev(const void *q, const void *k, const void *v, int64_t n_q,
+                     int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
+                     float scale, float softcap, int mask_mode, int64_t window,
+                     int64_t q0, int64_t k0, void *out, rk_stream stream);
+
+/* Head-major fp16 host buffers, the `RocketFaCtx::flash_attn` layout
+ * (lib.rs:294-323; attn/mod.rs:1541-1600): q [n_head][n_q][head_dim],
+ * k [n_kv_heads][n_kv][head_dim], v transposed [n_kv_heads][dv][n_kv],
+ * out [n_head][n_q][dv]; dv == head_dim. */
+int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv,
+                      int n_head, int n_kv_heads, float scale, float softcap,
+                      int mask_mode, int64_t window, int64_t q0, int64_t k0,
+                      const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                      uint16_t *out);
+
+/* ======================================================================== *
+ * MoE experts                                                               *
+ * ======================================================================== */
+
+/* Router: softmax over n_experts logits per token, top_k descending with ties
+ * to the lower id, optional renormalisation (`route`, src/clef/model.rs:462-489).
+ * logits f32 [s, n_experts] → ids u32 [s, top_k], wts f32 [s, top_k]. Host. */
+int rk_moe_route(const float *logits, int64_t s, int n_experts, int top_k,
+                 int norm_topk, uint32_t *ids, float *wts);
+
+/* Resident expert stack: n_experts Q8_0 expert FFNs, each gate [inter, hidden],
+ * up [inter, hidden], down [hidden, inter], as GGUF Q8_0 blocks
+ * (src/clef/engine_npu.rs:110-207 packs gate|up and down per expert). */
+int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up,
+                     const uint8_t *down, int n_experts, int64_t hidden,
+                     int64_t inter, rk_weight_id *id);
+
+/* The same expert stack from f32 weights (gate/up [E][inter][hidden], down
+ * [E][hidden][inter]), quantized to Q8_0 on the device as rk_pack_q8_0_f32. */
+int rk_pack_moe_f32(const float *gate, const float *up, const float *down,
+                    int n_experts, int64_t hidden, int64_t inter,
+                    rk_weight_id *id);
+
+/* Expert FFN over routed tokens on device buffers: per token t and slot j,
+ * y[t] += wts[t,j] · down(silu(gate(x_t)) ⊙ up(x_t)) of expert ids[t,j], the
+ * slots summed in ascending expert id (combine, src/clef/engine.rs:317-338;
+ * layer_forward_multi, src/clef/model.rs:526-620). x f32 [s, hidden] is
+ * quantized per token; the gate|up product is quantized per row before down.
+ * ids/wts are host arrays (bucketing runs on the host, engine.rs:284-313);
+ * y f32 [s, hidden] is overwritten. */
+int rk_moe_experts_dev(rk_weight_id id, const float *x, int64_t s, int top_k,
+                       const uint32_t *ids, const float *wts, float *y,
+                       rk_stream stream);
+
+/* The same split in two: bucket once (host), keep the per-expert row lists,
+ * tiles and combine order on the device, then run the expert FFN for any x
+ * with that routing. Calls that use a plan must finish before it is
+ * destroyed (rk_moe_plan_destroy synchronises the library stream). */
+int rk_moe_plan_create(rk_weight_id id, int64_t s, int top_k,
+                       const uint32_t *ids, const float *wts, void **plan);
+int rk_moe_experts_planned_dev(rk_weight_id id, const void *plan,
+                               const float *x, float *y, rk_stream stream);
+int rk_moe_plan_destroy(void *plan);
+
+/* ======================================================================== *
+ * Device plumbing for callers without their own HIP runtime bindings       *
+ * ======================================================================== */
+int rk_device_alloc(size_t bytes, void **ptr);
+int rk_device_free(void *ptr);
+int rk_memcpy_htod(void *dst, const void *src, size_t bytes);
+int rk_memcpy_dtoh(void *dst, const void *src, size_t bytes);
+int rk_memset_dev(void *dst, int value, size_t bytes);
+int rk_stream_get(rk_stream *stream);    /* the library stream */
+int rk_stream_sync(rk_stream stream);
+int rk_event_create(void **event);
+int rk_event_destroy(void *event);
+int rk_event_record(void *event, rk_stream stream);
+int rk_event_elapsed_ms(void *start, void *stop, float *ms);
+/* Device name, compute units and clock (kHz) of the engine's device. */
+int rk_device_info(char *name, size_t name_len, int *cus, int *clock_khz);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BURN_ROCKET_AMD_H */

@@ -1,0 +1,168 @@
+"""GPU parity of the fused GQA flash attention (K3) against the oracle.
+
+The oracle computes any subset of query rows exactly (rows are independent and
+positions are absolute via q0), so full-size runs are checked on slices of
+rows from the start, middle and end of the sequence. Gate: cosine >= 0.9999
+and max relative error <= 1e-2 against the f32 tiled restatement of the Burn
+CPU attention and the f64 flash_attn_ref restatement."""
+import sys
+
+import numpy as np
+import pytest
+
+from burn_rocket import synth
+
+pytestmark = pytest.mark.gpu
+COS_MIN, REL_MAX = 0.9999, 1e-2
+
+
+def note(msg):
+    print(f"[case] {msg}", file=sys.stderr, flush=True)
+
+
+def attn_dev(rk, q, k, v, h, kv, d, scale, softcap=0.0, mode=0, window=-1, q0=0, k0=0):
+    n_q, n_kv = q.shape[0], k.shape[0]
+    bufs = [rk.DeviceBuffer.from_array(np.ascontiguousarray(a).view(np.uint16)) for a in (q, k, v)]
+    out = rk.DeviceBuffer(n_q * h * d * 2)
+    rc = rk.lib().rk_attention_dev(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, n_q, n_kv, h, kv, d, scale, softcap, mode,
+                                   window, q0, k0, out.ptr, None)
+    assert rc == 0, rk.lib().rk_last_error()
+    rk.synchronize()
+    return out.download((n_q, h * d), np.uint16).view(np.float16).astype(np.float32)
+
+
+def check(orc, got, ref):
+    assert np.isfinite(got).all()
+    cos, rel = orc.cosine(got, ref), orc.max_rel(got, ref)
+    assert cos >= COS_MIN and rel <= REL_MAX, (cos, rel)
+
+
+def check_rows(orc, got, q, k, v, h, kv, d, scale, rows, softcap=0.0, mode=0, window=-1, q0=0, k0=0,
+               ref64=True):
+    for a, b in rows:
+        flex = orc.attention_flex(q[a:b], k, v, h, kv, d, scale, softcap, mode, window, q0 + a, k0)
+        check(orc, got[a:b], flex)
+        if ref64:
+            ref = orc.attention_ref(q[a:b], k, v, h, kv, d, scale, softcap, mode, window, q0 + a, k0)
+            check(orc, got[a:b], ref)
+
+
+def _slices(n, w=48):
+    return [(0, min(w, n)), (max(0, n // 2 - w // 2), min(n, n // 2 + w // 2)), (max(0, n - w), n)]
+
+
+def test_config3_causal_gqa_full(rk, orc):
+    c = synth.GQA_CAUSAL
+    s, h, kv, d = c["s"], c["n_head"], c["n_kv"], c["d"]
+    seeds = synth.SEEDS["gqa"]
+    note(f"causal GQA S={s} H={h} KV={kv} D={d}")
+    q = synth.normal_f16(seeds[0], (s, h * d))
+    k = synth.normal_f16(seeds[1], (s, kv * d))
+    v = synth.normal_f16(seeds[2], (s, kv * d))
+    got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=1)
+    check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(s), mode=1)
+
+
+def test_config4_bidirectional_mha_d72_full(rk, orc):
+    c = synth.VISION
+    s, h, d = c["s"], c["n_head"], c["d"]
+    seeds = synth.SEEDS["vision"]
+    note(f"bidirectional MHA S={s} H={h} D={d}")
+    q = synth.normal_f16(seeds[6], (s, h * d))
+    k = synth.normal_f16(seeds[7], (s, h * d))
+    v = synth.normal_f16(seeds[8], (s, h * d))
+    got = attn_dev(rk, q, k, v, h, h, d, d ** -0.5, mode=0)
+    check_rows(orc, got, q, k, v, h, h, d, d ** -0.5, _slices(s, 32))
+
+
+def test_config5_gqa_32_4_full(rk, orc):
+    c = synth.MOE
+    s, h, kv, d = c["s"], c["attn_heads"], c["attn_kv"], c["attn_d"]
+    seeds = synth.SEEDS["moe"]
+    note(f"causal GQA S={s} H={h} KV={kv} D={d}")
+    q = synth.normal_f16(seeds[6], (s, h * d))
+    k = synth.normal_f16(seeds[7], (s, kv * d))
+    v = synth.normal_f16(seeds[8], (s, kv * d))
+    got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=1)
+    check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(s, 64))
+
+
+@pytest.mark.parametrize("d", [64, 72, 80, 96, 112, 128])
+@pytest.mark.parametrize("h,kv", [(4, 4), (8, 2), (16, 2), (6, 3)])
+def test_head_dims_and_groups(rk, orc, d, h, kv):
+    note(f"attention d={d} h={h} kv={kv}")
+    r = np.random.default_rng(d * 31 + h)
+    n_q, n_kv = 150, 150
+    q = r.standard_normal((n_q, h * d)).astype(np.float16)
+    k = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    v = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    for mode in (0, 1):
+        got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=mode)
+        check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, mode=mode))
+
+
+@pytest.mark.parametrize("mode,window,n_q,n_kv,q0,k0", [
+    (2, 17, 200, 200, 0, 0),      # band
+    (3, 33, 200, 200, 0, 0),      # causal sliding window
+    (1, -1, 64, 300, 236, 0),     # causal query chunk against its key prefix
+    (3, 40, 64, 104, 400, 360),   # causal window chunk, keys start at q0 - window
+    (2, 20, 50, 90, 300, 280),    # band chunk
+    (1, -1, 40, 70, 10, 30),      # keys above the first rows: emptied rows average V
+    (2, 5, 30, 40, 100, 0),       # band entirely outside the keys: every row emptied
+    (0, -1, 1, 1, 0, 0),          # one query, one key
+    (1, -1, 1, 129, 128, 0),      # one query, ragged key count
+])
+def test_mask_modes_and_block_offsets(rk, orc, mode, window, n_q, n_kv, q0, k0):
+    note(f"mask mode={mode} w={window} n_q={n_q} n_kv={n_kv} q0={q0} k0={k0}")
+    r = np.random.default_rng(n_q * 7 + n_kv)
+    h, kv, d = 8, 2, 128
+    q = r.standard_normal((n_q, h * d)).astype(np.float16)
+    k = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    v = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    got = attn_dev(rk, q, k, v, h, kv, d, 0.0884, mode=mode, window=window, q0=q0, k0=k0)
+    ref = orc.attention_ref(q, k, v, h, kv, d, 0.0884, 0.0, mode, window, q0, k0)
+    check(orc, got, ref)
+
+
+def test_softcap(rk, orc):
+    note("softcap 20")
+    r = np.random.default_rng(99)
+    h, kv, d, n = 8, 4, 64, 190
+    q = (r.standard_normal((n, h * d)) * 3).astype(np.float16)
+    k = (r.standard_normal((n, kv * d)) * 3).astype(np.float16)
+    v = r.standard_normal((n, kv * d)).astype(np.float16)
+    got = attn_dev(rk, q, k, v, h, kv, d, 0.125, softcap=20.0, mode=1)
+    check(orc, got, orc.attention_ref(q, k, v, h, kv, d, 0.125, 20.0, 1))
+
+
+def test_host_api_and_head_major_layout(rk, orc):
+    note("rk_attention host f32 + rk_flash_attn_f16 head-major")
+    r = np.random.default_rng(5)
+    h, kv, d, n = 8, 2, 128, 97
+    q = r.standard_normal((1, n, h * d)).astype(np.float32)
+    k = r.standard_normal((1, n, kv * d)).astype(np.float32)
+    v = r.standard_normal((1, n, kv * d)).astype(np.float32)
+    out = rk.attention(q, k, v, h, kv, d, d ** -0.5, None, True)
+    assert out.shape == (1, n, h * d)
+    q16, k16, v16 = (orc.f32_to_f16(a[0]) for a in (q, k, v))
+    ref = orc.attention_ref(q16, k16, v16, h, kv, d, d ** -0.5, 0.0, 1)
+    check(orc, out[0], ref)
+    # head-major: q [H][n][D], k [KV][n][D], v [KV][D][n]
+    qh = q16.view(np.float16).reshape(n, h, d).transpose(1, 0, 2)
+    kh = k16.view(np.float16).reshape(n, kv, d).transpose(1, 0, 2)
+    vh = v16.view(np.float16).reshape(n, kv, d).transpose(1, 2, 0)
+    oh = rk.flash_attn_f16(qh, kh, vh, n, n, d, h, kv, d ** -0.5, 0.0, 1)
+    assert (oh.transpose(1, 0, 2).reshape(n, h * d).astype(np.float32) == out[0]).all()
+    # window < 0 in the window modes means no window (ext.rs:99-126)
+    a = rk.attention_window(q, k, v, h, kv, d, d ** -0.5, None, -1)
+    b = rk.attention(q, k, v, h, kv, d, d ** -0.5, None, False)
+    assert (a == b).all()
+    a = rk.attention_causal_window(q, k, v, h, kv, d, d ** -0.5, None, -1)
+    assert (a == out).all()
+
+
+def test_attention_rejects_bad_shapes(rk):
+    note("attention errors")
+    lib = rk.lib()
+    assert lib.rk_attention(None, None, None, 4, 4, 6, 4, 128, 1.0, 0.0, 0, -1, 0, 0, None) == rk.RK_E_SHAPE
+    assert lib.rk_attention(None, None, None, 4, 4, 4, 4, 40, 1.0, 0.0, 0, -1, 0, 0, None) == rk.RK_E_UNSUPPORTED

@@ -1,0 +1,136 @@
+"""GPU parity of the fp16 GEMM (K1) against the oracle, through the C ABI.
+
+Gate (fp16 outputs): cosine >= 0.9999 and max relative error <= 1e-2 with the
+floor max_i |g - r| / max(|r_i|, 1e-2·max|r|); integer-valued inputs must match
+exactly."""
+import sys
+
+import numpy as np
+import pytest
+
+from burn_rocket import synth
+
+pytestmark = pytest.mark.gpu
+COS_MIN, REL_MAX = 0.9999, 1e-2
+
+
+def note(msg):
+    print(f"[case] {msg}", file=sys.stderr, flush=True)
+
+
+def run_f16(rk, w_id, a16, n):
+    m, k = a16.shape
+    da = rk.DeviceBuffer.from_array(a16.view(np.uint16))
+    dc = rk.DeviceBuffer(m * n * 2)
+    rc = rk.lib().rk_matmul_f16_dev(int(w_id), da.ptr, m, k, dc.ptr, None)
+    assert rc == 0, rk.lib().rk_last_error()
+    rk.synchronize()
+    out = dc.download((m, n), np.uint16).view(np.float16)
+    da.free()
+    dc.free()
+    return out
+
+
+def check(orc, got, ref):
+    g = got.astype(np.float32)
+    assert np.isfinite(g).all()
+    cos, rel = orc.cosine(g, ref), orc.max_rel(g, ref)
+    assert cos >= COS_MIN and rel <= REL_MAX, (cos, rel)
+    return cos, rel
+
+
+def test_gemm_f16_config1_full(rk, orc):
+    c = synth.GEMM_F16
+    s1, s2 = synth.SEEDS["gemm_f16"]
+    note(f"fp16 GEMM {c} seeds {s1},{s2}")
+    a = synth.normal_f16(s1, (c["m"], c["k"]))
+    b = synth.normal_f16(s2, (c["n"], c["k"]), 0.02)
+    wid = rk.pack(b)
+    got = run_f16(rk, wid, a, c["n"])
+    ref = orc.gemm_f16(a, b)
+    check(orc, got, ref)
+    ref64 = orc.gemm_f16_f64(a[:64], b)
+    check(orc, got[:64], ref64)
+    # fp16 rounding of an f32-accumulated result: within 1 ulp of f16(ref)
+    r16 = ref.astype(np.float16).astype(np.float32)
+    ulp = np.abs(np.spacing(r16.astype(np.float16)).astype(np.float32))
+    assert (np.abs(got.astype(np.float32) - r16) <= 2 * ulp + 1e-6).mean() > 0.999
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 8, 1), (7, 24, 5), (65, 136, 97), (130, 4304, 200), (300, 1152, 3456),
+                                   (513, 1024, 3072), (64, 2048, 96), (129, 64, 130)])
+def test_gemm_f16_shapes(rk, orc, m, k, n):
+    note(f"fp16 GEMM m={m} k={k} n={n}")
+    r = np.random.default_rng(m * 1000 + n)
+    a = r.standard_normal((m, k)).astype(np.float16)
+    b = (r.standard_normal((n, k)) * 0.05).astype(np.float16)
+    got = run_f16(rk, rk.pack(b), a, n)
+    check(orc, got, orc.gemm_f16(a, b))
+
+
+@pytest.mark.parametrize("m,k,n", [(96, 64, 80), (256, 1024, 384), (37, 4304, 40)])
+def test_gemm_f16_integer_inputs_are_exact(rk, orc, m, k, n):
+    note(f"fp16 GEMM exact m={m} k={k} n={n}")
+    r = np.random.default_rng(7 + m)
+    a = r.integers(-3, 4, (m, k)).astype(np.float16)
+    b = r.integers(-3, 4, (n, k)).astype(np.float16)
+    got = run_f16(rk, rk.pack(b), a, n).astype(np.float32)
+    want = (a.astype(np.int64) @ b.astype(np.int64).T).astype(np.float32)
+    assert (got == want.astype(np.float16).astype(np.float32)).all()
+
+
+def test_vision_layer_gemms_full_size(rk, orc):
+    c = synth.VISION
+    s = c["s"]
+    seeds = synth.SEEDS["vision"]
+    x = synth.normal_f16(seeds[0], (s, c["hidden"]))
+    shapes = [("qkv", 3 * c["hidden"], c["hidden"]), ("out", c["hidden"], c["hidden"]),
+              ("fc1", c["mlp"], c["hidden"]), ("fc2", c["hidden"], c["mlp"])]
+    rows = np.r_[0:64, s // 2:s // 2 + 64, s - 64:s]
+    for i, (name, n, k) in enumerate(shapes):
+        note(f"vision {name} m={s} k={k} n={n}")
+        w = synth.normal_f16(seeds[1 + i], (n, k), 0.02)
+        a = x if k == c["hidden"] else synth.normal_f16(seeds[5], (s, k))
+        got = run_f16(rk, rk.pack(w), a, n)
+        check(orc, got[rows], orc.gemm_f16(a[rows], w))
+
+
+def test_host_matmul_api_f32_in_out(rk, orc):
+    note("rk_matmul f16 weight, host f32 in/out")
+    r = np.random.default_rng(11)
+    x = r.standard_normal((2, 50, 256)).astype(np.float32)
+    w = (r.standard_normal((96, 256)) * 0.05).astype(np.float32)
+    wid = rk.pack(w)
+    y = rk.matmul(x, wid)
+    assert y.shape == (2, 50, 96) and y.dtype == np.float32
+    ref = orc.gemm_f16(orc.f32_to_f16(x.reshape(100, 256)), orc.f32_to_f16(w))
+    check(orc, y.reshape(100, 96), ref)
+    # the result is an fp16 value widened to f32 (matmul_f16 reads back fp16)
+    assert (y.astype(np.float16).astype(np.float32) == y).all()
+
+
+def test_pack3_concatenates_along_n(rk):
+    note("pack3 segmentation")
+    r = np.random.default_rng(12)
+    x = r.standard_normal((33, 128)).astype(np.float32)
+    parts = [(r.standard_normal((n, 128)) * 0.1).astype(np.float32) for n in (64, 32, 40)]
+    y3 = rk.matmul(x, rk.pack3(*parts))
+    ys = np.concatenate([rk.matmul(x, rk.pack(p)) for p in parts], axis=1)
+    assert (y3 == ys).all()
+    y2 = rk.matmul(x, rk.pack2(parts[0], parts[1]))
+    assert (y2 == ys[:, :96]).all()
+
+
+def test_shape_errors_are_reported(rk):
+    note("error paths")
+    wid = rk.pack(np.ones((16, 64), np.float32))
+    with pytest.raises(AssertionError):
+        rk.matmul(np.ones((4, 32), np.float32), wid)
+    with pytest.raises(rk.RocketError) as e:
+        rk.pack(np.ones((16, 12), np.float32))  # K % 8 != 0
+    assert e.value.rc == rk.RK_E_SHAPE
+    lib = rk.lib()
+    assert lib.rk_matmul(987654321, None, 1, 64, None) == rk.RK_E_RANGE
+    assert b"not packed" in lib.rk_last_error()
+    ms = rk.mem_stats()
+    assert ms.n_weights >= 1 and ms.weights_bytes >= 16 * 64 * 2

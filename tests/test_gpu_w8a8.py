@@ -1,0 +1,199 @@
+"""GPU parity of the W8A8 / Q8_0 GEMM (K2) against the oracle, through the C ABI.
+
+Integer work is bit-exact: the activation quantizer's codes and scales, the raw
+int32 product over the full K and the per-32-block int32 partials. Scaled f32
+outputs follow the reference formula up to f32 rounding order and are held to
+cosine >= 0.9999, max relative error <= 1e-2 (the fp16-output gate)."""
+import sys
+
+import numpy as np
+import pytest
+
+from burn_rocket import synth
+
+pytestmark = pytest.mark.gpu
+COS_MIN, REL_MAX = 0.9999, 1e-2
+
+
+def note(msg):
+    print(f"[case] {msg}", file=sys.stderr, flush=True)
+
+
+def _lib(rk):
+    return rk.lib()
+
+
+def dev(rk, a):
+    return rk.DeviceBuffer.from_array(a)
+
+
+def quantize_dev(rk, x, group):
+    m, k = x.shape
+    dx = dev(rk, x)
+    dq = rk.DeviceBuffer(m * k)
+    ds = rk.DeviceBuffer(m * (k // group) * 4)
+    rc = _lib(rk).rk_quantize_rows_dev(dx.ptr, m, k, group, dq.ptr, ds.ptr, None)
+    assert rc == 0, _lib(rk).rk_last_error()
+    rk.synchronize()
+    return dq, ds
+
+
+def raw_dev(rk, wid, aq):
+    m, k = aq.shape
+    n = rk.weight_info(wid)[1]
+    da = dev(rk, aq)
+    dc = rk.DeviceBuffer(m * n * 4)
+    assert _lib(rk).rk_matmul_i8_raw_dev(int(wid), da.ptr, m, k, dc.ptr, None) == 0, _lib(rk).rk_last_error()
+    rk.synchronize()
+    return dc.download((m, n), np.int32)
+
+
+def w8a8_dev(rk, wid, dq, ds, a_group, m, k, f16out=False):
+    n = rk.weight_info(wid)[1]
+    dc = rk.DeviceBuffer(m * n * (2 if f16out else 4))
+    fn = _lib(rk).rk_matmul_w8a8_f16out_dev if f16out else _lib(rk).rk_matmul_w8a8_dev
+    assert fn(int(wid), dq.ptr, ds.ptr, a_group, m, k, dc.ptr, None) == 0, _lib(rk).rk_last_error()
+    rk.synchronize()
+    if f16out:
+        return dc.download((m, n), np.uint16).view(np.float16).astype(np.float32)
+    return dc.download((m, n), np.float32)
+
+
+def check(orc, got, ref):
+    assert np.isfinite(got).all()
+    cos, rel = orc.cosine(got, ref), orc.max_rel(got, ref)
+    assert cos >= COS_MIN and rel <= REL_MAX, (cos, rel)
+
+
+@pytest.fixture(scope="module")
+def config2(rk, orc):
+    c = synth.W8A8
+    s1, s2, s3 = synth.SEEDS["w8a8"]
+    x_up = synth.normal_f32(s1, (c["m"], c["hidden"]))
+    x_dn = synth.normal_f32(s1 + 1000, (c["m"], c["inter"]))
+    w_up = synth.normal_f32(s2, (c["inter"], c["hidden"]), 0.02)
+    w_dn = synth.normal_f32(s3, (c["hidden"], c["inter"]), 0.02)
+    out = {}
+    for name, x, w in (("up", x_up, w_up), ("down", x_dn, w_dn)):
+        wq, wd = orc.q8_0_quantize(w)
+        blocks = orc.q8_0_blocks(wq, wd)
+        wid = rk.pack_q8_0(blocks, *w.shape)
+        out[name] = dict(x=x, wq=wq, ws=wd.view(np.float16).astype(np.float32), wid=wid)
+    return out
+
+
+def test_activation_quantizer_is_bit_exact(rk, orc, config2):
+    for name in ("up", "down"):
+        x = config2[name]["x"]
+        m, k = x.shape
+        for group in (k, 32, 128):
+            note(f"quantize_rows {name} m={m} k={k} group={group}")
+            dq, ds = quantize_dev(rk, x, group)
+            q, s = orc.quantize_rows(x, group)
+            assert (dq.download((m, k), np.int8) == q).all()
+            assert (ds.download((m, k // group), np.float32).view(np.uint32) == s.view(np.uint32)).all()
+
+
+def test_raw_int32_full_config2_is_bit_exact(rk, orc, config2):
+    for name in ("up", "down"):
+        d = config2[name]
+        m, k = d["x"].shape
+        note(f"raw int32 {name} m={m} k={k} n={d['wq'].shape[0]}")
+        aq, _ = orc.quantize_rows(d["x"], k)
+        got = raw_dev(rk, d["wid"], aq)
+        want = orc.matmul_i8_raw(aq, d["wq"])
+        assert (got.astype(np.int64) == want).all()
+
+
+def test_block_partials_are_bit_exact(rk, orc, config2):
+    d = config2["down"]
+    rows = 192
+    aq, _ = orc.quantize_rows(d["x"][:rows], d["x"].shape[1])
+    m, k = aq.shape
+    n = d["wq"].shape[0]
+    note(f"int32 block partials m={m} k={k} n={n}")
+    da = dev(rk, aq)
+    dp = rk.DeviceBuffer(m * n * (k // 32) * 4)
+    assert _lib(rk).rk_matmul_i8_partials_dev(int(d["wid"]), da.ptr, m, k, dp.ptr, None) == 0
+    rk.synchronize()
+    got = dp.download((m, n, k // 32), np.int32)
+    assert (got == orc.i8_block_partials(aq, d["wq"])).all()
+
+
+@pytest.mark.parametrize("f16out", [False, True])
+def test_per_token_w8a8_full_config2(rk, orc, config2, f16out):
+    for name in ("up", "down"):
+        d = config2[name]
+        m, k = d["x"].shape
+        note(f"W8A8 per-token {name} m={m} k={k} f16out={f16out}")
+        dq, ds = quantize_dev(rk, d["x"], k)
+        got = w8a8_dev(rk, d["wid"], dq, ds, k, m, k, f16out)
+        aq, a_s = orc.quantize_rows(d["x"], k)
+        ref = orc.emu_matmul_gw(aq, a_s, k, d["wq"], d["ws"], 32)
+        check(orc, got, ref)
+        if not f16out:
+            # only f32 rounding order differs from the reference formula
+            assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_group_wise_host_matmul_matches_matmul_gw(rk, orc, group):
+    note(f"rk_matmul pack_i8 group={group}")
+    r = np.random.default_rng(group)
+    m, k, n = 77, 512, 160
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wid = rk.pack_i8(w, group)
+    y = rk.matmul(x, wid)
+    wq, ws = orc.quantize_rows(w, group)
+    aq, a_s = orc.quantize_rows(x, group)
+    ref = orc.emu_matmul_gw(aq, a_s, group, wq, ws, group)
+    check(orc, y, ref)
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    # the resident codes are the oracle's codes: the raw product is exact
+    assert (raw_dev(rk, wid, aq).astype(np.int64) == orc.matmul_i8_raw(aq, wq)).all()
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 32, 1), (5, 160, 40), (130, 4096, 96), (64, 96, 33)])
+def test_w8a8_edge_shapes(rk, orc, m, k, n):
+    note(f"W8A8 edge m={m} k={k} n={n}")
+    r = np.random.default_rng(m + k + n)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wq, wd = orc.q8_0_quantize(w)
+    wid = rk.pack_q8_0(orc.q8_0_blocks(wq, wd), n, k)
+    aq, a_s = orc.quantize_rows(x, k)
+    assert (raw_dev(rk, wid, aq).astype(np.int64) == orc.matmul_i8_raw(aq, wq)).all()
+    dq, ds = quantize_dev(rk, x, k)
+    got = w8a8_dev(rk, wid, dq, ds, k, m, k)
+    ref = orc.emu_matmul_gw(aq, a_s, k, wq, wd.view(np.float16).astype(np.float32), 32)
+    check(orc, got, ref)
+
+
+@pytest.mark.parametrize("in_scale,out_scale", [(0.02, 0.0), (0.0, 0.0), (0.02, 0.05)])
+def test_qat_matmul_is_bit_exact(rk, orc, in_scale, out_scale):
+    note(f"QAT in_scale={in_scale} out_scale={out_scale}")
+    r = np.random.default_rng(5)
+    m, k, n = 45, 256, 64
+    x = r.standard_normal((m, k)).astype(np.float32)
+    codes = r.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = (r.uniform(0.5, 1.5, n) * 1e-3).astype(np.float32)
+    wid = rk.pack_qat(codes, ws, n, k, in_scale, out_scale)
+    y = rk.matmul(x, wid)
+    q, rs = orc.quantize_static(x, in_scale)
+    ref = orc.qat_epilogue(orc.matmul_i8_raw(q, codes), rs, ws, out_scale)
+    assert (y.view(np.uint32) == ref.view(np.uint32)).all()
+
+
+def test_rewrite_replaces_the_resident_codes(rk, orc):
+    note("rewrite_i8")
+    r = np.random.default_rng(9)
+    m, k, n = 16, 128, 64
+    w1 = r.integers(-127, 128, (n, k), dtype=np.int8)
+    w2 = r.integers(-127, 128, (n, k), dtype=np.int8)
+    s = np.ones((n, k // 32), np.float32)
+    wid = rk.pack_i8_codes(w1, s, 32)
+    aq = r.integers(-127, 128, (m, k), dtype=np.int8)
+    assert (raw_dev(rk, wid, aq) == orc.matmul_i8_raw(aq, w1)).all()
+    rk.rewrite_i8(wid, w2, s)
+    assert (raw_dev(rk, wid, aq) == orc.matmul_i8_raw(aq, w2)).all()

@@ -1,0 +1,379 @@
+"""CPU tests that pin the oracle before it is trusted as the parity reference.
+
+Every check here is independent of the oracle's own formula: the reference's
+known-answer tests (cited), closed forms, exact integer arithmetic in numpy,
+and brute force on tiny inputs.
+"""
+import numpy as np
+import pytest
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------------ fp16 ----
+def test_f16_round_trip_is_exact_for_every_f16(orc):
+    h = np.arange(1 << 16, dtype=np.uint16)
+    f = orc.f16_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    same = (f.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(f) & np.isnan(ref))
+    assert same.all()
+    finite = ~np.isnan(ref)
+    back = orc.f32_to_f16(f[finite])
+    assert (back == h[finite]).all()
+
+
+def test_f32_to_f16_is_round_to_nearest_even(orc):
+    # numpy's float32 → float16 cast is IEEE RNE; compare on random values,
+    # exact ties, subnormals, overflow and the largest finite boundaries.
+    r = _rng(1)
+    x = np.concatenate([
+        r.standard_normal(200000).astype(np.float32) * np.float32(10.0) ** r.integers(-9, 6, 200000),
+        np.array([65504.0, 65519.0, 65520.0, 1e6, -1e6, 5.96e-8, 2.98e-8, 2.99e-8, 1e-10, 0.0, -0.0],
+                 dtype=np.float32),
+    ]).astype(np.float32)
+    # exact halfway points between consecutive f16 values
+    h = np.arange(0x0001, 0x7bff, 7, dtype=np.uint16).view(np.float16).astype(np.float32)
+    h2 = (np.arange(0x0002, 0x7c00, 7, dtype=np.uint16)).view(np.float16).astype(np.float32)
+    mid = ((h.astype(np.float64) + h2.astype(np.float64)) / 2).astype(np.float32)
+    x = np.concatenate([x, mid, -mid])
+    got = orc.f32_to_f16(x)
+    ref = x.astype(np.float16).view(np.uint16)
+    assert (got == ref).all()
+
+
+# ------------------------------------------------------------ quantizers ----
+def test_quantizer_roundtrip_bound_group_max_and_zero_group(orc):
+    # crates/burn-rocket/src/host.rs:189-222
+    k, group = 128, 32
+    r = _rng(2)
+    x = r.uniform(-1, 1, k).astype(np.float32)
+    x[70] = 9.5  # outlier in group 2
+    q, s = orc.quantize_rows(x[None, :], group)
+    q, s = q[0], s[0]
+    for g in range(k // group):
+        seg = x[g * group:(g + 1) * group]
+        amax = np.abs(seg).max()
+        assert abs(s[g] - amax / 127) <= 1e-9 * max(amax, 1)
+        deq = q[g * group:(g + 1) * group].astype(np.float32) * s[g]
+        assert (np.abs(seg - deq) <= s[g] * 0.5 + 1e-6).all()
+    assert q[70] == 127
+    assert s[2] > s[1]
+    zq, zs = orc.quantize_rows(np.zeros((1, 32), np.float32), 32)
+    assert zs[0, 0] > 0 and np.isfinite(zs[0, 0]) and (zq == 0).all()
+
+
+def test_quantizer_is_round_half_away_of_x_times_inverse(orc):
+    # src/clef/int8.rs:190-210: x·(1/s) and x/s differ only at exact .5 boundaries.
+    r = _rng(3)
+    x = (r.uniform(-1, 1, (4, 256)) * 5).astype(np.float32)
+    q, s = orc.quantize_rows(x, 128)
+    for row in range(4):
+        for g in range(2):
+            seg = x[row, g * 128:(g + 1) * 128]
+            want = np.clip(np.round(seg.astype(np.float64) / s[row, g]), -127, 127)
+            assert np.abs(q[row, g * 128:(g + 1) * 128] - want).max() <= 1
+            assert (np.abs(q[row, g * 128:(g + 1) * 128]) == 127).any()
+    # Half-away-from-zero, not ties-to-even: 2.5 → 3 and -2.5 → -3 at scale 1.
+    x = np.zeros((1, 32), np.float32)
+    x[0, :4] = [127.0, 2.5, -2.5, 0.5]
+    q, s = orc.quantize_rows(x, 32)
+    assert s[0, 0] == np.float32(1.0)
+    assert list(q[0, :4]) == [127, 3, -3, 1]
+
+
+def test_q8_0_block_dequant_kat(orc):
+    # src/util/gguf.rs:250-262: scale 0.5, codes ff/00/01 → -0.5/0/0.5.
+    raw = np.zeros(34, np.uint8)
+    raw[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    raw[2], raw[3], raw[4] = 0xFF, 0x00, 0x01
+    v = orc.q8_0_dequant(raw, 32)
+    assert v[0] == -0.5 and v[1] == 0.0 and v[2] == 0.5
+
+
+def test_q8_0_quantizes_against_the_stored_f16_scale(orc):
+    # crates/rocket-npu/src/bin/q8_bench.rs:200-220
+    r = _rng(4)
+    w = (r.standard_normal((8, 96)) * 0.02).astype(np.float32)
+    q, d = orc.q8_0_quantize(w)
+    dval = d.view(np.float16).astype(np.float32)
+    for row in range(8):
+        for b in range(3):
+            seg = w[row, b * 32:(b + 1) * 32]
+            assert d[row, b] == np.float16(np.abs(seg).max() / np.float32(127)).view(np.uint16)
+            inv = np.float32(1) / dval[row, b]
+            want = np.clip(np.trunc(seg * inv + np.copysign(0.5, seg * inv)), -127, 127)
+            assert (q[row, b * 32:(b + 1) * 32] == want).all()
+    blocks = orc.q8_0_blocks(q, d)
+    deq = orc.q8_0_dequant(blocks, w.size).reshape(w.shape)
+    assert np.allclose(deq, q.astype(np.float32) * np.repeat(dval, 32, axis=1), rtol=0, atol=0)
+    assert (np.abs(deq - w) <= np.repeat(dval, 32, axis=1) * 0.5 + 1e-7).all()
+
+
+def test_static_code_rounds_ties_to_even_and_saturates(orc):
+    # crates/burn-rocket/src/ext.rs:2257-2272
+    x = np.array([[0.5, 1.5, 2.5, -0.5, -1.5, 1000.0, -1000.0]], np.float32)
+    q, rs = orc.quantize_static(x, 1.0)
+    assert list(q[0]) == [0, 2, 2, 0, -2, 127, -128] and rs[0] == 1.0
+    scale = np.float32(0.0173)
+    codes = np.array([-128, -77, -1, 0, 3, 64, 127], np.float32)
+    q, _ = orc.quantize_static((codes * scale)[None, :], float(scale))
+    assert list(q[0]) == list(codes.astype(int))
+    # in_scale == 0 → per-row dynamic max(amax/127, 1e-12)
+    x = np.array([[1.0, -2.54, 0.0]], np.float32)
+    q, rs = orc.quantize_static(x, 0.0)
+    assert rs[0] == np.float32(np.float32(2.54) / np.float32(127))
+
+
+# ------------------------------------------------------- int8 products ----
+def test_raw_int8_product_is_exact(orc):
+    r = _rng(5)
+    a = r.integers(-127, 128, (37, 160), dtype=np.int8)
+    w = r.integers(-127, 128, (23, 160), dtype=np.int8)
+    got = orc.matmul_i8_raw(a, w)
+    assert (got == a.astype(np.int64) @ w.astype(np.int64).T).all()
+    p = orc.i8_block_partials(a, w)
+    ref = np.einsum("mbk,nbk->mnb", a.reshape(37, 5, 32).astype(np.int64), w.reshape(23, 5, 32).astype(np.int64))
+    assert (p == ref).all()
+    assert (p.sum(axis=2) == got).all()
+
+
+def test_emulated_gw_matmul_has_an_exact_integer_part(orc):
+    # src/clef/int8.rs:212-240: unit scales give the exact int64 dot.
+    r = _rng(6)
+    m, k, n, g = 7, 256, 5, 128
+    aq = r.integers(-127, 128, (m, k), dtype=np.int8)
+    wq = r.integers(-127, 128, (n, k), dtype=np.int8)
+    got = orc.emu_matmul_gw(aq, np.ones((m, k // g), np.float32), g, wq, np.ones((n, k // g), np.float32), g)
+    assert (got.astype(np.int64) == aq.astype(np.int64) @ wq.astype(np.int64).T).all()
+    assert (orc.emu_matmul_gw(aq, np.ones((m, k // g), np.float32), g, wq, np.ones((n, k // g), np.float32), g,
+                              threads=1) == got).all()
+
+
+def test_emulated_gw_matmul_applies_scales_per_group(orc):
+    # host.rs:225-276: int8 codes + per-row/per-group scales ≈ the f32 product.
+    r = _rng(7)
+    m, k, n, g = 8, 64, 8, 32
+    a = (r.uniform(-1, 1, (m, k)) * 2).astype(np.float32)
+    b = r.uniform(-1, 1, (n, k)).astype(np.float32)
+    aq, a_s = orc.quantize_rows(a, g)
+    bq, b_s = orc.quantize_rows(b, g)
+    got = orc.emu_matmul_gw(aq, a_s, g, bq, b_s, g)
+    want = a @ b.T
+    assert (np.abs(got - want) <= 0.1 * np.maximum(np.abs(want), 1)).all()
+    # Exact formula in f64 from the integer partials: a transposed or shifted
+    # scale layout would be off by far more than f32 rounding.
+    p = orc.i8_block_partials(aq, bq).astype(np.float64)
+    exact = (p * (a_s[:, None, :].astype(np.float64) * b_s[None, :, :])).sum(axis=2)
+    assert np.abs(got - exact).max() <= 1e-5 * np.abs(exact).max()
+
+
+def test_per_token_activation_scale(orc):
+    r = _rng(8)
+    m, k, n = 16, 256, 24
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    xq, xs = orc.quantize_rows(x, k)
+    wq, wd = orc.q8_0_quantize(w)
+    ws = wd.view(np.float16).astype(np.float32)
+    got = orc.emu_matmul_gw(xq, xs, k, wq, ws, 32)
+    p = orc.i8_block_partials(xq, wq).astype(np.float64)
+    exact = xs.astype(np.float64)[:, :, None][:, 0, :] * (p * ws[None, :, :]).sum(axis=2)
+    assert np.abs(got - exact).max() <= 1e-5 * np.abs(exact).max()
+    assert orc.cosine(got, x @ w.T) > 0.999
+
+
+def test_qat_epilogue(orc):
+    acc = np.array([[100, -200], [0, 7]], np.int64)
+    rs = np.array([0.5, 2.0], np.float32)
+    ws = np.array([0.1, 0.01], np.float32)
+    y = orc.qat_epilogue(acc, rs, ws, 0.0)
+    assert np.allclose(y, [[5.0, -1.0], [0.0, 0.14]], rtol=1e-6)
+    y = orc.qat_epilogue(acc, rs, ws, 0.5)  # rounded to the 0.5 grid
+    assert np.allclose(y, [[5.0, -1.0], [0.0, 0.0]])
+
+
+# ------------------------------------------------------------- fp16 GEMM ----
+def test_gemm_f16_closed_forms(orc):
+    r = _rng(9)
+    # identity: C = A exactly
+    a = r.standard_normal((16, 64)).astype(np.float16)
+    eye = np.eye(64, dtype=np.float16)
+    assert (orc.gemm_f16(a, eye) == a.astype(np.float32)).all()
+    # small integers: every partial sum is exact in f32
+    a = r.integers(-8, 9, (9, 48)).astype(np.float16)
+    b = r.integers(-8, 9, (11, 48)).astype(np.float16)
+    assert (orc.gemm_f16(a, b) == (a.astype(np.int64) @ b.astype(np.int64).T)).all()
+    # random: f32 accumulation within a few ulp-multiples of the f64 product
+    a = r.standard_normal((33, 1024)).astype(np.float16)
+    b = (r.standard_normal((17, 1024)) * 0.02).astype(np.float16)
+    ref = a.astype(np.float64) @ b.astype(np.float64).T
+    got = orc.gemm_f16(a, b)
+    assert np.abs(got - ref).max() < 1e-4 * np.abs(ref).max()
+    assert np.allclose(orc.gemm_f16_f64(a, b), ref, rtol=1e-12, atol=1e-12)
+
+
+# ----------------------------------------------------------------- masks ----
+def _keep_grid(orc, mode, w, n_q, n_kv, q0, k0):
+    return np.array([[orc.mask_keep(mode, w, q0 + i, k0 + j) for j in range(n_kv)] for i in range(n_q)])
+
+
+def test_mask_predicates_match_the_reference_builders(orc):
+    # crates/burn-rocket/src/masks.rs:124-301
+    t, j = np.meshgrid(np.arange(8), np.arange(8), indexing="ij")
+    assert (_keep_grid(orc, 1, -1, 8, 8, 0, 0) == (j <= t)).all()
+    assert (_keep_grid(orc, 2, 3, 8, 8, 0, 0) == (np.abs(t - j) <= 3)).all()
+    assert (_keep_grid(orc, 3, 3, 8, 8, 0, 0) == ((j <= t) & (t - j < 3))).all()
+    # block forms with offsets
+    i, jj = np.meshgrid(np.arange(5), np.arange(7), indexing="ij")
+    assert (_keep_grid(orc, 2, 3, 5, 7, 10, 8) == (np.abs((10 + i) - (8 + jj)) <= 3)).all()
+    i, jj = np.meshgrid(np.arange(4), np.arange(10), indexing="ij")
+    assert (_keep_grid(orc, 1, -1, 4, 10, 8, 4) == (4 + jj <= 8 + i)).all()
+    i, jj = np.meshgrid(np.arange(5), np.arange(12), indexing="ij")
+    k_ = _keep_grid(orc, 3, 4, 5, 12, 16, 8)
+    assert (k_ == ((8 + jj <= 16 + i) & ((16 + i) - (8 + jj) < 4))).all()
+    # keys above the chunk: fully masked; one-row overlap
+    assert not _keep_grid(orc, 1, -1, 4, 8, 20, 24).any()
+    # ragged 30k tail: visible run of row i is exactly q0 + i + 1
+    n_kv, q0 = 29960, 29952
+    for i in range(8):
+        vis = sum(orc.mask_keep(1, -1, q0 + i, jj) for jj in range(q0 - 2, n_kv))
+        assert vis == min(q0 + i + 1, n_kv) - (q0 - 2)
+    # window 1 causal: only the diagonal
+    assert (_keep_grid(orc, 3, 1, 6, 6, 0, 0) == np.eye(6, dtype=bool)).all()
+
+
+# ------------------------------------------------------------- attention ----
+def _qkv(r, n_q, n_kv, h, kv, d, sig=1.0):
+    q = (r.standard_normal((n_q, h * d)) * sig).astype(np.float16)
+    k = (r.standard_normal((n_kv, kv * d)) * sig).astype(np.float16)
+    v = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("fn", ["attention_ref", "attention_flex"])
+def test_attention_single_visible_key_returns_that_value_row(orc, fn):
+    # attn/oneshot.rs:763-805: a one-hot softmax returns the key's value exactly.
+    r = _rng(10)
+    n, h, kv, d = 6, 4, 2, 32
+    q, k, v = _qkv(r, n, n, h, kv, d)
+    out = getattr(orc, fn)(q, k, v, h, kv, d, 0.125, mode=3, window=1)  # t - 1 < j <= t
+    for hh in range(h):
+        g = hh // (h // kv)
+        assert (out[:, hh * d:(hh + 1) * d] == v[:, g * d:(g + 1) * d].astype(np.float32)).all()
+
+
+@pytest.mark.parametrize("fn", ["attention_ref", "attention_flex"])
+def test_attention_closed_forms(orc, fn):
+    r = _rng(11)
+    n, h, kv, d = 9, 4, 2, 16
+    q, k, v = _qkv(r, n, n, h, kv, d)
+    f = getattr(orc, fn)
+    # zero queries: uniform average of the visible prefix (causal) per kv head
+    out = f(np.zeros_like(q), k, v, h, kv, d, 0.3, mode=1)
+    vf = v.astype(np.float64)
+    for hh in range(h):
+        g = hh // 2
+        cum = np.cumsum(vf[:, g * d:(g + 1) * d], axis=0) / np.arange(1, n + 1)[:, None]
+        assert np.allclose(out[:, hh * d:(hh + 1) * d], cum, rtol=1e-5, atol=1e-5)
+    # constant V: output is that constant whatever the scores
+    vc = np.full_like(v, 0.75)
+    out = f(q, k, vc, h, kv, d, 0.3, mode=0)
+    assert np.allclose(out, 0.75, rtol=1e-6)
+    # emptied rows (keys all above the chunk) average V over every key
+    # (attn/oneshot.rs:909-944)
+    out = f(q[:3], k, v, h, kv, d, 0.3, mode=1, q0=0, k0=5)
+    for hh in range(h):
+        g = hh // 2
+        assert np.allclose(out[:, hh * d:(hh + 1) * d], vf[:, g * d:(g + 1) * d].mean(axis=0), rtol=1e-5,
+                           atol=1e-5)
+
+
+def test_attention_ref_matches_brute_force_softmax(orc):
+    # Tiny brute force in numpy float64 (GQA head mapping, scale, softcap, mask).
+    r = _rng(12)
+    n_q, n_kv, h, kv, d = 5, 37, 8, 2, 64
+    q, k, v = _qkv(r, n_q, n_kv, h, kv, d)
+    for softcap in (0.0, 20.0):
+        for mode, window in ((0, -1), (2, 2)):
+            out = orc.attention_ref(q, k, v, h, kv, d, 0.125, softcap, mode, window, q0=30, k0=0)
+            for hh in range(h):
+                g = hh // (h // kv)
+                qq = q[:, hh * d:(hh + 1) * d].astype(np.float64)
+                kk = k[:, g * d:(g + 1) * d].astype(np.float64)
+                vv = v[:, g * d:(g + 1) * d].astype(np.float64)
+                s = (qq @ kk.T) * 0.125
+                if softcap:
+                    s = softcap * np.tanh(s / softcap)
+                t = 30 + np.arange(n_q)[:, None]
+                j = np.arange(n_kv)[None, :]
+                if mode == 2:
+                    s = np.where(np.abs(t - j) <= window, s, -np.inf)
+                p = np.exp(s - s.max(axis=1, keepdims=True))
+                want = (p / p.sum(axis=1, keepdims=True)) @ vv
+                assert np.abs(out[:, hh * d:(hh + 1) * d] - want).max() < 2e-6
+
+
+def test_attention_flex_online_fold_equals_one_pass(orc):
+    # attn/mod.rs:1902-1990: the tiled online softmax equals one materialised pass.
+    r = _rng(13)
+    n, h, kv, d = 200, 4, 1, 72
+    q, k, v = _qkv(r, n, n, h, kv, d)
+    for mode, w in ((1, -1), (0, -1), (3, 50), (2, 17)):
+        a = orc.attention_flex(q, k, v, h, kv, d, 72 ** -0.5, mode=mode, window=w)
+        b = orc.attention_ref(q, k, v, h, kv, d, 72 ** -0.5, mode=mode, window=w)
+        assert orc.cosine(a, b) > 0.999999
+        assert np.abs(a - b).max() < 2e-5
+
+
+# ------------------------------------------------------------------- MoE ----
+def test_route_top_k_ties_and_renormalisation(orc):
+    r = _rng(14)
+    logits = r.standard_normal((64, 16)).astype(np.float32)
+    logits[0, :] = 0.0  # all tied: ids 0..k-1
+    logits[1, 5] = logits[1, 9] = 7.0  # tie between 5 and 9 at the top
+    ids, wts = orc.route(logits, 4, True)
+    assert list(ids[0]) == [0, 1, 2, 3]
+    assert list(ids[1][:2]) == [5, 9]
+    for t in range(64):
+        p = np.exp(logits[t].astype(np.float64) - logits[t].max())
+        p /= p.sum()
+        order = sorted(range(16), key=lambda e: (-p[e], e))[:4]
+        if t > 1:
+            assert list(ids[t]) == order
+        assert abs(wts[t].sum() - 1.0) < 1e-6
+        assert np.allclose(wts[t], p[list(ids[t])] / p[list(ids[t])].sum(), rtol=1e-5)
+    ids2, wts2 = orc.route(logits, 4, False)
+    assert (ids2 == ids).all() and (wts2 <= wts + 1e-7).all()
+
+
+def test_moe_emulation_against_dequantised_f64(orc):
+    # src/clef/engine/tests.rs:445-505: the emulated W8A8 expert is within
+    # quantisation error of the naive f64 expert.
+    r = _rng(15)
+    s, H, I, E, K = 12, 64, 32, 4, 2
+    x = r.standard_normal((s, H)).astype(np.float32)
+    ids, wts = orc.route(r.standard_normal((s, E)).astype(np.float32), K)
+    gw = (r.standard_normal((E, I, H)) * 0.3).astype(np.float32)
+    uw = (r.standard_normal((E, I, H)) * 0.3).astype(np.float32)
+    dw = (r.standard_normal((E, H, I)) * 0.3).astype(np.float32)
+    q8 = lambda w: orc.q8_0_quantize(w.reshape(-1, w.shape[-1]))
+    gq, gd = q8(gw)
+    uq, ud = q8(uw)
+    dq, dd = q8(dw)
+    f = lambda d: d.view(np.float16).astype(np.float32)
+    y = orc.moe_experts(x, ids, wts, gq.reshape(E, I, H), f(gd).reshape(E, I, H // 32), uq.reshape(E, I, H),
+                        f(ud).reshape(E, I, H // 32), dq.reshape(E, H, I), f(dd).reshape(E, H, I // 32))
+    want = np.zeros((s, H))
+    silu = lambda z: z / (1 + np.exp(-z))
+    for t in range(s):
+        for j in range(K):
+            e = ids[t, j]
+            xx = x[t].astype(np.float64)
+            g = gw[e].astype(np.float64) @ xx
+            u = uw[e].astype(np.float64) @ xx
+            want[t] += wts[t, j] * (dw[e].astype(np.float64) @ (silu(g) * u))
+    peak = np.abs(want).max()
+    assert np.abs(y - want).max() <= 2e-2 * peak
+    assert orc.cosine(y, want) > 0.999
