@@ -65,6 +65,7 @@ SIGNATURES = {
     "rk_moe_plan_create": (_i, [_u64, _i64, _i, _p, _p, _p]),
     "rk_moe_experts_planned_dev": (_i, [_u64, _p, _p, _p, _p]),
     "rk_moe_plan_destroy": (_i, [_p]),
+    "rk_moe_gate_up_dev": (_i, [_u64, _p, _p, _p, _p]),
     "rk_device_alloc": (_i, [_sz, _p]),
     "rk_device_free": (_i, [_p]),
     "rk_memcpy_htod": (_i, [_p, _p, _sz]),

@@ -265,20 +265,29 @@ __global__ __launch_bounds__(NWAVES * 64) void attn_fwd_kernel(AttnArgs a, int G
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     m_run = m_new;
 
-    half8 pf[4];
+    // P as an unevaluated sum of two fp16 values: hi keeps the top 11 bits of
+    // the f32 probability (exactly representable, so the round-toward-zero
+    // pack is exact) and lo = p - hi carries the rest. Rounding P itself to
+    // fp16 would leave ~2^-12 relative noise per probability in O.
+    half8 phi[4], plo[4];
     float lsum = 0.f;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
 #pragma unroll
       for (int c2 = 0; c2 < 2; ++c2) {
-        half8 p;
+        uintx4 hw, lw;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e = __builtin_amdgcn_exp2f(s[sb][8 * c2 + j] - m_use);
-          lsum += e;
-          p[j] = (f16)e;
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(s[sb][8 * c2 + 2 * j] - m_use);
+          const float e1 = __builtin_amdgcn_exp2f(s[sb][8 * c2 + 2 * j + 1] - m_use);
+          lsum += e0 + e1;
+          const float h0 = __uint_as_float(__float_as_uint(e0) & 0xffffe000u);
+          const float h1 = __uint_as_float(__float_as_uint(e1) & 0xffffe000u);
+          hw[j] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(h0, h1));
+          lw[j] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
         }
-        pf[sb * 2 + c2] = p;
+        phi[sb * 2 + c2] = __builtin_bit_cast(half8, hw);
+        plo[sb * 2 + c2] = __builtin_bit_cast(half8, lw);
       }
     }
     l_run = l_run * alpha + lsum;
@@ -287,14 +296,15 @@ __global__ __launch_bounds__(NWAVES * 64) void attn_fwd_kernel(AttnArgs a, int G
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
 
-    // Oᵀ += Vᵀ·Pᵀ over the four 16-key chunks.
+    // Oᵀ += Vᵀ·Pᵀ over the four 16-key chunks (hi and lo parts).
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
         const half8 vf =
             *(const half8 *)(&sV[buf][(db * 32 + (lane & 31)) * VROW + 16 * c + 8 * hh]);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[c], o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, phi[c], o[db], 0, 0, 0);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, plo[c], o[db], 0, 0, 0);
       }
     }
 

@@ -1095,12 +1095,16 @@ int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const f
   return RK_OK;
 }
 
-int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipStream_t st) {
+int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipStream_t st,
+            float *act_out = nullptr) {
   const int64_t H = w.hidden, I = w.inter, S = plan.s, R = plan.rows;
   void *xq, *xs, *act, *aq, *as, *yb;
   RK_TRY(scratch("moe_xq", (size_t)S * H, &xq));
   RK_TRY(scratch("moe_xs", (size_t)S * 4, &xs));
-  RK_TRY(scratch("moe_act", (size_t)std::max<int64_t>(R, 1) * I * 4, &act));
+  if (act_out)
+    act = act_out;
+  else
+    RK_TRY(scratch("moe_act", (size_t)std::max<int64_t>(R, 1) * I * 4, &act));
   RK_TRY(scratch("moe_aq", (size_t)std::max<int64_t>(R, 1) * I, &aq));
   RK_TRY(scratch("moe_as", (size_t)std::max<int64_t>(R, 1) * 4, &as));
   RK_TRY(scratch("moe_yb", (size_t)std::max<int64_t>(R, 1) * H * 4, &yb));
@@ -1111,6 +1115,7 @@ int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipS
                                 2 * I * w.gu_ws_stride, w.gu_ws_stride, (int)(2 * I), (int)H,
                                 (float *)act, g_eng->num_cus, st),
           op);
+  if (!y) return RK_OK;  // stage 1 only
   HIP_TRY(rk_launch_quantize_rows((const float *)act, R, I, I, (int8_t *)aq, (float *)as, st), op);
   HIP_TRY(rk_launch_moe_gemm_down((const int8_t *)aq, (const float *)as, plan.tiles, plan.n_tiles,
                                   w.dn_codes, w.dn_scales, H * I, H * w.dn_ws_stride,
@@ -1179,6 +1184,20 @@ extern "C" int rk_moe_experts_planned_dev(rk_weight_id id, const void *plan, con
     return fail(RK_E_SHAPE, "rk_moe_experts_planned_dev", "plan was made for another expert stack");
   RK_TRY(moe_run(*w, *p, x, y, pick(stream)));
   g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_moe_gate_up_dev(rk_weight_id id, const void *plan, const float *x, float *act,
+                                  rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_moe_gate_up_dev"));
+  const MoePlan *p = (const MoePlan *)plan;
+  if (!p || !act) return fail(RK_E_SHAPE, "rk_moe_gate_up_dev", "null plan or output");
+  Weight *w;
+  RK_TRY(moe_check(id, p->s, p->top_k, &w, "rk_moe_gate_up_dev"));
+  if (p->weight != id)
+    return fail(RK_E_SHAPE, "rk_moe_gate_up_dev", "plan was made for another expert stack");
+  RK_TRY(moe_run(*w, *p, x, nullptr, pick(stream), act));
   return RK_OK;
 }
 

@@ -280,6 +280,11 @@ int rk_moe_plan_create(rk_weight_id id, int64_t s, int top_k,
 int rk_moe_experts_planned_dev(rk_weight_id id, const void *plan,
                                const float *x, float *y, rk_stream stream);
 int rk_moe_plan_destroy(void *plan);
+/* First stage alone, for exactness checks: act f32 [rows, inter] =
+ * silu(gate·x)·(up·x) for every bucket row, rows ordered by expert id and,
+ * within an expert, by token (the bucket order of engine.rs:292-305). */
+int rk_moe_gate_up_dev(rk_weight_id id, const void *plan, const float *x,
+                       float *act, rk_stream stream);
 
 /* ======================================================================== *
  * Device plumbing for callers without their own HIP runtime bindings       *

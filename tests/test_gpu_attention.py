@@ -84,7 +84,7 @@ def test_config5_gqa_32_4_full(rk, orc):
     k = synth.normal_f16(seeds[7], (s, kv * d))
     v = synth.normal_f16(seeds[8], (s, kv * d))
     got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=1)
-    check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(s, 64))
+    check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(s, 64), mode=1)
 
 
 @pytest.mark.parametrize("d", [64, 72, 80, 96, 112, 128])
@@ -166,3 +166,18 @@ def test_attention_rejects_bad_shapes(rk):
     lib = rk.lib()
     assert lib.rk_attention(None, None, None, 4, 4, 6, 4, 128, 1.0, 0.0, 0, -1, 0, 0, None) == rk.RK_E_SHAPE
     assert lib.rk_attention(None, None, None, 4, 4, 4, 4, 40, 1.0, 0.0, 0, -1, 0, 0, None) == rk.RK_E_UNSUPPORTED
+
+
+def test_attention_is_deterministic(rk, orc):
+    # Same inputs, same bits: the kernel has no atomics or order-dependent sums.
+    c = synth.MOE
+    s, h, kv, d = c["s"], c["attn_heads"], c["attn_kv"], c["attn_d"]
+    note(f"determinism S={s} H={h} KV={kv}")
+    seeds = synth.SEEDS["moe"]
+    q = synth.normal_f16(seeds[6], (s, h * d))
+    k = synth.normal_f16(seeds[7], (s, kv * d))
+    v = synth.normal_f16(seeds[8], (s, kv * d))
+    a = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=1)
+    b = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=1)
+    assert (a == b).all()
+    check(orc, a, orc.attention_flex(q, k, v, h, kv, d, d ** -0.5, 0.0, 1))

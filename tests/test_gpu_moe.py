@@ -1,5 +1,15 @@
 """GPU parity of the MoE expert pipeline (K4: grouped W8A8 GEMMs over per-expert
-token lists, silu·up, down, combine) against the oracle's W8A8 emulation."""
+token lists, silu·up, down, combine) against the oracle.
+
+The pipeline re-quantizes the intermediate activation to int8, so an f32
+rounding-order difference in stage 1 can move an activation across a code
+boundary and change one int8 code; that is a property of the two-stage W8A8
+algorithm, not of the kernels. Each stage is therefore pinned separately:
+stage 1 (gate|up, silu·up) against the oracle within f32 rounding, and stages
+2-3 (re-quantize, down, router weight, combine) against the oracle fed with the
+GPU's own stage-1 output, within f32 rounding and the fp16-output gate. The end
+to end result is held to cosine >= 0.9999."""
+import ctypes
 import sys
 
 import numpy as np
@@ -33,59 +43,140 @@ def make_experts(orc, seed, E, H, I):
     return dict(gq=gq, gs=f(gd), uq=uq, us=f(ud), dq=dq, ds=f(dd), blocks=blocks)
 
 
-def run_moe(rk, wid, x, ids, wts):
-    s, H = x.shape
-    dx = rk.DeviceBuffer.from_array(x)
-    dy = rk.DeviceBuffer(x.nbytes)
+def bucket_order(ids):
+    """(expert, token, slot) of every bucket row: experts ascending, tokens ascending."""
+    S, K = ids.shape
+    tok = np.repeat(np.arange(S), K)
+    slot = np.tile(np.arange(K), S)
+    exp = ids.reshape(-1).astype(np.int64)
+    order = np.lexsort((tok, exp))
+    return exp[order], tok[order], slot[order]
+
+
+def run(rk, wid, x, ids, wts):
+    """Returns (stage-1 act in bucket order, final y) from the planned API."""
+    lib = rk.lib()
+    S, H = x.shape
+    K = ids.shape[1]
     ids = np.ascontiguousarray(ids, np.uint32)
     wts = np.ascontiguousarray(wts, np.float32)
-    rc = rk.lib().rk_moe_experts_dev(int(wid), dx.ptr, s, ids.shape[1], ids.ctypes.data, wts.ctypes.data, dy.ptr,
-                                     None)
-    assert rc == 0, rk.lib().rk_last_error()
+    plan = ctypes.c_void_p()
+    assert lib.rk_moe_plan_create(int(wid), S, K, ids.ctypes.data, wts.ctypes.data, ctypes.byref(plan)) == 0, \
+        lib.rk_last_error()
+    I = rk_inter(rk, wid)
+    dx, dy = rk.DeviceBuffer.from_array(x), rk.DeviceBuffer(x.nbytes)
+    dact = rk.DeviceBuffer(S * K * I * 4)
+    assert lib.rk_moe_gate_up_dev(int(wid), plan, dx.ptr, dact.ptr, None) == 0, lib.rk_last_error()
+    assert lib.rk_moe_experts_planned_dev(int(wid), plan, dx.ptr, dy.ptr, None) == 0, lib.rk_last_error()
     rk.synchronize()
-    return dy.download((s, H), np.float32)
+    act = dact.download((S * K, I), np.float32)
+    y = dy.download((S, H), np.float32)
+    assert lib.rk_moe_plan_destroy(plan) == 0
+    # the one-shot entry gives the same result
+    dy2 = rk.DeviceBuffer(x.nbytes)
+    assert lib.rk_moe_experts_dev(int(wid), dx.ptr, S, K, ids.ctypes.data, wts.ctypes.data, dy2.ptr, None) == 0
+    rk.synchronize()
+    assert (dy2.download((S, H), np.float32) == y).all()
+    return act, y
+
+
+_INTER = {}
+
+
+def rk_inter(rk, wid):
+    return _INTER[int(wid)]
+
+
+def oracle_stage1(orc, x, ex, e_rows, t_rows):
+    H = x.shape[1]
+    xq, xs = orc.quantize_rows(x, H)
+    I = ex["gq"].shape[1]
+    act = np.empty((len(e_rows), I), np.float32)
+    for e in np.unique(e_rows):
+        sel = np.nonzero(e_rows == e)[0]
+        t = t_rows[sel]
+        g = orc.emu_matmul_gw(xq[t], xs[t], H, ex["gq"][e], ex["gs"][e], 32)
+        u = orc.emu_matmul_gw(xq[t], xs[t], H, ex["uq"][e], ex["us"][e], 32)
+        act[sel] = g / (np.float32(1) + np.exp(-g)) * u
+    return act
+
+
+def oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S):
+    I = act.shape[1]
+    H = ex["dq"].shape[1]
+    aq, a_s = orc.quantize_rows(act, I)
+    yb = np.empty((len(e_rows), H), np.float32)
+    for e in np.unique(e_rows):
+        sel = np.nonzero(e_rows == e)[0]
+        yb[sel] = orc.emu_matmul_gw(aq[sel], a_s[sel], I, ex["dq"][e], ex["ds"][e], 32) * w_rows[sel][:, None]
+    y = np.zeros((S, H), np.float32)
+    for row in range(len(e_rows)):  # bucket rows are expert-ascending: the combine order
+        y[t_rows[row]] += yb[row]
+    return y
+
+
+def check_pipeline(rk, orc, S, H, I, E, ids, wts, seed):
+    ex = make_experts(orc, seed, E, H, I)
+    wid = rk.pack_moe_q8_0(*ex["blocks"], E, H, I)
+    _INTER[int(wid)] = I
+    x = synth.normal_f32(seed + 10_000, (S, H))
+    act, y = run(rk, wid, x, ids, wts)
+    e_rows, t_rows, s_rows = bucket_order(ids)
+    w_rows = wts[t_rows, s_rows]
+    # stage 1 within f32 rounding
+    act_ref = oracle_stage1(orc, x, ex, e_rows, t_rows)
+    assert np.abs(act - act_ref).max() <= 2e-5 * np.abs(act_ref).max()
+    # stages 2-3 from the GPU's own activations: f32 rounding only
+    y_ref2 = oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S)
+    assert np.abs(y - y_ref2).max() <= 2e-5 * np.abs(y_ref2).max()
+    assert orc.cosine(y, y_ref2) >= COS_MIN and orc.max_rel(y, y_ref2) <= REL_MAX
+    # end to end against the full oracle pipeline
+    y_ref = orc.moe_experts(x, ids, wts, ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"])
+    assert orc.cosine(y, y_ref) >= COS_MIN
+    return y
 
 
 @pytest.mark.parametrize("S,H,I,E,K", [(256, 512, 256, 16, 4), (300, 256, 128, 8, 8), (5, 128, 64, 4, 2)])
-def test_moe_pipeline_matches_emulation(rk, orc, S, H, I, E, K):
+def test_moe_pipeline_matches_oracle(rk, orc, S, H, I, E, K):
     note(f"MoE S={S} H={H} I={I} E={E} top{K}")
     r = np.random.default_rng(S + E)
-    ex = make_experts(orc, 700 + E, E, H, I)
-    wid = rk.pack_moe_q8_0(*ex["blocks"], E, H, I)
-    x = r.standard_normal((S, H)).astype(np.float32)
     ids, wts = rk.moe_route(r.standard_normal((S, E)).astype(np.float32), K)
-    got = run_moe(rk, wid, x, ids, wts)
-    ref = orc.moe_experts(x, ids, wts, ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"])
-    assert np.isfinite(got).all()
-    cos, rel = orc.cosine(got, ref), orc.max_rel(got, ref)
-    assert cos >= COS_MIN and rel <= REL_MAX, (cos, rel)
+    check_pipeline(rk, orc, S, H, I, E, ids, wts, 700 + E)
 
 
 def test_moe_skewed_routing_over_128_rows_per_expert(rk, orc):
     # Every token picks experts 0 and 1: 600 rows per expert span several tiles.
     note("MoE skewed routing")
-    S, H, I, E = 600, 128, 64, 4
-    ex = make_experts(orc, 900, E, H, I)
-    wid = rk.pack_moe_q8_0(*ex["blocks"], E, H, I)
-    r = np.random.default_rng(1)
-    x = r.standard_normal((S, H)).astype(np.float32)
+    S = 600
     ids = np.tile(np.array([[1, 0]], np.uint32), (S, 1))
     wts = np.tile(np.array([[0.7, 0.3]], np.float32), (S, 1))
-    got = run_moe(rk, wid, x, ids, wts)
-    ref = orc.moe_experts(x, ids, wts, ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"])
-    assert orc.cosine(got, ref) >= COS_MIN and orc.max_rel(got, ref) <= REL_MAX
+    check_pipeline(rk, orc, S, 128, 64, 4, ids, wts, 900)
 
 
-def test_moe_config5_subset_of_experts(rk, orc):
-    # Config-5 expert shapes (hidden 2048, inter 768, top-8 of 128 logits) on
-    # 16 resident experts, with the router over those 16.
+def test_moe_config5_shapes_on_16_experts(rk, orc):
+    # Config-5 expert shapes (hidden 2048, inter 768, top-8) on 16 resident
+    # experts, routed by a softmax over 16 seeded logits.
     c = synth.MOE
     S, H, I, E, K = 512, c["hidden"], c["inter"], 16, c["top_k"]
     note(f"MoE config5 shapes S={S} H={H} I={I} E={E} top{K}")
-    ex = make_experts(orc, synth.SEEDS["moe"][2], E, H, I)
-    wid = rk.pack_moe_q8_0(*ex["blocks"], E, H, I)
-    x = synth.normal_f32(synth.SEEDS["moe"][0], (S, H))
     ids, wts = rk.moe_route(synth.normal_f32(synth.SEEDS["moe"][1], (S, E)), K)
-    got = run_moe(rk, wid, x, ids, wts)
-    ref = orc.moe_experts(x, ids, wts, ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"])
-    assert orc.cosine(got, ref) >= COS_MIN and orc.max_rel(got, ref) <= REL_MAX
+    check_pipeline(rk, orc, S, H, I, E, ids, wts, synth.SEEDS["moe"][2])
+
+
+def test_pack_moe_f32_equals_pack_from_blocks(rk, orc):
+    # The device Q8_0 quantizer gives the stack the GGUF blocks give.
+    note("pack_moe_f32 vs pack_moe_q8_0")
+    E, H, I, S, K = 4, 128, 64, 40, 2
+    r = np.random.default_rng(3)
+    g = (r.standard_normal((E, I, H)) * 0.02).astype(np.float32)
+    u = (r.standard_normal((E, I, H)) * 0.02).astype(np.float32)
+    d = (r.standard_normal((E, H, I)) * 0.02).astype(np.float32)
+    q8 = lambda w: orc.q8_0_blocks(*orc.q8_0_quantize(w.reshape(-1, w.shape[-1])))
+    w1 = rk.pack_moe_q8_0(q8(g), q8(u), q8(d), E, H, I)
+    w2 = rk.pack_moe_f32(g, u, d)
+    _INTER[int(w1)] = _INTER[int(w2)] = I
+    x = r.standard_normal((S, H)).astype(np.float32)
+    ids, wts = rk.moe_route(r.standard_normal((S, E)).astype(np.float32), K)
+    a1, y1 = run(rk, w1, x, ids, wts)
+    a2, y2 = run(rk, w2, x, ids, wts)
+    assert (a1 == a2).all() and (y1 == y2).all()

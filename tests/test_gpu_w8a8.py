@@ -197,3 +197,28 @@ def test_rewrite_replaces_the_resident_codes(rk, orc):
     assert (raw_dev(rk, wid, aq) == orc.matmul_i8_raw(aq, w1)).all()
     rk.rewrite_i8(wid, w2, s)
     assert (raw_dev(rk, wid, aq) == orc.matmul_i8_raw(aq, w2)).all()
+
+
+def test_device_q8_0_packer_equals_gguf_blocks(rk, orc):
+    # rk_pack_q8_0_f32 quantizes on the GPU with the llama.cpp rule; the
+    # resident weight must equal the one packed from the oracle's blocks.
+    note("pack_q8_0_f32 vs pack_q8_0")
+    r = np.random.default_rng(21)
+    m, k, n = 48, 384, 72
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[3, :32] = 0.0  # an all-zero block: scale 0, codes 0
+    wq, wd = orc.q8_0_quantize(w)
+    w1 = rk.pack_q8_0(orc.q8_0_blocks(wq, wd), n, k)
+    w2 = rk.pack_q8_0_f32(w)
+    eye = np.zeros((k, k), np.int8)
+    np.fill_diagonal(eye, 1)
+    # one-hot activations read the codes back exactly: c[i, j] = w_codes[j, i]
+    assert (raw_dev(rk, w2, eye) == wq.T.astype(np.int32)).all()
+    assert (raw_dev(rk, w1, eye) == raw_dev(rk, w2, eye)).all()
+    # unit activation scales read the block scales back: c[i, j] = d[j, i/32]·code
+    dq, ds = dev(rk, eye), dev(rk, np.ones((k, 1), np.float32))
+    s1 = w8a8_dev(rk, w1, dq, ds, k, k, k)
+    s2 = w8a8_dev(rk, w2, dq, ds, k, k, k)
+    assert (s1 == s2).all()
+    d32 = wd.view(np.float16).astype(np.float32)
+    assert (s2 == (wq.astype(np.float32) * np.repeat(d32, 32, axis=1)).T).all()
