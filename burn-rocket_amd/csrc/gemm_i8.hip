@@ -28,6 +28,8 @@
 // Pipeline: a STAGES-deep LDS ring filled by global_load_lds (16-byte chunks
 // for codes, 4-byte elements for scales); a stage is 128 K-values (4 blocks).
 // Code rows are 128 bytes with chunk c of row r at chunk c ^ (r & 7).
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -277,6 +279,286 @@ static hipError_t launch_i8(const I8GemmArgs &g, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel for the two hot modes: per-token activations against a
+// weight with one scale per 32-value block (GGUF Q8_0, group 32), and the raw
+// int32 product. Compared with gemm_i8_kernel above it
+//   * moves tiles with buffer→LDS copies whose K offset is a scalar, and whose
+//     range check zero-fills rows past M/N (no per-stage vector address math);
+//   * computes each lane's LDS fragment addresses once: stage, tile and block
+//     offsets are instruction immediates (the K loop is unrolled over the
+//     STAGES·4 blocks of the LDS ring);
+//   * swizzles 16-byte chunks with (row >> 1) & 7, which keeps the 16 lanes of
+//     each ds_read_b128 phase on distinct banks;
+//   * prefetches the next block's fragments into a second register set and
+//     interleaves every MFMA with the 32 VALU instructions (16 cvt + 16 fma)
+//     that fold the previous tile's int32 block result into the f32
+//     accumulator.
+// The fold is 2 VALU instructions per output element and block (4 cycles
+// each, wave64) against 32 cycles per 32x32x32 MFMA for 1024 elements, so the
+// scaled mode is VALU-bound at 1/4 of the int8 MFMA rate.
+// ---------------------------------------------------------------------------
+namespace {
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Raw buffer descriptor word 3 for gfx9: 32-bit data format, no swizzle.
+constexpr int RSRC_WORD3 = 0x00020000;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  const int64_t b = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)b, RSRC_WORD3);
+}
+// 16-byte buffer→LDS copy: lane i lands at lds_base + 16·i.
+__device__ __forceinline__ void bdma16(rsrc_t r, void *lds_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds_base), 16, voff, soff, 0, 0);
+}
+template <int V>
+using ic = std::integral_constant<int, V>;
+}  // namespace
+
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16>
+__global__ __launch_bounds__(WM *WN * 64, 2) void gemm_i8_q8_kernel(
+    const int8_t *__restrict__ A, const float *__restrict__ AS, const int8_t *__restrict__ W,
+    const float *__restrict__ WS, int ws_stride, void *__restrict__ Cout, int M, int N, int K,
+    int tiles_m) {
+  static_assert(MODE == MODE_PER_TOKEN || MODE == MODE_RAW, "per-token or raw");
+  constexpr int NW = WM * WN;
+  constexpr int NT = NW * 64;
+  constexpr int ROWB = 128;  // K bytes of one stage row
+  constexpr bool SCALED = (MODE == MODE_PER_TOKEN);
+  constexpr int CODE_BYTES = (BM + BN) * ROWB;
+  constexpr int WS_BYTES = SCALED ? BN * 16 : 0;
+  constexpr int STAGE_BYTES = CODE_BYTES + WS_BYTES;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int A_PER = BM / 8 / NW, B_PER = BN / 8 / NW;  // 8-row copies per wave
+  constexpr int WS_INS = SCALED ? BN / 64 : 0;            // 64 scale rows per copy
+  constexpr int L = A_PER + B_PER;                        // copies every wave issues
+  static_assert(A_PER * 8 * NW == BM && B_PER * 8 * NW == BN, "tile/wave split");
+  static_assert(WS_INS <= NW && (!SCALED || WS_INS * 64 == BN), "scale split");
+  static_assert(TM * 32 * WM == BM && TN * 32 * WN == BN, "mfma split");
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  float *s_as = (float *)(smem + STAGES * STAGE_BYTES);  // [BM] activation scales
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int tm = bid % tiles_m, tn = bid / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KT = (K + 127) / 128;
+  const int KB = K / 32;
+
+  const rsrc_t ra = make_rsrc(A + (size_t)m0 * K, (int64_t)(M - m0) * K);
+  const rsrc_t rw = make_rsrc(W + (size_t)n0 * K, (int64_t)(N - n0) * K);
+  const rsrc_t rs = make_rsrc(SCALED ? WS + (size_t)n0 * ws_stride : WS, (int64_t)(N - n0) * ws_stride * 4);
+
+  // Copy geometry: lane covers tile row 8·q + lane/8 and physical chunk lane%8,
+  // which holds logical chunk (lane%8) ^ ((row >> 1) & 7); the swizzle depends
+  // on the parity of q only.
+  const int r8 = lane >> 3, p8 = lane & 7;
+  const uint32_t voff_even = r8 * K + ((p8 ^ (r8 >> 1)) << 4);
+  const uint32_t voff_odd = r8 * K + ((p8 ^ (4 + (r8 >> 1))) << 4);
+  const uint32_t voff_ws = lane * ws_stride * 4;
+
+  if constexpr (SCALED) {
+    for (int r = threadIdx.x; r < BM; r += NT) s_as[r] = AS[min(m0 + r, M - 1)];
+  }
+
+  auto issue = [&](auto slot_c, int kt) {
+    constexpr int slot = decltype(slot_c)::value;
+    uint8_t *sb = smem + slot * STAGE_BYTES;
+    const uint32_t k0 = kt * 128;
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int q = wave * A_PER + i;
+      bdma16(ra, sb + q * 1024, (q & 1) ? voff_odd : voff_even, q * 8 * K + k0);
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+      const int q = wave * B_PER + i;
+      bdma16(rw, sb + BM * ROWB + q * 1024, (q & 1) ? voff_odd : voff_even, q * 8 * K + k0);
+    }
+    if constexpr (WS_INS > 0) {
+      if (wave < WS_INS)
+        bdma16(rs, sb + CODE_BYTES + wave * 1024, voff_ws, wave * 64 * ws_stride * 4 + kt * 16);
+    }
+  };
+  // Make stage kt visible to every wave. Copies return in issue order, so
+  // waiting until at most L·later copies (the stages issued after kt) remain is
+  // enough even for the waves that also copy scales.
+  auto stage_ready = [&](int kt) {
+    if constexpr (STAGES >= 3) {
+      const int later = min(STAGES - 2, KT - 1 - kt);
+      if (later >= 2) {
+        WAIT_VMCNT(L * 2);
+      } else if (later == 1) {
+        WAIT_VMCNT(L);
+      } else {
+        WAIT_VMCNT(0);
+      }
+    } else {
+      WAIT_VMCNT(0);
+    }
+    WAIT_LGKMCNT0();
+    BARRIER();
+  };
+
+  const int wm = wave / WN, wn = wave % WN;
+  const int fcol = lane & 31, fh = lane >> 5;
+  const int swz = (fcol >> 1) & 7;
+  uint32_t a_off[4], b_off[4];  // lane's fragment byte offsets per block (stage 0)
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t ch = (uint32_t)(((2 * b + fh) ^ swz) << 4);
+    a_off[b] = (wm * WTM + fcol) * ROWB + ch;
+    b_off[b] = BM * ROWB + (wn * WTN + fcol) * ROWB + ch;
+  }
+  const uint32_t s_off = CODE_BYTES + (wn * WTN + fcol) * 16;
+
+  intx4 af[2][TM], bf[2][TN];
+  float dsc[2][TN];
+  auto load_frags = [&](auto buf_c, auto slot_c, auto b_c) {
+    constexpr int buf = decltype(buf_c)::value, slot = decltype(slot_c)::value,
+                  b = decltype(b_c)::value;
+    const uint8_t *base = smem + slot * STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[buf][i] = *(const intx4 *)(base + a_off[b] + i * 32 * ROWB);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      bf[buf][j] = *(const intx4 *)(base + b_off[b] + j * 32 * ROWB);
+      if constexpr (SCALED) dsc[buf][j] = *(const float *)(base + s_off + j * 32 * 16 + b * 4);
+    }
+  };
+
+  intx16 iacc[TM][TN];
+  floatx16 facc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        facc[i][j][r] = 0.f;
+        iacc[i][j][r] = 0;
+      }
+
+  issue(ic<0>{}, 0);
+  if constexpr (STAGES > 2) {
+    if (1 < KT) issue(ic<1>{}, 1);
+  }
+  stage_ready(0);
+  if (STAGES - 1 < KT) issue(ic<STAGES - 1>{}, STAGES - 1);
+  load_frags(ic<0>{}, ic<0>{}, ic<0>{});
+
+  // Block step: global block g sits at slot S, block B of its stage, and uses
+  // register set CUR (= B parity).
+  auto step = [&](int g, auto s_c, auto b_c) {
+    constexpr int S = decltype(s_c)::value, B = decltype(b_c)::value;
+    constexpr int CUR = B & 1, NXT = CUR ^ 1;
+    constexpr int NS = (B == 3) ? (S + 1) % STAGES : S, NB = (B + 1) & 3;
+    const int gn = g + 1;
+    if constexpr (B == 3) {
+      if (gn < KB) {
+        const int kt = gn >> 2;
+        stage_ready(kt);
+        if (kt + STAGES - 1 < KT) issue(ic<S>{}, kt + STAGES - 1);
+      }
+    }
+    // The prefetch of block g+1 is unconditional (past the last block it reads
+    // stale, in-bounds LDS that is never used) so that it shares a scheduling
+    // region with the MFMAs below.
+    load_frags(ic<NXT>{}, ic<NS>{}, ic<NB>{});
+    if constexpr (MODE == MODE_RAW) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          iacc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][i], bf[CUR][j], iacc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          iacc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][i], bf[CUR][j], intx16{}, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            facc[i][j][r] = __builtin_fmaf((float)iacc[i][j][r], dsc[CUR][j], facc[i][j][r]);
+        }
+      // Issue order: MFMA 0, the next block's LDS reads, then for every
+      // further MFMA the fold of the tile before it; the last tile's fold ends
+      // the step.
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + 2 * TN), 0);
+#pragma unroll
+      for (int t = 1; t < TM * TN; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
+    }
+  };
+
+  for (int g0 = 0; g0 < KB; g0 += 4 * STAGES) {
+    auto stage = [&](auto s_c) {
+      const int gs = g0 + 4 * decltype(s_c)::value;
+      if (gs + 0 < KB) step(gs + 0, s_c, ic<0>{});
+      if (gs + 1 < KB) step(gs + 1, s_c, ic<1>{});
+      if (gs + 2 < KB) step(gs + 2, s_c, ic<2>{});
+      if (gs + 3 < KB) step(gs + 3, s_c, ic<3>{});
+    };
+    stage(ic<0>{});
+    if constexpr (STAGES > 1) stage(ic<1>{});
+    if constexpr (STAGES > 2) stage(ic<2>{});
+  }
+
+  // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of column lane%32.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    floatx4 as4[4];
+    if constexpr (SCALED) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) as4[q] = *(const floatx4 *)(s_as + wm * WTM + i * 32 + q * 8 + fh * 4);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * WTN + j * 32 + fcol;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * WTM + i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+        if (m < M && n < N) {
+          if constexpr (MODE == MODE_RAW) {
+            ((int32_t *)Cout)[(size_t)m * N + n] = iacc[i][j][r];
+          } else {
+            const float v = as4[r >> 2][r & 3] * facc[i][j][r];
+            if constexpr (OUT_F16)
+              ((f16 *)Cout)[(size_t)m * N + n] = (f16)v;
+            else
+              ((float *)Cout)[(size_t)m * N + n] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16>
+static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
+  constexpr int smem =
+      STAGES * ((BM + BN) * 128 + (MODE == MODE_PER_TOKEN ? BN * 16 : 0)) + BM * 4;
+  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, g.A, g.AS, g.W, g.WS,
+                     g.ws_stride, g.C, g.M, g.N, g.K, tm);
+  return hipGetLastError();
+}
+
 template <int MODE, bool OUT_F16, bool GB1>
 static hipError_t dispatch_i8(const I8GemmArgs &g, hipStream_t st) {
   const long t128 = ((g.M + 127) / 128) * (long)((g.N + 127) / 128);
@@ -294,11 +576,15 @@ static hipError_t dispatch_scaled(const I8GemmArgs &g, hipStream_t st) {
 hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
   switch (g.mode) {
     case I8_PER_TOKEN:
+      // One scale per 32-value block (GGUF Q8_0 / group 32): pipelined kernel.
+      if (g.gb == 1)
+        return g.out_f16 ? launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, true>(g, st)
+                         : launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, false>(g, st);
       return dispatch_scaled<MODE_PER_TOKEN>(g, st);
     case I8_PER_GROUP:
       return dispatch_scaled<MODE_PER_GROUP>(g, st);
     case I8_RAW:
-      return dispatch_i8<MODE_RAW, false, false>(g, st);
+      return launch_q8<128, 128, 2, 2, 2, MODE_RAW, false>(g, st);
     case I8_PARTIALS:
       return launch_i8<64, 64, 2, 2, 4, MODE_PARTIALS, false, true>(g, st);
   }
