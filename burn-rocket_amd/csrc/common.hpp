@@ -58,5 +58,32 @@ __device__ __forceinline__ int xcd_swizzle(int b, int nblocks) {
   return (b % nx) * (nblocks / nx) + b / nx;
 }
 
+// The same for any grid size: XCD x receives workgroups x, x+8, x+16, ...,
+// which become one contiguous range of logical indices.
+__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
+  const int nx = 8, x = b % nx, q = nblocks / nx, r = nblocks % nx;
+  return x * q + min(x, r) + b / nx;
+}
+
+// Logical tile index → (tile row, tile column). group_m <= 0: row-fastest
+// over the whole grid. Otherwise tiles come in groups of group_m tile rows,
+// row-fastest inside a group, so a run of consecutive tiles (one XCD's share)
+// reads a few A row-blocks and a few B column-blocks instead of all of A.
+__device__ __forceinline__ void tile_coords(int L, int tiles_m, int tiles_n, int group_m, int &tm,
+                                            int &tn) {
+  if (group_m <= 0 || group_m >= tiles_m) {
+    tm = L % tiles_m;
+    tn = L / tiles_m;
+    return;
+  }
+  const int per_group = group_m * tiles_n;
+  const int g = L / per_group;
+  const int first_m = g * group_m;
+  const int gm = min(tiles_m - first_m, group_m);
+  const int l = L - g * per_group;
+  tm = first_m + l % gm;
+  tn = l / gm;
+}
+
 static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }

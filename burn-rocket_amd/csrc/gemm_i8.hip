@@ -29,6 +29,7 @@
 // for codes, 4-byte elements for scales); a stage is 128 K-values (4 blocks).
 // Code rows are 128 bytes with chunk c of row r at chunk c ^ (r & 7).
 #include <type_traits>
+#include <utility>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -313,13 +314,22 @@ __device__ __forceinline__ void bdma16(rsrc_t r, void *lds_base, uint32_t voff, 
 }
 template <int V>
 using ic = std::integral_constant<int, V>;
+template <typename F, int... U>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, U...>) {
+  (f(ic<U>{}), ...);
+}
+// f(ic<0>{}), ..., f(ic<N-1>{}) in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 }  // namespace
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16>
-__global__ __launch_bounds__(WM *WN * 64, 2) void gemm_i8_q8_kernel(
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2>
+__global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     const int8_t *__restrict__ A, const float *__restrict__ AS, const int8_t *__restrict__ W,
     const float *__restrict__ WS, int ws_stride, void *__restrict__ Cout, int M, int N, int K,
-    int tiles_m) {
+    int tiles_m, int tiles_n, int group_m) {
   static_assert(MODE == MODE_PER_TOKEN || MODE == MODE_RAW, "per-token or raw");
   constexpr int NW = WM * WN;
   constexpr int NT = NW * 64;
@@ -342,8 +352,8 @@ __global__ __launch_bounds__(WM *WN * 64, 2) void gemm_i8_q8_kernel(
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int tm = bid % tiles_m, tn = bid / tiles_m;
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = (K + 127) / 128;
   const int KB = K / 32;
@@ -450,6 +460,24 @@ __global__ __launch_bounds__(WM *WN * 64, 2) void gemm_i8_q8_kernel(
   if (STAGES - 1 < KT) issue(ic<STAGES - 1>{}, STAGES - 1);
   load_frags(ic<0>{}, ic<0>{}, ic<0>{});
 
+  // Scaled mode software pipeline. The block results of the T = TM·TN tiles
+  // are produced into two alternating register sets (ires) and each is folded
+  // one MFMA later: MFMA(u+1) is issued before the 32 VALU instructions that
+  // fold tile u, so the MFMA of the next tile runs while the VALU folds the
+  // previous one. The pending tile of a block is folded at the start of the
+  // next block. sched_barrier(0) fences keep this issue order.
+  constexpr int T = TM * TN;
+  static_assert(!SCALED || (T % 2) == 0, "even tile count per wave");
+  intx16 ires[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ires[0][r] = ires[1][r] = 0;
+  float dpend = 0.f;  // scale of the pending tile (the last tile of the previous block)
+  auto fold = [&](auto p_c, auto i_c, auto j_c, float d) {
+    constexpr int P = decltype(p_c)::value, I = decltype(i_c)::value, J = decltype(j_c)::value;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) facc[I][J][r] = __builtin_fmaf((float)ires[P][r], d, facc[I][J][r]);
+  };
+
   // Block step: global block g sits at slot S, block B of its stage, and uses
   // register set CUR (= B parity).
   auto step = [&](int g, auto s_c, auto b_c) {
@@ -464,37 +492,38 @@ __global__ __launch_bounds__(WM *WN * 64, 2) void gemm_i8_q8_kernel(
         if (kt + STAGES - 1 < KT) issue(ic<S>{}, kt + STAGES - 1);
       }
     }
-    // The prefetch of block g+1 is unconditional (past the last block it reads
-    // stale, in-bounds LDS that is never used) so that it shares a scheduling
-    // region with the MFMAs below.
-    load_frags(ic<NXT>{}, ic<NS>{}, ic<NB>{});
     if constexpr (MODE == MODE_RAW) {
+      // The prefetch of block g+1 is unconditional (past the last block it
+      // reads stale, in-bounds LDS that is never used) so that it shares a
+      // scheduling region with the MFMAs below.
+      load_frags(ic<NXT>{}, ic<NS>{}, ic<NB>{});
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
           iacc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][i], bf[CUR][j], iacc[i][j], 0, 0, 0);
     } else {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          iacc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][i], bf[CUR][j], intx16{}, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            facc[i][j][r] = __builtin_fmaf((float)iacc[i][j][r], dsc[CUR][j], facc[i][j][r]);
-        }
-      // Issue order: MFMA 0, the next block's LDS reads, then for every
-      // further MFMA the fold of the tile before it; the last tile's fold ends
-      // the step.
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TM + 2 * TN), 0);
-#pragma unroll
-      for (int t = 1; t < TM * TN; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
+      // The next block's fragments are read from LDS first (register set
+      // NXT is free: its MFMAs were all issued in the previous step), then
+      // tile 0 of this block, then the fold of the previous block's last tile.
+      const float dlast = dsc[CUR][TN - 1];
+      load_frags(ic<NXT>{}, ic<NS>{}, ic<NB>{});
+      __builtin_amdgcn_sched_barrier(0);
+      ires[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bf[CUR][0], intx16{}, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      fold(ic<1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+      __builtin_amdgcn_sched_barrier(0);
+      // Tiles 1..T-1: MFMA of tile u, then the fold of tile u-1.
+      static_for<T - 1>([&](auto uc) {
+        constexpr int u = decltype(uc)::value + 1;
+        constexpr int I = u / TN, J = u % TN;
+        constexpr int PI = (u - 1) / TN, PJ = (u - 1) % TN;
+        ires[u & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][I], bf[CUR][J], intx16{}, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(ic<(u - 1) & 1>{}, ic<PI>{}, ic<PJ>{}, dsc[CUR][PJ]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      dpend = dlast;
     }
   };
 
@@ -510,6 +539,7 @@ __global__ __launch_bounds__(WM *WN * 64, 2) void gemm_i8_q8_kernel(
     if constexpr (STAGES > 1) stage(ic<1>{});
     if constexpr (STAGES > 2) stage(ic<2>{});
   }
+  if constexpr (SCALED) fold(ic<1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
 
   // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of column lane%32.
 #pragma unroll
@@ -541,11 +571,11 @@ __global__ __launch_bounds__(WM *WN * 64, 2) void gemm_i8_q8_kernel(
   }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16>
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2>
 static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   constexpr int smem =
       STAGES * ((BM + BN) * 128 + (MODE == MODE_PER_TOKEN ? BN * 16 : 0)) + BM * 4;
-  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16>;
+  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16, MINW>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -555,8 +585,44 @@ static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   }
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, g.A, g.AS, g.W, g.WS,
-                     g.ws_stride, g.C, g.M, g.N, g.K, tm);
+                     g.ws_stride, g.C, g.M, g.N, g.K, tm, tn, rk_knob("RK_TILE_GROUP_M", 0));
   return hipGetLastError();
+}
+
+// Tile configurations of the per-token Q8_0 kernel. Default: 128x128 tiles on
+// 8 waves (2 workgroups and 4 waves per SIMD) when that fills every CU, else
+// 128x64 tiles on 4 waves. RK_Q8_TILE selects a configuration by number.
+template <bool OUT_F16>
+static hipError_t launch_q8_cfg(const I8GemmArgs &g, hipStream_t st) {
+  const long t128 = ((g.M + 127) / 128) * (long)((g.N + 127) / 128);
+  switch (rk_knob("RK_Q8_TILE", t128 >= g.num_cus ? 10 : 0)) {
+    case 1:
+      return launch_q8<128, 64, 2, 2, 3, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 2:
+      return launch_q8<128, 128, 2, 2, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 3:
+      return launch_q8<128, 128, 2, 2, 3, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 4:
+      return launch_q8<256, 64, 4, 1, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 5:
+      return launch_q8<64, 128, 1, 4, 3, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 6:
+      return launch_q8<64, 64, 2, 1, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 7:
+      return launch_q8<64, 128, 2, 2, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 8:
+      return launch_q8<64, 64, 2, 1, 3, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 9:
+      return launch_q8<64, 64, 1, 2, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
+    case 10:
+      return launch_q8<128, 128, 2, 4, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 11:
+      return launch_q8<256, 128, 4, 4, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 12:
+      return launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    default:
+      return launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
+  }
 }
 
 template <int MODE, bool OUT_F16, bool GB1>
@@ -578,8 +644,7 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
     case I8_PER_TOKEN:
       // One scale per 32-value block (GGUF Q8_0 / group 32): pipelined kernel.
       if (g.gb == 1)
-        return g.out_f16 ? launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, true>(g, st)
-                         : launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, false>(g, st);
+        return g.out_f16 ? launch_q8_cfg<true>(g, st) : launch_q8_cfg<false>(g, st);
       return dispatch_scaled<MODE_PER_TOKEN>(g, st);
     case I8_PER_GROUP:
       return dispatch_scaled<MODE_PER_GROUP>(g, st);

@@ -3,6 +3,17 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
+
+// Integer tuning knob from the environment (read at every call, like the
+// reference's ROCKET_* knobs); `dflt` when unset or not a number.
+static inline int rk_knob(const char *name, int dflt) {
+  const char *v = getenv(name);
+  if (!v || !*v) return dflt;
+  char *end = nullptr;
+  const long x = strtol(v, &end, 10);
+  return (end && *end == 0) ? (int)x : dflt;
+}
 
 // fp16 GEMM, C[M,N] = A[M,K]·B[N,K]ᵀ, K % 8 == 0.
 hipError_t rk_launch_gemm_f16(const void *A, const void *B, void *C, int M, int N, int K,
