@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "../../include/burn_rocket_amd.h"
 
 typedef _Float16 f16;
@@ -83,6 +86,35 @@ __device__ __forceinline__ void tile_coords(int L, int tiles_m, int tiles_n, int
   const int l = L - g * per_group;
   tm = first_m + l % gm;
   tn = l / gm;
+}
+
+
+// ---- buffer resources and compile-time loops ------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Raw buffer descriptor word 3 for gfx9: 32-bit data format, no swizzle.
+constexpr int RSRC_WORD3 = 0x00020000;
+
+// Buffer over [base, base + bytes); loads at offsets past the end return 0.
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  const int64_t b = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)b, RSRC_WORD3);
+}
+// A byte offset that is past the end of every buffer (the load returns 0).
+constexpr uint32_t OOB_OFFSET = 0x80000000u;
+// 16-byte buffer→LDS copy: lane i lands at lds_base + 16·i.
+__device__ __forceinline__ void bdma16(rsrc_t r, void *lds_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds_base), 16, voff, soff, 0, 0);
+}
+template <int V>
+using ic = std::integral_constant<int, V>;
+template <typename F, int... U>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, U...>) {
+  (f(ic<U>{}), ...);
+}
+// f(ic<0>{}), ..., f(ic<N-1>{}) in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -3,76 +3,117 @@
 // Stands in for the resident fp16 matmul of the reference
 // (crates/rocket-npu/src/matmul/context.rs:497-513, run.rs:244/571): both
 // operands are K-contiguous (activations [M,K], HF weights [N,K]), which is
-// the natural MFMA operand order, so no transpose or repack is needed.
+// the MFMA operand order, so no transpose or repack is needed.
 //
 // Design
-//   * Workgroup tile BM×BN, K-step 64, WM×WN waves; each wave owns a
-//     (BM/WM)×(BN/WN) block of v_mfma_f32_16x16x32_f16 tiles.
-//   * A STAGES-deep LDS ring is filled with global_load_lds_dwordx4 (one
-//     16-byte chunk per lane, no VGPR staging). A stage holds BM + BN rows of
-//     128 bytes; chunk c of row r sits at chunk c ^ (r & 7), so the eight rows
-//     read by consecutive lanes of an MFMA fragment load hit distinct banks.
-//   * One barrier per K-step: wait for this stage's copies (vmcnt), barrier,
-//     refill the stage consumed in the previous step, compute.
-//   * Rows past M/N are clamped (their results are never stored); chunks past
-//     K read a zero block so the tail contributes nothing.
+//   * Workgroup tile BM×BN on WM×WN waves; each wave owns a (BM/WM)×(BN/WN)
+//     block of v_mfma_f32_16x16x32_f16 tiles (the 16x16x32 form sustains a
+//     higher fraction of the fp16 peak on gfx950 than 32x32x16).
+//   * The K loop advances 64 values per stage. An ST-deep LDS ring holds one
+//     stage per slot: BM + BN rows of 128 bytes, filled by buffer→LDS copies
+//     of 8 whole rows (full 128-byte lines) per instruction, with no VGPR
+//     staging. Rows past M/N and chunks past K are read at an out-of-range
+//     offset, which the buffer unit returns as zeros, so ragged edges need no
+//     extra code.
+//   * Chunk c (16 bytes) of row r sits at chunk c ^ f(r), f(r) = (r & 7) ^
+//     ((r >> 3) & 1): any 8 consecutive rows of one fragment read cover the 8
+//     16-byte bank groups of a 128-byte bank row and any 16 rows cover the 16
+//     groups of a 256-byte row, so fragment reads are conflict-free.
+//   * A stage is two MFMA sub-steps of 32 K-values. Sub-step 0's MFMAs run
+//     while sub-step 1's fragments are read; then the next stage is waited
+//     for (one barrier per stage), the slot consumed one stage ago is
+//     refilled, and sub-step 1's MFMAs run while the next stage's first
+//     fragments are read (two register sets).
+//   * The MFMA computes Cᵀ tiles (B fragment as the A operand), so a lane
+//     holds four consecutive columns of one row of C: 8-byte stores.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
-template <int BM, int BN, int WM, int WN, int STAGES>
-__global__ __launch_bounds__(WM *WN * 64) void gemm_f16_nt_kernel(
-    const f16 *__restrict__ A, const f16 *__restrict__ B, f16 *__restrict__ C,
-    int M, int N, int K, int tiles_m) {
+namespace {
+constexpr int KS = 64;    // K values per stage
+constexpr int ROWB = 128;  // bytes per LDS row of one stage
+}  // namespace
+
+template <int BM, int BN, int WM, int WN, int ST, int MINW>
+__global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
+    const f16 *__restrict__ A, const f16 *__restrict__ B, f16 *__restrict__ C, int M, int N, int K,
+    int tiles_m, int tiles_n, int group_m) {
   constexpr int NW = WM * WN;
-  constexpr int BK = 64;
-  constexpr int ROWB = BK * 2;
-  constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  constexpr int STAGE = (BM + BN) * ROWB;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 16, TN = WTN / 16;
-  constexpr int A_PER = BM / 8 / NW, B_PER = BN / 8 / NW;
-  constexpr int L = A_PER + B_PER;
-  static_assert(A_PER * 8 * NW == BM && B_PER * 8 * NW == BN, "tile/wave split");
+  // One stage is A_INS + B_INS copies of 8 rows; wave w issues copies w,
+  // w + NW, ...; when they do not divide evenly the last ones copy zeros into
+  // a dummy 1 KB area past the ring, so every wave issues L copies.
+  constexpr int A_INS = BM / 8, B_INS = BN / 8;
+  constexpr int L = (A_INS + B_INS + NW - 1) / NW;
+  constexpr int DUMMY = ST * STAGE;
   static_assert(TM * 16 * WM == BM && TN * 16 * WN == BN, "mfma split");
+  static_assert(ST >= 3 && (ST - 2) * L <= 63, "pipeline depth");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int tm = bid % tiles_m, tn = bid / tiles_m;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int tm, tn;
+  tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = (K + BK - 1) / BK;
+  const int KT = (K + KS - 1) / KS;  // stages
 
-  // DMA sources: lane covers row 8·instr + lane/8, physical chunk lane%8,
-  // which holds logical chunk (lane%8) ^ (lane/8).
-  const int r8 = lane >> 3;
-  const int lchunk = (lane & 7) ^ r8;
-  const f16 *a_src[A_PER];
-  const f16 *b_src[B_PER];
-#pragma unroll
-  for (int i = 0; i < A_PER; ++i) {
-    int row = (wave * A_PER + i) * 8 + r8;
-    int gm = min(m0 + row, M - 1);
-    a_src[i] = A + (size_t)gm * K + lchunk * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < B_PER; ++i) {
-    int row = (wave * B_PER + i) * 8 + r8;
-    int gn = min(n0 + row, N - 1);
-    b_src[i] = B + (size_t)gn * K + lchunk * 8;
-  }
+  const rsrc_t ra = make_rsrc(A + (size_t)m0 * K, (int64_t)min(M - m0, BM) * K * 2);
+  const rsrc_t rb = make_rsrc(B + (size_t)n0 * K, (int64_t)min(N - n0, BN) * K * 2);
 
-  auto issue = [&](int kt) {
-    uint8_t *sb = smem + (kt % STAGES) * STAGE_BYTES;
-    const int k0 = kt * BK;
-    const bool in = (k0 + lchunk * 8) < K;
+  // Copy geometry: copy q covers rows 8q..8q+7; lane → row r = 8q + lane/8,
+  // physical chunk lane%8, which holds logical chunk (lane%8) ^ f(r). f(r)
+  // depends on the parity of q only.
+  const int crow = lane >> 3;
+  const int lch0 = (lane & 7) ^ (crow & 7);        // q even
+  const int lch1 = (lane & 7) ^ ((crow & 7) ^ 1);  // q odd
+  const uint32_t voff0 = (uint32_t)(crow * K * 2 + lch0 * 16);
+  const uint32_t voff1 = (uint32_t)(crow * K * 2 + lch1 * 16);
+  const bool ktail = (K % KS) != 0;
+
+  // Copies of stage s; stages past the end copy zeros (into a slot no later
+  // stage reads), which keeps the loop body free of branches.
+  auto issue = [&](int s) {
+    uint8_t *sb = smem + (s % ST) * STAGE;
+    const int k0 = s * KS;
+    const bool past = s >= KT;
+    const uint32_t v0 = (past || (ktail && k0 + lch0 * 8 >= K)) ? OOB_OFFSET : voff0;
+    const uint32_t v1 = (past || (ktail && k0 + lch1 * 8 >= K)) ? OOB_OFFSET : voff1;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      dma16(in ? (const void *)(a_src[i] + k0) : (const void *)g_zero_chunk,
-            sb + (wave * A_PER + i) * 1024);
+    for (int i = 0; i < L; ++i) {
+      const int q = wave + NW * i;  // wave-uniform
+      if (q < A_INS) {
+        bdma16(ra, sb + q * 1024, (q & 1) ? v1 : v0, (uint32_t)((q * 8 * K + k0) * 2));
+      } else if (q < A_INS + B_INS) {
+        const int qb = q - A_INS;
+        bdma16(rb, sb + BM * ROWB + qb * 1024, (qb & 1) ? v1 : v0, (uint32_t)((qb * 8 * K + k0) * 2));
+      } else {
+        bdma16(ra, smem + DUMMY, OOB_OFFSET, 0);
+      }
+    }
+  };
+
+  // Fragment reads: lane → row lane%16 of a 16-row tile, K chunk 4·kk + lane/16.
+  const int wm = wave / WN, wn = wave % WN;
+  const int frow = lane & 15;
+  const int ff = (frow & 7) ^ (frow >> 3);
+  const uint32_t fch0 = (uint32_t)((((lane >> 4)) ^ ff) << 4);      // sub-step 0
+  const uint32_t fch1 = (uint32_t)((((lane >> 4) + 4) ^ ff) << 4);  // sub-step 1
+  const uint32_t a_row = (uint32_t)((wm * WTM + frow) * ROWB);
+  const uint32_t b_row = (uint32_t)(BM * ROWB + (wn * WTN + frow) * ROWB);
+
+  half8 fa[2][TM], fb[2][TN];
+  auto load_frags = [&](auto buf_c, int s, uint32_t fch) {
+    constexpr int BUF = decltype(buf_c)::value;
+    const uint8_t *base = smem + (s % ST) * STAGE;
 #pragma unroll
-    for (int i = 0; i < B_PER; ++i)
-      dma16(in ? (const void *)(b_src[i] + k0) : (const void *)g_zero_chunk,
-            sb + BM * ROWB + (wave * B_PER + i) * 1024);
+    for (int i = 0; i < TM; ++i) fa[BUF][i] = *(const half8 *)(base + a_row + fch + i * 16 * ROWB);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[BUF][j] = *(const half8 *)(base + b_row + fch + j * 16 * ROWB);
   };
 
   floatx4 acc[TM][TN];
@@ -81,70 +122,84 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_f16_nt_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int wm = wave / WN, wn = wave % WN;
-  const int frow = lane & 15, fgrp = lane >> 4;
-
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < KT) issue(s);
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int ahead = min(STAGES - 2, KT - 1 - kt);
-    if (ahead >= 2 && STAGES >= 4) {
-      WAIT_VMCNT(L * 2);
-    } else if (ahead == 1) {
-      WAIT_VMCNT(L);
-    } else {
-      WAIT_VMCNT(0);
+  constexpr int T = TM * TN;
+  auto mfmas = [&](auto buf_c) {
+    constexpr int BUF = decltype(buf_c)::value;
+    static_for<T>([&](auto u_c) {
+      constexpr int U = decltype(u_c)::value, I = U / TN, J = U % TN;
+      acc[I][J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[BUF][J], fa[BUF][I], acc[I][J], 0, 0, 0);
+    });
+  };
+  // One MFMA, one copy; one MFMA, one fragment read; then the rest.
+  auto interleave = [&](auto ncopy_c) {
+    constexpr int NC = decltype(ncopy_c)::value;
+    if constexpr (T >= NC + TM + TN) {
+      static_for<NC>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      });
+      static_for<TM + TN>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      });
+      __builtin_amdgcn_sched_group_barrier(0x008, T - NC - TM - TN, 0);
     }
-    WAIT_LGKMCNT0();
+  };
+
+  // Prologue: stages 0..ST-2 in flight, stage 0 visible, its first fragments read.
+#pragma unroll
+  for (int s = 0; s < ST - 1; ++s) issue(s);
+  WAIT_VMCNT((ST - 2) * L);
+  BARRIER();
+  load_frags(ic<0>{}, 0, fch0);
+
+  for (int s = 0; s < KT; ++s) {
+    // Sub-step 0 (register set 0) while sub-step 1's fragments are read.
+    load_frags(ic<1>{}, s, fch1);
+    mfmas(ic<0>{});
+    interleave(ic<0>{});
+    __builtin_amdgcn_sched_barrier(0);
+    // Stage s+1 visible to all waves (stages up to s+ST-2 were issued); the
+    // slot of stage s-1 is refilled with stage s+ST-1. Sub-step 1 runs while
+    // stage s+1's first fragments are read (past the last stage: stale, unused).
+    WAIT_VMCNT((ST - 3) * L);
     BARRIER();
-    if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
-
-    const uint8_t *sa = smem + (kt % STAGES) * STAGE_BYTES;
-    const uint8_t *sbm = sa + BM * ROWB;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int c = kk * 4 + fgrp;
-      half8 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        int row = wm * WTM + i * 16 + frow;
-        af[i] = *(const half8 *)(sa + row * ROWB + ((c ^ (row & 7)) << 4));
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        int row = wn * WTN + j * 16 + frow;
-        bf[j] = *(const half8 *)(sbm + row * ROWB + ((c ^ (row & 7)) << 4));
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
+    issue(s + ST - 1);
+    load_frags(ic<0>{}, s + 1, fch0);
+    mfmas(ic<1>{});
+    interleave(ic<L>{});
+    __builtin_amdgcn_sched_barrier(0);
   }
+  WAIT_VMCNT(0);  // no copy may still be writing LDS when the workgroup ends
 
-  // Epilogue: lane holds C[row = 4·(lane/16) + r][col = lane%16] of each tile.
+  // Epilogue: lane holds C[row lane%16][cols 4·(lane/16) + 0..3] of each tile.
+  const bool vec = (N % 4) == 0;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WTM + i * 16 + frow;
+    if (m >= M) continue;
+    f16 *crow_p = C + (size_t)m * N;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * WTN + j * 16 + frow;
+      const int n = n0 + wn * WTN + j * 16 + 4 * (lane >> 4);
+      const half4 h = {(f16)acc[i][j][0], (f16)acc[i][j][1], (f16)acc[i][j][2], (f16)acc[i][j][3]};
+      if (vec && n + 3 < N) {
+        *(half4 *)(crow_p + n) = h;
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * WTM + i * 16 + fgrp * 4 + r;
-        if (m < M && n < N) C[(size_t)m * N + n] = (f16)acc[i][j][r];
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) crow_p[n + e] = h[e];
       }
     }
   }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES>
-static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, f16 *C, int M, int N,
-                                  int K, hipStream_t st) {
-  constexpr int smem = STAGES * (BM + BN) * 128;
-  auto kern = gemm_f16_nt_kernel<BM, BN, WM, WN, STAGES>;
+template <int BM, int BN, int WM, int WN, int ST, int MINW>
+static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, f16 *C, int M, int N, int K,
+                                  hipStream_t st) {
+  constexpr int smem = ST * (BM + BN) * ROWB + 1024;
+  static_assert(smem <= 160 * 1024, "LDS per workgroup");
+  auto kern = gemm_f16_kernel<BM, BN, WM, WN, ST, MINW>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -153,21 +208,75 @@ static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, f16 *C, int M, int
     attr_set = true;
   }
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, A, B, C, M, N, K, tm);
+  hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, A, B, C, M, N, K, tm, tn,
+                     rk_knob("RK_TILE_GROUP_M", 0));
   return hipGetLastError();
 }
 
-// Tile choice: the largest tile that still gives at least one workgroup per
-// CU; small problems fall back to 64-row tiles.
+namespace {
+// Tile configurations: workgroup tile, workgroups per CU that fit in LDS, and
+// the fraction of a CU's fp16 MFMA peak one tile sustains once running
+// (measured on the vision-layer and 512x1024x3072 shapes at K ~ 1-4k).
+struct F16Cfg {
+  int bm, bn, per_cu;
+  float eff;
+};
+constexpr F16Cfg F16_CFGS[] = {
+    {256, 128, 1, .30f}, {192, 192, 1, .31f}, {128, 128, 1, .27f}, {128, 64, 2, .18f},
+    {64, 64, 2, .20f},   {128, 256, 1, .30f}, {96, 128, 1, .26f},  {128, 192, 1, .29f},
+    {192, 128, 1, .29f}, {64, 128, 2, .20f},  {192, 192, 1, .33f}, {192, 192, 1, .33f},
+    {128, 128, 1, .28f}, {128, 192, 1, .34f}, {192, 128, 1, .34f},
+};
+constexpr int N_F16_CFGS = sizeof(F16_CFGS) / sizeof(F16_CFGS[0]);
+
+hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, int K,
+                      hipStream_t st) {
+  switch (c) {
+    case 0: return launch_gemm_f16<256, 128, 4, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 1: return launch_gemm_f16<192, 192, 2, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 2: return launch_gemm_f16<128, 128, 2, 2, 4, 2>(a, b, d, M, N, K, st);
+    case 3: return launch_gemm_f16<128, 64, 2, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 4: return launch_gemm_f16<64, 64, 2, 2, 4, 2>(a, b, d, M, N, K, st);
+    case 5: return launch_gemm_f16<128, 256, 2, 4, 3, 2>(a, b, d, M, N, K, st);
+    case 6: return launch_gemm_f16<96, 128, 2, 2, 4, 2>(a, b, d, M, N, K, st);
+    case 7: return launch_gemm_f16<128, 192, 2, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 8: return launch_gemm_f16<192, 128, 2, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 9: return launch_gemm_f16<64, 128, 2, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 10: return launch_gemm_f16<192, 192, 2, 4, 3, 2>(a, b, d, M, N, K, st);
+    case 11: return launch_gemm_f16<192, 192, 4, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 12: return launch_gemm_f16<128, 128, 2, 4, 4, 2>(a, b, d, M, N, K, st);
+    case 13: return launch_gemm_f16<128, 192, 2, 4, 3, 2>(a, b, d, M, N, K, st);
+    case 14: return launch_gemm_f16<192, 128, 4, 2, 3, 2>(a, b, d, M, N, K, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+// Choose the configuration with the least estimated time: rounds of
+// workgroups over the CUs, each round a fixed ~3 us (launch, pipeline fill,
+// output store) plus the work of the tiles one CU holds at that tile's
+// sustained MFMA efficiency.
+int choose_cfg(int M, int N, int K, int num_cus) {
+  int best = 4;
+  double best_t = 1e300;
+  for (int c = 0; c < N_F16_CFGS; ++c) {
+    const F16Cfg &f = F16_CFGS[c];
+    const long tiles = ((M + f.bm - 1) / f.bm) * (long)((N + f.bn - 1) / f.bn);
+    const long slots = (long)num_cus * f.per_cu;
+    const long rounds = (tiles + slots - 1) / slots;
+    const long held = std::min<long>(f.per_cu, (tiles + num_cus - 1) / num_cus);
+    const double t = rounds * (3e-6 + held * 2.0 * f.bm * f.bn * K / (9.83e12 * f.eff));
+    if (t < best_t) {
+      best_t = t;
+      best = c;
+    }
+  }
+  return best;
+}
+}  // namespace
+
 hipError_t rk_launch_gemm_f16(const void *A, const void *B, void *C, int M, int N, int K,
                               int num_cus, hipStream_t st) {
-  const f16 *a = (const f16 *)A;
-  const f16 *b = (const f16 *)B;
-  f16 *c = (f16 *)C;
-  const long t128 = ((M + 127) / 128) * (long)((N + 127) / 128);
-  if (t128 >= num_cus) return launch_gemm_f16<128, 128, 2, 2, 3>(a, b, c, M, N, K, st);
-  const long t64x96 = ((M + 63) / 64) * (long)((N + 95) / 96);
-  if (N % 96 == 0 && t64x96 >= num_cus / 2)
-    return launch_gemm_f16<64, 96, 2, 2, 4>(a, b, c, M, N, K, st);
-  return launch_gemm_f16<64, 64, 2, 2, 4>(a, b, c, M, N, K, st);
+  const int c = rk_knob("RK_F16_TILE", -1);
+  return launch_cfg(c >= 0 && c < N_F16_CFGS ? c : choose_cfg(M, N, K, num_cus), (const f16 *)A,
+                    (const f16 *)B, (f16 *)C, M, N, K, st);
 }

@@ -299,31 +299,6 @@ static hipError_t launch_i8(const I8GemmArgs &g, hipStream_t st) {
 // each, wave64) against 32 cycles per 32x32x32 MFMA for 1024 elements, so the
 // scaled mode is VALU-bound at 1/4 of the int8 MFMA rate.
 // ---------------------------------------------------------------------------
-namespace {
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-// Raw buffer descriptor word 3 for gfx9: 32-bit data format, no swizzle.
-constexpr int RSRC_WORD3 = 0x00020000;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
-  const int64_t b = bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)b, RSRC_WORD3);
-}
-// 16-byte buffer→LDS copy: lane i lands at lds_base + 16·i.
-__device__ __forceinline__ void bdma16(rsrc_t r, void *lds_base, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds_base), 16, voff, soff, 0, 0);
-}
-template <int V>
-using ic = std::integral_constant<int, V>;
-template <typename F, int... U>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, U...>) {
-  (f(ic<U>{}), ...);
-}
-// f(ic<0>{}), ..., f(ic<N-1>{}) in order.
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-}  // namespace
 
 template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2>
 __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
