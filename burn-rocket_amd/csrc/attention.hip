@@ -4,53 +4,55 @@
 // host f32 softmax, AV matmul; crates/rocket-npu/src/attn/mod.rs:1541-1600) and
 // the host layout passes around it (fill_heads / fill_heads_transposed /
 // unpack_heads, ext.rs:2174-2220): Q, K and O are read and written in the
-// caller's token-major layout; only V is rewritten, once per call, into the
-// transposed layout the PV product consumes (the reference's own V layout,
-// [KV][D][n_kv], with keys permuted inside each 16-key chunk).
+// caller's layout; only V is rewritten, once per call, into the transposed
+// layout the PV product consumes (the reference's own V layout, [KV][D][n_kv],
+// with keys permuted inside each 32-key chunk).
 //
-// One workgroup = one query tile of one KV head, covering all G = H/KV query
-// heads that read it: 4 waves × 32 rows, row r ↔ (head g = r / BQ, query
-// qt·BQ + r % BQ). K/V tiles of 64 keys are staged once in LDS and used by all
-// G·BQ rows.
+// Work decomposition. A workgroup owns one KV head and a query tile of 128
+// rows, row r ↔ (query head g = r / BQ of the group, query qt·BQ + r % BQ),
+// BQ = 128 / G, so every K/V tile staged in LDS serves all G query heads that
+// read it. Its 8 waves form two key groups of 4 waves; wave w of a group owns
+// rows 32w..32w+31 and the group walks every other 64-key tile (group 0 the
+// even tiles, group 1 the odd ones). The two partial softmax states are
+// merged through LDS at the end. Two waves per SIMD let one wave's softmax
+// VALU work overlap the other's MFMAs. Query tiles are dispatched from the
+// last one down, so under a causal mask the longest tiles start first and the
+// short ones fill in behind them.
 //
-// Per wave and 32-key block the kernel computes Sᵀ = K·Qᵀ with
-// v_mfma_f32_32x32x16_f16 (A = K rows from LDS, B = Q fragment held in VGPRs),
-// so each lane owns one query column and 16 of its keys; the row max and row
-// sum are in-lane plus one exchange with lane ^ 32. P is converted to fp16 in
-// registers and fed straight back as the B operand of Oᵀ = Vᵀ·Pᵀ (A = Vᵀ rows
-// from LDS); Oᵀ keeps the same query-per-lane ownership, so the online-softmax
-// rescale is a per-lane scalar.
+// Per wave and 64-key tile (v_mfma_f32_16x16x32_f16 throughout):
+//   Sᵀ = K·Qᵀ   A = K rows from LDS, B = Q fragments held in VGPRs; a lane
+//               owns one query column (lane % 16 of each 16-query block) and
+//               keys 4·(lane/16)+e of each 16-key block, so the row max is
+//               in-lane plus two lane swaps (v_permlane16/32_swap);
+//   P          exp2 of the scaled scores, split into an unevaluated sum of
+//               two fp16 values (hi = top 11 bits of the f32 probability, lo =
+//               the rest): fp16-rounded P alone leaves ~2^-12 relative noise
+//               per probability, above the parity gate for small outputs;
+//   Oᵀ += Vᵀ·Pᵀ A = Vᵀ rows from LDS, B = P hi and lo; Oᵀ keeps the query per
+//               lane, so the online-softmax rescale is a per-lane scalar.
 //
-// Masks are predicates on absolute positions (masks.rs:11-114); key tiles that
-// no row of the workgroup can see are skipped. Scores follow fa_score
+// LDS: per group two buffers of {K tile: 64 rows of 2·DQ+16 bytes (an odd
+// multiple of 16, so 16 consecutive rows read at one column hit 16 distinct
+// bank groups), Vᵀ tile: DV rows of 64 key slots with 16-byte chunk c of row
+// r at c ^ ((r & 7) ^ ((r >> 3) & 1))}, filled by buffer→LDS copies; keys
+// past n_kv and head columns past D read as zeros.
+//
+// Masks are predicates on absolute positions (masks.rs:11-114); key tiles
+// that no row of the tile can see are skipped. Scores follow fa_score
 // (attn/oneshot.rs:193-199) without the lower clamp for visible keys: masked
-// keys score -30000 only in workgroups holding a row with no visible key at
-// all, which then sweep every key so such a row averages V over all n_kv keys
+// keys score -30000 only in tiles holding a row with no visible key at all,
+// which then sweep every key so such a row averages V over all n_kv keys
 // (flash_attn_ref, attn/oneshot.rs:118-127).
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace {
 
-constexpr int BK = 64;         // keys per tile
-constexpr int NWAVES = 4;      // waves per workgroup
-constexpr int ROWS = NWAVES * 32;
+constexpr int BK = 64;          // keys per tile
+constexpr int ROWS = 128;       // query rows per workgroup tile
+constexpr int NWAVES = 8;       // 2 key groups × 4 waves
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float MASKED_SCORE = -30000.0f;  // fa_score clamp (attn/softmax.rs:59)
-
-// Does absolute query t see absolute key j?
-__device__ __forceinline__ bool visible(int mode, int64_t w, int64_t t, int64_t j) {
-  switch (mode) {
-    case RK_MASK_CAUSAL:
-      return j <= t;
-    case RK_MASK_WINDOW:
-      return (t - j <= w) && (j - t <= w);
-    case RK_MASK_CAUSAL_WINDOW:
-      return j <= t && t - j < w;
-    default:
-      return true;
-  }
-}
 
 // Visible absolute key interval [lo, hi] of query t (hi may exceed the keys).
 __device__ __forceinline__ void vis_range(int mode, int64_t w, int64_t t, int64_t &lo,
@@ -75,267 +77,417 @@ __device__ __forceinline__ void vis_range(int mode, int64_t w, int64_t t, int64_
   }
 }
 
+// max over lanes l, l^16, l^32, l^48 (the four lane groups holding one query).
+__device__ __forceinline__ float max4groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum4groups(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int D>
+struct AttnGeom {
+  static constexpr int DQ = (D + 15) / 16 * 16;  // padded head dim
+  static constexpr int NQC = DQ / 32;            // 32-wide d chunks of QKᵀ
+  static constexpr bool TAIL16 = (DQ % 32) != 0;  // one 16-wide chunk (x16 MFMA)
+  static constexpr int DV = DQ;
+  static constexpr int NDB = DV / 16;            // 16-row d blocks of Oᵀ
+  static constexpr int KROW = 2 * DQ + 16;       // bytes per K row in LDS
+  static constexpr int KCPR = DQ / 8 + 1;        // 16-byte chunks per K row (last: pad)
+  static constexpr int K_BYTES = BK * KROW;
+  static constexpr int V_BYTES = DV * 128;
+  static constexpr int BUF_BYTES = K_BYTES + V_BYTES;
+  static constexpr int K_INS = KCPR;              // 1 KB copies per K tile (64·KCPR chunks)
+  static constexpr int V_INS = DV / 8;            // 8 rows per copy
+  static constexpr int CPW = (K_INS + V_INS + 3) / 4;  // copies per wave of a group
+  static constexpr int SMEM = 4 * BUF_BYTES;          // 2 groups × 2 buffers
+};
+
 }  // namespace
 
-template <int DQ, int DV, bool SOFTCAP>
-__global__ __launch_bounds__(NWAVES * 64) void attn_fwd_kernel(AttnArgs a, int G, int BQ,
-                                                           int n_qtiles) {
-  static_assert(DQ % 16 == 0 && DV % 32 == 0, "head padding");
-  constexpr int KROW = DQ + 8;   // halfs per K row in LDS (16-byte pad)
-  constexpr int VROW = BK + 8;   // halfs per Vᵀ row in LDS
-  constexpr int K_TILE = BK * KROW;
-  constexpr int V_TILE = DV * VROW;
-  constexpr int NQC = DQ / 16;   // Q fragments (K=16 each)
-  constexpr int NDB = DV / 32;   // output d-blocks
-  constexpr int THREADS = NWAVES * 64;
-  constexpr int K_CHUNKS = BK * DQ / 8;
-  constexpr int V_CHUNKS = DV * BK / 8;
-  constexpr int K_PER = (K_CHUNKS + THREADS - 1) / THREADS;
-  constexpr int V_PER = (V_CHUNKS + THREADS - 1) / THREADS;
+template <int D, bool SOFTCAP>
+__global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int G, int BQ,
+                                                                 int n_qtiles) {
+  using Gm = AttnGeom<D>;
+  constexpr int DQ = Gm::DQ, NQC = Gm::NQC, NDB = Gm::NDB, DV = Gm::DV;
+  constexpr bool TAIL16 = Gm::TAIL16;
+  constexpr int KROW = Gm::KROW, KCPR = Gm::KCPR;
+  constexpr int K_BYTES = Gm::K_BYTES, BUF_BYTES = Gm::BUF_BYTES;
+  constexpr int K_INS = Gm::K_INS, V_INS = Gm::V_INS, CPW = Gm::CPW;
+  static_assert(Gm::SMEM <= 160 * 1024, "LDS");
 
-  __shared__ __attribute__((aligned(16))) f16 sK[2][K_TILE];
-  __shared__ __attribute__((aligned(16))) f16 sV[2][V_TILE];
-  __shared__ int s_flags[2];
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_flag;
 
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wq = wave & 3;
   const int KV = a.n_kv_heads;
   const int kvh = blockIdx.x % KV;
-  const int qt = n_qtiles - 1 - (int)(blockIdx.x / KV);  // heaviest causal tiles first
-  const int D = a.head_dim;
+  const int qt = n_qtiles - 1 - (int)(blockIdx.x / KV);  // longest causal tiles first
+  const int l16 = lane & 15, lg = lane >> 4;
 
-  // ---- this lane's query row
-  const int r = wave * 32 + (lane & 31);
-  const int hh = lane >> 5;
-  const int g = r / BQ;
-  const int qi = qt * BQ + (r % BQ);
-  const bool row_ok = (g < G) && (qi < a.n_q);
-  const int h = kvh * G + min(g, G - 1);
-  const int64_t t_abs = a.q0 + (row_ok ? qi : 0);
-
-  // ---- workgroup query range and degenerate-row check
-  const int q_lo = qt * BQ, q_hi = min(qt * BQ + BQ, a.n_q) - 1;
-  const int64_t t_min = a.q0 + q_lo, t_max = a.q0 + q_hi;
-  const int64_t kabs0 = a.k0, kabs1 = a.k0 + a.n_kv - 1;
-  if (threadIdx.x == 0) s_flags[0] = 0;
-  __syncthreads();
-  if (row_ok) {
-    int64_t lo, hi;
-    vis_range(a.mask_mode, a.window, t_abs, lo, hi);
-    if (max(lo, kabs0) > min(hi, kabs1)) s_flags[0] = 1;  // no visible key
-  }
-  __syncthreads();
-  const bool degenerate = s_flags[0] != 0;
-
-  int kt_begin = 0, kt_end = (a.n_kv + BK - 1) / BK;
-  int64_t full_lo = kabs0, full_hi = kabs1;  // keys visible to every row
-  {
-    int64_t lo_a, hi_a, lo_b, hi_b;
-    vis_range(a.mask_mode, a.window, t_min, lo_a, hi_a);
-    vis_range(a.mask_mode, a.window, t_max, lo_b, hi_b);
-    full_lo = max(lo_b, kabs0);
-    full_hi = min(hi_a, kabs1);
-    if (!degenerate) {
-      const int64_t any_lo = max(lo_a, kabs0) - a.k0;  // relative key indices
-      const int64_t any_hi = min(hi_b, kabs1) - a.k0;
-      kt_begin = (int)(max(any_lo, (int64_t)0) / BK);
-      kt_end = (int)min((any_hi / BK) + 1, (int64_t)kt_end);
-    }
-  }
-  const float masked_x = degenerate ? MASKED_SCORE * LOG2E : -INFINITY;
-
-  // ---- Q fragments (B operand of Sᵀ = K·Qᵀ): d = 16c + 8·hh + 0..7
-  half8 qf[NQC];
-  {
-    const f16 *qrow = (const f16 *)a.q + (int64_t)(row_ok ? qi : 0) * a.q_tok_stride +
-                      (int64_t)h * a.q_head_stride;
-#pragma unroll
-    for (int c = 0; c < NQC; ++c) {
-      const int d0 = 16 * c + 8 * hh;
-      if (row_ok && d0 < D)
-        qf[c] = *(const half8 *)(qrow + d0);
-      else
-        qf[c] = half8{};
-    }
-  }
-
-  // ---- K / Vᵀ tile staging (global → VGPR → LDS)
+  // ---- copy geometry (per wave of a group, constant over tiles)
   const f16 *kbase = (const f16 *)a.k + (int64_t)kvh * a.k_head_stride;
+  const rsrc_t rk =
+      make_rsrc(kbase, ((int64_t)(a.n_kv - 1) * a.k_tok_stride + D) * 2);
   const f16 *vtbase = (const f16 *)a.vt + (int64_t)kvh * DV * a.n_kv_pad;
-  uintx4 kreg[K_PER], vreg[V_PER];
-  auto load_tile = [&](int kt) {
-    const int kb = kt * BK;
-#pragma unroll
-    for (int i = 0; i < K_PER; ++i) {
-      const int cidx = i * THREADS + threadIdx.x;
-      const int key = cidx / (DQ / 8), ch = cidx % (DQ / 8);
-      uintx4 v = {0u, 0u, 0u, 0u};
-      if (cidx < K_CHUNKS && ch * 8 < D) {
-        const int kk = min(kb + key, a.n_kv - 1);
-        v = *(const uintx4 *)(kbase + (int64_t)kk * a.k_tok_stride + ch * 8);
-      }
-      kreg[i] = v;
+  const rsrc_t rv = make_rsrc(vtbase, (int64_t)DV * a.n_kv_pad * 2);
+  const uint32_t kstride_b = (uint32_t)(a.k_tok_stride * 2);  // bytes between keys
+  const uint32_t vrow_b = (uint32_t)(a.n_kv_pad * 2);         // bytes between Vᵀ rows
+  // Per-lane byte offset of copy c (recomputed at issue time: a few integer
+  // ops, instead of keeping one VGPR per copy live through the loop).
+  auto copy_voff = [&](int c) -> uint32_t {
+    if (c < K_INS) {
+      const int p = 64 * c + lane, row = p / KCPR, ch = p - row * KCPR;
+      return (ch < D / 8) ? (uint32_t)row * kstride_b + (uint32_t)(ch * 16) : OOB_OFFSET;
     }
-#pragma unroll
-    for (int i = 0; i < V_PER; ++i) {
-      const int cidx = i * THREADS + threadIdx.x;
-      const int d = cidx / (BK / 8), ch = cidx % (BK / 8);
-      uintx4 v = {0u, 0u, 0u, 0u};
-      if (cidx < V_CHUNKS) v = *(const uintx4 *)(vtbase + (int64_t)d * a.n_kv_pad + kb + ch * 8);
-      vreg[i] = v;
-    }
+    const int d = 8 * (c - K_INS) + (lane >> 3);
+    const int lch = (lane & 7) ^ ((d & 7) ^ ((d >> 3) & 1));
+    return (uint32_t)d * vrow_b + (uint32_t)(lch * 16);
   };
-  auto store_tile = [&](int buf) {
+  // Copies of the K part of key tile tk into buffer bk and of the Vᵀ part of
+  // key tile tv into buffer bv of this wave's group (a tile < 0: no copy).
+  auto issue = [&](int tk, int bk, int tv, int bv) {
 #pragma unroll
-    for (int i = 0; i < K_PER; ++i) {
-      const int cidx = i * THREADS + threadIdx.x;
-      if (cidx < K_CHUNKS) {
-        const int key = cidx / (DQ / 8), ch = cidx % (DQ / 8);
-        *(uintx4 *)(&sK[buf][key * KROW + ch * 8]) = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < V_PER; ++i) {
-      const int cidx = i * THREADS + threadIdx.x;
-      if (cidx < V_CHUNKS) {
-        const int d = cidx / (BK / 8), ch = cidx % (BK / 8);
-        *(uintx4 *)(&sV[buf][d * VROW + ch * 8]) = vreg[i];
+    for (int i = 0; i < CPW; ++i) {
+      const int c = wq + 4 * i;  // wave-uniform
+      if (c < K_INS) {
+        if (tk >= 0)
+          bdma16(rk, smem + (grp * 2 + bk) * BUF_BYTES + c * 1024, copy_voff(c),
+                 (uint32_t)tk * (BK * kstride_b));
+      } else if (c < K_INS + V_INS) {
+        if (tv >= 0)
+          bdma16(rv, smem + (grp * 2 + bv) * BUF_BYTES + K_BYTES + (c - K_INS) * 1024, copy_voff(c),
+                 (uint32_t)(tv * BK * 2));
       }
     }
   };
 
-  floatx16 o[NDB];
+  // ---- LDS fragment addresses (within a buffer)
+  const uint32_t k_off = (uint32_t)(l16 * KROW + lg * 16);  // + kb·16·KROW + c·64
+  const uint32_t k_off16 = (uint32_t)(l16 * KROW + NQC * 64 + lg * 8);
+  const int vf = (l16 & 7) ^ (l16 >> 3);
+  uint32_t v_off[2];  // per 32-key chunk c2; + db·16·128
 #pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m_run = -INFINITY;  // running max (exp2 domain), same on lane and lane^32
-  float l_run = 0.f;        // this lane's partial row sum
+  for (int c2 = 0; c2 < 2; ++c2) v_off[c2] = (uint32_t)(K_BYTES + l16 * 128 + (((4 * c2 + lg) ^ vf) << 4));
+
   const float C = SOFTCAP ? LOG2E : a.scale * LOG2E;
+  const int n_kt = (a.n_kv + BK - 1) / BK;
+  {
 
-  if (kt_begin < kt_end) {
-    load_tile(kt_begin);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int kt = kt_begin; kt < kt_end; ++kt) {
-    const int buf = (kt - kt_begin) & 1;
-    if (kt + 1 < kt_end) load_tile(kt + 1);
-
-    // Sᵀ for the two 32-key blocks of the tile.
-    floatx16 s[2];
+    // ---- this lane's query rows (two 16-query blocks)
+    int qi[2], hq[2];
+    bool rok[2];
+    int64_t tab[2];
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = wq * 32 + qb * 16 + l16;
+      const int g = r / BQ;
+      qi[qb] = qt * BQ + (r % BQ);
+      rok[qb] = (g < G) && (qi[qb] < a.n_q);
+      hq[qb] = kvh * G + min(g, G - 1);
+      tab[qb] = a.q0 + (rok[qb] ? qi[qb] : 0);
+    }
+
+    // ---- tile query range, key range, degenerate rows
+    const int q_lo = qt * BQ, q_hi = min(qt * BQ + BQ, a.n_q) - 1;
+    const int64_t t_min = a.q0 + q_lo, t_max = a.q0 + q_hi;
+    const int64_t kabs0 = a.k0, kabs1 = a.k0 + a.n_kv - 1;
+    if (threadIdx.x == 0) s_flag = 0;
+    __syncthreads();
+    if (grp == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
-      const f16 *krow = &sK[buf][(sb * 32 + (lane & 31)) * KROW + 8 * hh];
+      for (int qb = 0; qb < 2; ++qb) {
+        if (rok[qb]) {
+          int64_t lo, hi;
+          vis_range(a.mask_mode, a.window, tab[qb], lo, hi);
+          if (max(lo, kabs0) > min(hi, kabs1)) s_flag = 1;  // no visible key
+        }
+      }
+    }
+    __syncthreads();
+    const bool degenerate = s_flag != 0;
+    int kt_begin = 0, kt_end = n_kt;
+    int full_lo, full_hi;  // relative keys visible to every row of the tile
+    {
+      int64_t lo_a, hi_a, lo_b, hi_b;
+      vis_range(a.mask_mode, a.window, t_min, lo_a, hi_a);
+      vis_range(a.mask_mode, a.window, t_max, lo_b, hi_b);
+      full_lo = (int)min(max(lo_b - a.k0, (int64_t)0), (int64_t)a.n_kv);
+      full_hi = (int)max(min(hi_a - a.k0, (int64_t)a.n_kv - 1), (int64_t)-1);
+      if (!degenerate) {
+        const int64_t any_lo = max(lo_a, kabs0) - a.k0;  // relative key indices
+        const int64_t any_hi = min(hi_b, kabs1) - a.k0;
+        kt_begin = (int)(max(any_lo, (int64_t)0) / BK);
+        kt_end = (int)min((any_hi / BK) + 1, (int64_t)n_kt);
+      }
+    }
+    const float masked_x = degenerate ? MASKED_SCORE * LOG2E : -INFINITY;
+    // Visible keys of each of this lane's queries as a relative key interval
+    // [klo, khi] (every mask mode is an interval), clipped to [0, n_kv).
+    int klo[2], khi[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      int64_t lo, hi;
+      vis_range(a.mask_mode, a.window, tab[qb], lo, hi);
+      lo = max(lo - a.k0, (int64_t)0);
+      hi = min(hi - a.k0, (int64_t)a.n_kv - 1);
+      klo[qb] = rok[qb] ? (int)min(lo, (int64_t)a.n_kv) : a.n_kv;
+      khi[qb] = rok[qb] ? (int)max(hi, (int64_t)-1) : -1;
+    }
+
+    // ---- Q fragments (B operand of Sᵀ = K·Qᵀ): d = 32c + 8·lg + 0..7
+    half8 qf[2][NQC > 0 ? NQC : 1];
+    half4 qt16[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const f16 *qrow = (const f16 *)a.q + (int64_t)(rok[qb] ? qi[qb] : 0) * a.q_tok_stride +
+                        (int64_t)hq[qb] * a.q_head_stride;
 #pragma unroll
       for (int c = 0; c < NQC; ++c) {
-        const half8 kf = *(const half8 *)(krow + 16 * c);
-        s[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[c], s[sb], 0, 0, 0);
+        const int d0 = 32 * c + 8 * lg;
+        qf[qb][c] = (rok[qb] && d0 < D) ? *(const half8 *)(qrow + d0) : half8{};
+      }
+      if constexpr (TAIL16) {
+        const int d0 = 32 * NQC + 4 * lg;
+        qt16[qb] = (rok[qb] && d0 < D) ? *(const half4 *)(qrow + d0) : half4{};
       }
     }
 
-    // Scores in the exp2 domain with masking.
-    const int kb = kt * BK;
-    const bool interior = (a.k0 + kb >= full_lo) && (a.k0 + kb + BK - 1 <= full_hi) &&
-                          (kb + BK <= a.n_kv) && !degenerate;
-    float mt = -INFINITY;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = s[sb][i];
-        if constexpr (SOFTCAP) x = a.softcap * tanhf(x * a.scale / a.softcap);
-        x *= C;
-        if (!interior) {
-          const int key = kb + sb * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (key >= a.n_kv)
-            x = -INFINITY;
-          else if (!row_ok || !visible(a.mask_mode, a.window, t_abs, a.k0 + key))
-            x = masked_x;
-        }
-        s[sb][i] = x;
-        mt = fmaxf(mt, x);
-      }
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
-
-    // P as an unevaluated sum of two fp16 values: hi keeps the top 11 bits of
-    // the f32 probability (exactly representable, so the round-toward-zero
-    // pack is exact) and lo = p - hi carries the rest. Rounding P itself to
-    // fp16 would leave ~2^-12 relative noise per probability in O.
-    half8 phi[4], plo[4];
-    float lsum = 0.f;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        uintx4 hw, lw;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float e0 = __builtin_amdgcn_exp2f(s[sb][8 * c2 + 2 * j] - m_use);
-          const float e1 = __builtin_amdgcn_exp2f(s[sb][8 * c2 + 2 * j + 1] - m_use);
-          lsum += e0 + e1;
-          const float h0 = __uint_as_float(__float_as_uint(e0) & 0xffffe000u);
-          const float h1 = __uint_as_float(__float_as_uint(e1) & 0xffffe000u);
-          hw[j] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(h0, h1));
-          lw[j] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
-        }
-        phi[sb * 2 + c2] = __builtin_bit_cast(half8, hw);
-        plo[sb * 2 + c2] = __builtin_bit_cast(half8, lw);
-      }
-    }
-    l_run = l_run * alpha + lsum;
+    floatx4 o[NDB][2];
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      for (int qb = 0; qb < 2; ++qb) o[db][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY};  // running max (exp2 domain), per query
+    float l_run[2] = {0.f, 0.f};              // this lane's partial row sums
 
-    // Oᵀ += Vᵀ·Pᵀ over the four 16-key chunks (hi and lo parts).
+    // ---- key loop. Group g walks tiles kt_begin + 2j + g, j < nj. Its work
+    // alternates between an MFMA slot (PV of tile j-1, then Sᵀ of tile j) and
+    // a VALU slot (softmax of tile j); group 1 runs one slot behind group 0,
+    // so in every slot one wave of each SIMD multiplies while the other does
+    // the softmax. Slots are separated by workgroup barriers. K(j+1) and Vᵀ(j)
+    // are copied at the start of MFMA slot j (their buffers were last read in
+    // slot j-1) and waited for at the end of VALU slot j.
+    const int n_tiles = kt_end - kt_begin;
+    const int nj = (n_tiles - grp + 1) / 2;
+    const int nj_max = (n_tiles + 1) / 2;
+    floatx4 sacc[4][2];
+    half8 phi[2][2], plo[2][2];
+    // MFMA slot j: PV of tile j-1, Sᵀ of tile j.
+    auto mfma_slot = [&](int j) {
+    if (j < nj) issue(j + 1 < nj ? kt_begin + 2 * (j + 1) + grp : -1, (j + 1) & 1, kt_begin + 2 * j + grp, j & 1);
+    if (j >= 1 && j - 1 < nj) {
+      // Oᵀ += Vᵀ·Pᵀ for tile j-1 (hi and lo).
+      const uint8_t *vb = smem + (grp * 2 + ((j - 1) & 1)) * BUF_BYTES;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+      for (int c2 = 0; c2 < 2; ++c2) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const half8 vf =
-            *(const half8 *)(&sV[buf][(db * 32 + (lane & 31)) * VROW + 16 * c + 8 * hh]);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, phi[c], o[db], 0, 0, 0);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, plo[c], o[db], 0, 0, 0);
+        for (int db = 0; db < NDB; ++db) {
+          const half8 vf8 = *(const half8 *)(vb + v_off[c2] + db * 16 * 128);
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf8, phi[qb][c2], o[db][qb], 0, 0, 0);
+            o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf8, plo[qb][c2], o[db][qb], 0, 0, 0);
+          }
+        }
+      }
+      // Each fragment read two reads ahead of its four MFMAs.
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      static_for<2 * NDB - 2>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      });
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    }
+    // P of tile j-1 dies here, before S of tile j is produced (keeps the two
+    // register sets from overlapping).
+    __builtin_amdgcn_sched_barrier(0);
+    if (j < nj) {
+      // Sᵀ for the four 16-key blocks and two 16-query blocks of tile j.
+      const uint8_t *kbuf = smem + (grp * 2 + (j & 1)) * BUF_BYTES;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) sacc[kb][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NQC; ++c) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const half8 kf = *(const half8 *)(kbuf + k_off + kb * 16 * KROW + c * 64);
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[qb][c], sacc[kb][qb], 0, 0, 0);
+        }
+      }
+      if constexpr (TAIL16) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const half4 kf = *(const half4 *)(kbuf + k_off16 + kb * 16 * KROW);
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x16f16(kf, qt16[qb], sacc[kb][qb], 0, 0, 0);
+        }
+      }
+      // Each fragment read two reads ahead of its two MFMAs.
+      constexpr int NR = 4 * (NQC + (TAIL16 ? 1 : 0));
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      static_for<NR - 2>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      });
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    };
+    // VALU slot j: online softmax of tile j.
+    auto valu_slot = [&](int j) {
+    if (j < nj) {
+      const int kt = kt_begin + 2 * j + grp;
+      const int kb0 = kt * BK;
+      const bool interior = (kb0 >= full_lo) && (kb0 + BK - 1 <= full_hi) && !degenerate;
+      float mt[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = sacc[kb][qb][e];
+            if constexpr (SOFTCAP) x = a.softcap * tanhf(x * a.scale / a.softcap);
+            x *= C;
+            if (!interior) {
+              const int key = kb0 + kb * 16 + 4 * lg + e;
+              x = (key >= a.n_kv) ? -INFINITY : (key < klo[qb] || key > khi[qb]) ? masked_x : x;
+            }
+            sacc[kb][qb][e] = x;
+            mt[qb] = fmaxf(mt[qb], x);
+          }
+        }
+      }
+      // P hi/lo in the B-operand order of the PV product: chunk c2 =
+      // keys 32·c2.., slot 8·lg + i ↔ block 2·c2 + i/4, e = i%4.
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float m_t = max4groups(mt[qb]);
+        const float m_new = fmaxf(m_run[qb], m_t);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
+        m_run[qb] = m_new;
+        float lsum = 0.f;
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          uintx4 hw, lw;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int kb = 2 * c2 + (jj >> 1), e = 2 * (jj & 1);
+            const float e0 = __builtin_amdgcn_exp2f(sacc[kb][qb][e] - m_use);
+            const float e1 = __builtin_amdgcn_exp2f(sacc[kb][qb][e + 1] - m_use);
+            lsum += e0 + e1;
+            const float h0 = __uint_as_float(__float_as_uint(e0) & 0xffffe000u);
+            const float h1 = __uint_as_float(__float_as_uint(e1) & 0xffffe000u);
+            hw[jj] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(h0, h1));
+            lw[jj] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
+          }
+          phi[qb][c2] = __builtin_bit_cast(half8, hw);
+          plo[qb][c2] = __builtin_bit_cast(half8, lw);
+        }
+        l_run[qb] = l_run[qb] * alpha + lsum;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db][qb] *= alpha;
       }
     }
+    WAIT_VMCNT(0);  // K(j+1) and Vᵀ(j) land before the next MFMA slot
+    };
+    issue(nj > 0 ? kt_begin + grp : -1, 0, -1, 0);
+    WAIT_VMCNT(0);
+    BARRIER();
+    // One loop per group, so that only S (group 1) or only P (group 0) is
+    // live across a loop iteration; both make 2·nj_max + 2 barriers.
+    if (grp == 0) {
+      for (int j = 0; j <= nj_max; ++j) {
+        mfma_slot(j);
+        BARRIER();
+        valu_slot(j);
+        BARRIER();
+      }
+    } else {
+      BARRIER();
+      mfma_slot(0);
+      BARRIER();
+      for (int j = 0; j < nj_max; ++j) {
+        valu_slot(j);
+        BARRIER();
+        mfma_slot(j + 1);
+        BARRIER();
+      }
+    }
+    WAIT_VMCNT(0);
 
-    if (kt + 1 < kt_end) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  // ---- normalise and store Oᵀ: lane holds d = 32·db + 8·(i/4) + 4·hh + i%4
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  if (row_ok) {
-    f16 *orow = (f16 *)a.out + (int64_t)qi * a.o_tok_stride + (int64_t)h * a.o_head_stride;
+    // ---- merge the two key groups through LDS, normalise and store.
+    // Group 1 writes (m, l, Oᵀ) per lane; group 0 combines.
+    float *xch = (float *)smem + wq * 64 * (2 * 2 + NDB * 2 * 4);
+    BARRIER();  // all compute done: the K/V buffers are free
+    float lt[2];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+    for (int qb = 0; qb < 2; ++qb) lt[qb] = sum4groups(l_run[qb]);
+    if (grp == 1) {
+      float *p = xch + lane;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int d0 = 32 * db + 8 * i4 + 4 * hh;
-        if (d0 < D) {
-          half4 v = {(f16)(o[db][4 * i4 + 0] * inv), (f16)(o[db][4 * i4 + 1] * inv),
-                     (f16)(o[db][4 * i4 + 2] * inv), (f16)(o[db][4 * i4 + 3] * inv)};
-          *(half4 *)(orow + d0) = v;
+      for (int qb = 0; qb < 2; ++qb) {
+        p[(2 * qb) * 64] = m_run[qb];
+        p[(2 * qb + 1) * 64] = lt[qb];
+      }
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p[(4 + (db * 2 + qb) * 4 + e) * 64] = o[db][qb][e];
+    }
+    BARRIER();
+    if (grp == 0) {
+      const float *p = xch + lane;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float m1 = p[(2 * qb) * 64], l1 = p[(2 * qb + 1) * 64];
+        const float m = fmaxf(m_run[qb], m1);
+        const float mu = (m == -INFINITY) ? 0.f : m;
+        const float a0 = __builtin_amdgcn_exp2f(m_run[qb] - mu);
+        const float a1 = __builtin_amdgcn_exp2f(m1 - mu);
+        const float l = lt[qb] * a0 + l1 * a1;
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        if (rok[qb]) {
+          f16 *orow = (f16 *)a.out + (int64_t)qi[qb] * a.o_tok_stride + (int64_t)hq[qb] * a.o_head_stride;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const int d0 = db * 16 + 4 * lg;
+            if (d0 < D) {
+              half4 h;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float o1 = p[(4 + (db * 2 + qb) * 4 + e) * 64];
+                h[e] = (f16)((o[db][qb][e] * a0 + o1 * a1) * inv);
+              }
+              *(half4 *)(orow + d0) = h;
+            }
+          }
         }
       }
     }
   }
 }
 
-// V [n_kv] × (head g, d) → Vt[g][d][p] for p in [0, n_kv_pad), where position
-// p of each 16-key chunk holds key 8·((p%8)/4) + 4·(p/8 % 2) + p%4 of the
-// chunk (the order in which the PV operand lanes consume keys). Rows d ≥ D and
-// keys ≥ n_kv are zero.
+// V [n_kv] × (head g, d) → Vt[g][d][p] for p in [0, n_kv_pad): slot p of each
+// 32-key chunk holds key 4·(p/8 % 4) + p%4 + 16·((p%8)/4) of the chunk (the
+// order in which the PV operand lanes consume keys). Rows d ≥ D and keys ≥
+// n_kv are zero.
 __global__ void v_transpose_kernel(const f16 *__restrict__ v, int64_t tok_stride,
                                    int64_t head_stride, int64_t d_stride, int n_kv, int n_kv_pad,
                                    int D, int DVp, f16 *__restrict__ vt) {
@@ -355,14 +507,13 @@ __global__ void v_transpose_kernel(const f16 *__restrict__ v, int64_t tok_stride
     const int dd = idx / 64, p = idx % 64;
     const int d = d0 + dd;
     if (d >= DVp) continue;
-    const int pc = p & 15;
-    const int key_in_chunk = 8 * ((pc & 7) >> 2) + 4 * (pc >> 3) + (pc & 3);
-    const int kk = (p & ~15) + key_in_chunk;
+    const int pc = p & 31;
+    const int kk = (p & ~31) + 4 * ((pc >> 3) & 3) + (pc & 3) + 16 * ((pc & 7) >> 2);
     vt[((int64_t)g * DVp + d) * n_kv_pad + key0 + p] = tile[kk][dd];
   }
 }
 
-int rk_attn_dv_pad(int head_dim) { return (head_dim + 31) / 32 * 32; }
+int rk_attn_dv_pad(int head_dim) { return (head_dim + 15) / 16 * 16; }
 int rk_attn_kv_tile() { return BK; }
 
 hipError_t rk_launch_v_transpose(const void *v, int64_t v_tok_stride, int64_t v_head_stride,
@@ -384,18 +535,31 @@ hipError_t rk_launch_v_transpose_strided(const void *v, int64_t tok_stride, int6
   return hipGetLastError();
 }
 
-template <int DQ, int DV>
+template <int D>
 static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
   const int G = a.n_head / a.n_kv_heads;
   const int BQ = ROWS / G;
   const int n_qtiles = (a.n_q + BQ - 1) / BQ;
-  dim3 grid((unsigned)(n_qtiles * a.n_kv_heads));
+  const int grid = n_qtiles * a.n_kv_heads;
+  auto kern0 = attn_fa_kernel<D, false>;
+  auto kern1 = attn_fa_kernel<D, true>;
+  constexpr int smem = AttnGeom<D>::SMEM;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void *)kern0,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void *)kern1, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              smem);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
   if (a.softcap != 0.f)
-    hipLaunchKernelGGL((attn_fwd_kernel<DQ, DV, true>), grid, dim3(NWAVES * 64), 0, st, a, G, BQ,
+    hipLaunchKernelGGL(kern1, dim3((unsigned)grid), dim3(NWAVES * 64), smem, st, a, G, BQ,
                        n_qtiles);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<DQ, DV, false>), grid, dim3(NWAVES * 64), 0, st, a, G,
-                       BQ, n_qtiles);
+    hipLaunchKernelGGL(kern0, dim3((unsigned)grid), dim3(NWAVES * 64), smem, st, a, G, BQ,
+                       n_qtiles);
   return hipGetLastError();
 }
 
@@ -404,16 +568,17 @@ hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st) {
   if (G < 1 || G > ROWS || a.n_head % a.n_kv_heads) return hipErrorInvalidValue;
   switch (a.head_dim) {
     case 64:
-      return launch_attn<64, 64>(a, st);
+      return launch_attn<64>(a, st);
     case 72:
+      return launch_attn<72>(a, st);
     case 80:
-      return launch_attn<80, 96>(a, st);
+      return launch_attn<80>(a, st);
     case 96:
-      return launch_attn<96, 96>(a, st);
+      return launch_attn<96>(a, st);
     case 112:
-      return launch_attn<112, 128>(a, st);
+      return launch_attn<112>(a, st);
     case 128:
-      return launch_attn<128, 128>(a, st);
+      return launch_attn<128>(a, st);
   }
   return hipErrorInvalidValue;
 }
