@@ -53,6 +53,7 @@ constexpr int ROWS = 128;       // query rows per workgroup tile
 constexpr int NWAVES = 8;       // 2 key groups × 4 waves
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float MASKED_SCORE = -30000.0f;  // fa_score clamp (attn/softmax.rs:59)
+constexpr float RESCALE = 8.0f;  // log2 headroom before the running max is raised
 
 // Visible absolute key interval [lo, hi] of query t (hi may exceed the keys).
 __device__ __forceinline__ void vis_range(int mode, int64_t w, int64_t t, int64_t &lo,
@@ -285,23 +286,33 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
     auto mfma_slot = [&](int j) {
     if (j < nj) issue(j + 1 < nj ? kt_begin + 2 * (j + 1) + grp : -1, (j + 1) & 1, kt_begin + 2 * j + grp, j & 1);
     if (j >= 1 && j - 1 < nj) {
-      // Oᵀ += Vᵀ·Pᵀ for tile j-1 (hi and lo).
+      // Oᵀ += Vᵀ·Pᵀ for tile j-1: the hi products of one V fragment, then
+      // the lo products of the previous fragment, so that the two MFMAs into
+      // one accumulator are four MFMAs apart.
       const uint8_t *vb = smem + (grp * 2 + ((j - 1) & 1)) * BUF_BYTES;
+      constexpr int NF = 2 * NDB;  // fragments: f = c2·NDB + db
+      half8 vprev = half8{};
+      static_for<NF + 1>([&](auto f_c) {
+        constexpr int F = decltype(f_c)::value;
+        half8 vcur = half8{};
+        if constexpr (F < NF) {
+          constexpr int C2 = F / NDB, DB = F % NDB;
+          vcur = *(const half8 *)(vb + v_off[C2] + DB * 16 * 128);
 #pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const half8 vf8 = *(const half8 *)(vb + v_off[c2] + db * 16 * 128);
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf8, phi[qb][c2], o[db][qb], 0, 0, 0);
-            o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf8, plo[qb][c2], o[db][qb], 0, 0, 0);
-          }
+          for (int qb = 0; qb < 2; ++qb)
+            o[DB][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vcur, phi[qb][C2], o[DB][qb], 0, 0, 0);
         }
-      }
+        if constexpr (F > 0) {
+          constexpr int C2 = (F - 1) / NDB, DB = (F - 1) % NDB;
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            o[DB][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vprev, plo[qb][C2], o[DB][qb], 0, 0, 0);
+        }
+        vprev = vcur;
+      });
       // Each fragment read two reads ahead of its four MFMAs.
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      static_for<2 * NDB - 2>([&](auto) {
+      static_for<NF - 2>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       });
@@ -346,40 +357,69 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     }
     };
-    // VALU slot j: online softmax of tile j.
+    // VALU slot j: online softmax of tile j. Scores stay in the raw domain s
+    // (softcap applied in place) and the exp2 argument is always one FMA,
+    // s·C - m; on boundary tiles masked scores are first replaced in place by
+    // raw values that map to the masked value under that FMA. The running max is
+    // only raised (and O and l rescaled) when some query of the wave sees a score
+    // more than 2^RESCALE above it; otherwise P is taken against the stale max
+    // (values up to 2^RESCALE, exact after the final normalisation).
     auto valu_slot = [&](int j) {
-    if (j < nj) {
-      const int kt = kt_begin + 2 * j + grp;
-      const int kb0 = kt * BK;
-      const bool interior = (kb0 >= full_lo) && (kb0 + BK - 1 <= full_hi) && !degenerate;
-      float mt[2] = {-INFINITY, -INFINITY};
+      if (j >= nj) return;
+      const int kb0 = (kt_begin + 2 * j + grp) * BK;
+      if constexpr (SOFTCAP) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+          for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float x = sacc[kb][qb][e];
-            if constexpr (SOFTCAP) x = a.softcap * tanhf(x * a.scale / a.softcap);
-            x *= C;
-            if (!interior) {
-              const int key = kb0 + kb * 16 + 4 * lg + e;
-              x = (key >= a.n_kv) ? -INFINITY : (key < klo[qb] || key > khi[qb]) ? masked_x : x;
-            }
-            sacc[kb][qb][e] = x;
-            mt[qb] = fmaxf(mt[qb], x);
-          }
-        }
+            for (int e = 0; e < 4; ++e)
+              sacc[kb][qb][e] = a.softcap * tanhf(sacc[kb][qb][e] * a.scale / a.softcap);
       }
-      // P hi/lo in the B-operand order of the PV product: chunk c2 =
-      // keys 32·c2.., slot 8·lg + i ↔ block 2·c2 + i/4, e = i%4.
+      if (!((kb0 >= full_lo) && (kb0 + BK - 1 <= full_hi) && !degenerate)) {
+        const float masked_raw = masked_x / C;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int key = kb0 + kb * 16 + 4 * lg + e;
+              const float v = sacc[kb][qb][e];
+              sacc[kb][qb][e] =
+                  (key >= a.n_kv) ? -INFINITY : (key < klo[qb] || key > khi[qb]) ? masked_raw : v;
+            }
+      }
+      float mt[2];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        const float m_t = max4groups(mt[qb]);
-        const float m_new = fmaxf(m_run[qb], m_t);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
-        m_run[qb] = m_new;
+        float m = sacc[0][qb][0];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (kb | e) m = fmaxf(m, sacc[kb][qb][e]);
+        mt[qb] = max4groups(m) * C;
+      }
+      // Raise the running max (wave-uniform decision).
+      const bool up = mt[0] > m_run[0] + RESCALE || mt[1] > m_run[1] + RESCALE;
+      if (__builtin_amdgcn_ballot_w64(up) != 0) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const float m_new = fmaxf(m_run[qb], mt[qb]);
+          const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+          m_run[qb] = m_new;
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) o[db][qb] *= alpha;
+        }
+      }
+      // P = exp2(s·C - m) as hi + lo fp16 halves, in the B-operand order of the
+      // PV product: chunk c2 = keys 32·c2.., slot 8·lg + i ↔ block 2·c2 + i/4,
+      // e = i%4.
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float nm = (m_run[qb] == -INFINITY) ? 0.f : -m_run[qb];
         float lsum = 0.f;
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
@@ -387,23 +427,20 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
             const int kb = 2 * c2 + (jj >> 1), e = 2 * (jj & 1);
-            const float e0 = __builtin_amdgcn_exp2f(sacc[kb][qb][e] - m_use);
-            const float e1 = __builtin_amdgcn_exp2f(sacc[kb][qb][e + 1] - m_use);
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][e], C, nm));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][e + 1], C, nm));
             lsum += e0 + e1;
-            const float h0 = __uint_as_float(__float_as_uint(e0) & 0xffffe000u);
-            const float h1 = __uint_as_float(__float_as_uint(e1) & 0xffffe000u);
-            hw[jj] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(h0, h1));
-            lw[jj] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(e0 - h0, e1 - h1));
+            const auto h = __builtin_amdgcn_cvt_pkrtz(e0, e1);
+            hw[jj] = __builtin_bit_cast(unsigned int, h);
+            lw[jj] = __builtin_bit_cast(unsigned int,
+                                        __builtin_amdgcn_cvt_pkrtz(e0 - (float)h[0], e1 - (float)h[1]));
           }
           phi[qb][c2] = __builtin_bit_cast(half8, hw);
           plo[qb][c2] = __builtin_bit_cast(half8, lw);
         }
-        l_run[qb] = l_run[qb] * alpha + lsum;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) o[db][qb] *= alpha;
+        l_run[qb] += lsum;
       }
-    }
-    WAIT_VMCNT(0);  // K(j+1) and Vᵀ(j) land before the next MFMA slot
+      WAIT_VMCNT(0);  // K(j+1) and Vᵀ(j) land before the next MFMA slot
     };
     issue(nj > 0 ? kt_begin + grp : -1, 0, -1, 0);
     WAIT_VMCNT(0);
