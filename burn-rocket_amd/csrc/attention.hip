@@ -524,29 +524,50 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
 // V [n_kv] × (head g, d) → Vt[g][d][p] for p in [0, n_kv_pad): slot p of each
 // 32-key chunk holds key 4·(p/8 % 4) + p%4 + 16·((p%8)/4) of the chunk (the
 // order in which the PV operand lanes consume keys). Rows d ≥ D and keys ≥
-// n_kv are zero.
-__global__ void v_transpose_kernel(const f16 *__restrict__ v, int64_t tok_stride,
-                                   int64_t head_stride, int64_t d_stride, int n_kv, int n_kv_pad,
-                                   int D, int DVp, f16 *__restrict__ vt) {
-  __shared__ f16 tile[64][65];
+// n_kv are zero. A block moves a 64-key × 64-d tile: 16-byte loads along d
+// into LDS, 16-byte stores of 8 consecutive slots along the keys.
+__global__ __launch_bounds__(256) void v_transpose_kernel(const f16 *__restrict__ v,
+                                                          int64_t tok_stride, int64_t head_stride,
+                                                          int64_t d_stride, int n_kv, int n_kv_pad,
+                                                          int D, int DVp, f16 *__restrict__ vt) {
+  __shared__ f16 tile[64][64 + 2];
   const int g = blockIdx.z;
   const int key0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
   const f16 *vg = v + (int64_t)g * head_stride;
-  for (int idx = threadIdx.x; idx < 64 * 64; idx += blockDim.x) {
-    const int kk = idx / 64, dd = idx % 64;
-    const int key = key0 + kk, d = d0 + dd;
-    f16 val = (f16)0.f;
-    if (key < n_kv && d < D) val = vg[(int64_t)key * tok_stride + (int64_t)d * d_stride];
-    tile[kk][dd] = val;
+  if (d_stride == 1) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int idx = r * 256 + threadIdx.x;  // 64 keys × 8 chunks of 8 d
+      const int kk = idx >> 3, ch = idx & 7;
+      const int key = key0 + kk, d = d0 + ch * 8;
+      half8 x = half8{};
+      if (key < n_kv && d < D) x = *(const half8 *)(vg + (int64_t)key * tok_stride + d);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tile[kk][ch * 8 + i] = x[i];
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
+      const int kk = idx / 64, dd = idx % 64;
+      const int key = key0 + kk, d = d0 + dd;
+      tile[kk][dd] = (key < n_kv && d < D) ? vg[(int64_t)key * tok_stride + (int64_t)d * d_stride]
+                                           : (f16)0.f;
+    }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 64 * 64; idx += blockDim.x) {
-    const int dd = idx / 64, p = idx % 64;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int idx = r * 256 + threadIdx.x;  // 64 d rows × 8 chunks of 8 slots
+    const int dd = idx >> 3, ch = idx & 7;
     const int d = d0 + dd;
     if (d >= DVp) continue;
-    const int pc = p & 31;
-    const int kk = (p & ~31) + 4 * ((pc >> 3) & 3) + (pc & 3) + 16 * ((pc & 7) >> 2);
-    vt[((int64_t)g * DVp + d) * n_kv_pad + key0 + p] = tile[kk][dd];
+    half8 y;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int p = ch * 8 + i, pc = p & 31;
+      const int kk = (p & ~31) + 4 * ((pc >> 3) & 3) + (pc & 3) + 16 * ((pc & 7) >> 2);
+      y[i] = tile[kk][dd];
+    }
+    *(half8 *)(vt + ((int64_t)g * DVp + d) * n_kv_pad + key0 + ch * 8) = y;
   }
 }
 
