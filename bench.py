@@ -111,6 +111,77 @@ def run_headline(layers, steps, warmup):
     return ms, up_ms, wall
 
 
+COPY_PROBE_BYTES = 256 << 20
+TRAFFIC_LAUNCHES = 10
+
+
+def traffic_probe(layers, launches):
+    """Launches for the rocprofv3 --pmc byte counters: a plain device copy of
+    COPY_PROBE_BYTES (its FETCH_SIZE / WRITE_SIZE calibrate the counters), then
+    the up- and down-projection kernels `launches` times each."""
+    lib = rk.lib()
+    src, dst = rk.DeviceBuffer(COPY_PROBE_BYTES), rk.DeviceBuffer(COPY_PROBE_BYTES)
+    call(lib.rk_memset_dev(src.ptr, 1, COPY_PROBE_BYTES), "memset")
+    for _ in range(launches):
+        call(lib.rk_memcpy_dtod(dst.ptr, src.ptr, COPY_PROBE_BYTES, None), "copy")
+    rk.synchronize()
+    for L in layers:
+        for _ in range(launches):
+            gemm_w8a8(L)
+        rk.synchronize()
+    log(f"traffic probe: {launches} copies of {COPY_PROBE_BYTES} B, {launches} launches per projection")
+
+
+def pmc_summary(paths):
+    """Per-kernel HBM bytes per launch from rocprofv3 --pmc CSVs (FETCH_SIZE
+    and WRITE_SIZE in KiB per dispatch), each counter scaled by what it reads
+    for the probe copy of COPY_PROBE_BYTES. Writes profiles/traffic.json and
+    prints a markdown table."""
+    import csv
+    vals = {}
+    for path in paths:
+        rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
+        gemm = 0
+        for row in rows:
+            name = row["Kernel_Name"]
+            if "gemm_i8" in name:
+                # traffic_probe launches the up-projection `launches` times, then the down-projection
+                name = ("[up] " if gemm < TRAFFIC_LAUNCHES else "[down] ") + name
+                gemm += 1
+            key = (name, int(row["Grid_Size"]))
+            vals.setdefault(row["Counter_Name"], {}).setdefault(key, []).append(float(row["Counter_Value"]))
+    copy_kib = COPY_PROBE_BYTES / 1024.0
+    factor = {}
+    for ctr, per in vals.items():
+        copies = [v for (name, _), vs in per.items() if "copyBuffer" in name for v in vs]
+        factor[ctr] = (sum(copies) / len(copies)) / copy_kib if copies else 1.0
+    m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]
+    alg = {"w8a8_up": m * h + i * h + 4 * i * h // 32 + 4 * m + 4 * m * i,
+           "w8a8_down": m * i + h * i + 4 * h * i // 32 + 4 * m + 4 * m * h}
+    out, lines = {}, ["| kernel | grid | FETCH KiB | WRITE KiB | bytes/launch (calibrated) | algorithmic bytes |",
+                      "|---|---|---|---|---|---|"]
+    keys = sorted({k for per in vals.values() for k in per})
+    for name, grid in keys:
+        f = vals.get("FETCH_SIZE", {}).get((name, grid), [0.0])
+        w = vals.get("WRITE_SIZE", {}).get((name, grid), [0.0])
+        fk, wk = sum(f) / len(f), sum(w) / len(w)
+        bytes_ = 1024.0 * (fk / factor.get("FETCH_SIZE", 1.0) + wk / factor.get("WRITE_SIZE", 1.0))
+        tag = None
+        if name.startswith("[up]") or name.startswith("[down]"):
+            tag = "w8a8_up" if name.startswith("[up]") else "w8a8_down"
+            out[tag] = {"kernel": name[:120], "grid": grid, "fetch_kib": fk, "write_kib": wk,
+                        "bytes_per_launch": round(bytes_), "algorithmic_bytes": alg[tag]}
+        lines.append(f"| `{name[:80]}` | {grid} | {fk:.0f} | {wk:.0f} | {bytes_ / 1e6:.2f} MB | "
+                     f"{alg[tag] / 1e6 if tag else float('nan'):.2f} MB |")
+    out["calibration"] = {"copy_bytes": COPY_PROBE_BYTES, "fetch_factor": factor.get("FETCH_SIZE"),
+                          "write_factor": factor.get("WRITE_SIZE")}
+    with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as fh:
+        json.dump(out, fh, indent=1)
+    print("\n".join(lines))
+    print(f"\ncalibration: FETCH_SIZE reads {factor.get('FETCH_SIZE', 1.0):.4f}x and WRITE_SIZE "
+          f"{factor.get('WRITE_SIZE', 1.0):.4f}x the bytes of a {COPY_PROBE_BYTES >> 20} MiB device copy")
+
+
 def load_traffic(kernel_key):
     """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -284,11 +355,18 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only the launches the rocprofv3 --pmc byte counts are taken from")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="summarise rocprofv3 --pmc counter CSVs into profiles/traffic.json (no GPU)")
     a = ap.parse_args()
+    if a.pmc_summary:
+        pmc_summary(a.pmc_summary)
+        return
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported on this single-GPU build "
               "(the multi-GPU sharding is a design note only)", file=sys.stderr)
@@ -298,6 +376,9 @@ def main():
     name, cus, clk = rk.device_info()
     log(f"device {name}, {cus} CUs, {clk / 1e3:.0f} MHz")
     layers = setup_w8a8()
+    if a.traffic_probe:
+        traffic_probe(layers, TRAFFIC_LAUNCHES)
+        return
     log("W8A8 config ready; timing")
     ms, up_ms, wall = run_headline(layers, a.steps, a.warmup)
     m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]

@@ -70,6 +70,7 @@ SIGNATURES = {
     "rk_device_free": (_i, [_p]),
     "rk_memcpy_htod": (_i, [_p, _p, _sz]),
     "rk_memcpy_dtoh": (_i, [_p, _p, _sz]),
+    "rk_memcpy_dtod": (_i, [_p, _p, _sz, _p]),
     "rk_memset_dev": (_i, [_p, _i, _sz]),
     "rk_stream_get": (_i, [_p]),
     "rk_stream_sync": (_i, [_p]),

@@ -1237,6 +1237,14 @@ extern "C" int rk_memcpy_dtoh(void *dst, const void *src, size_t bytes) {
   HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "rk_memcpy_dtoh");
   return RK_OK;
 }
+extern "C" int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_memcpy_dtod"));
+  HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
+                         stream ? (hipStream_t)stream : g_eng->stream),
+          "rk_memcpy_dtod");
+  return RK_OK;
+}
 extern "C" int rk_memset_dev(void *dst, int value, size_t bytes) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_memset_dev"));

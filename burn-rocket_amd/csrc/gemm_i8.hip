@@ -315,10 +315,13 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   constexpr int STAGE_BYTES = CODE_BYTES + WS_BYTES;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int A_PER = BM / 8 / NW, B_PER = BN / 8 / NW;  // 8-row copies per wave
+  // Copies of 8 code rows (1 KiB) per stage: QA for A, QB for B, dealt
+  // round-robin to the waves (wave w issues copies w, w+NW, ...); QMIN is
+  // the smallest number any wave issues.
+  constexpr int QA = BM / 8, QB = BN / 8, QT = QA + QB;
+  constexpr int CP = (QT + NW - 1) / NW, QMIN = QT / NW;
   constexpr int WS_INS = SCALED ? BN / 64 : 0;            // 64 scale rows per copy
-  constexpr int L = A_PER + B_PER;                        // copies every wave issues
-  static_assert(A_PER * 8 * NW == BM && B_PER * 8 * NW == BN, "tile/wave split");
+  static_assert(QA % 2 == 0, "A copies keep the swizzle parity of B copies");
   static_assert(WS_INS <= NW && (!SCALED || WS_INS * 64 == BN), "scale split");
   static_assert(TM * 32 * WM == BM && TN * 32 * WN == BN, "mfma split");
 
@@ -332,6 +335,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT = (K + 127) / 128;
   const int KB = K / 32;
+  const int NBLK = KB;  // blocks the main loop steps through
 
   const rsrc_t ra = make_rsrc(A + (size_t)m0 * K, (int64_t)(M - m0) * K);
   const rsrc_t rw = make_rsrc(W + (size_t)n0 * K, (int64_t)(N - n0) * K);
@@ -354,14 +358,15 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     uint8_t *sb = smem + slot * STAGE_BYTES;
     const uint32_t k0 = kt * 128;
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i) {
-      const int q = wave * A_PER + i;
-      bdma16(ra, sb + q * 1024, (q & 1) ? voff_odd : voff_even, q * 8 * K + k0);
-    }
-#pragma unroll
-    for (int i = 0; i < B_PER; ++i) {
-      const int q = wave * B_PER + i;
-      bdma16(rw, sb + BM * ROWB + q * 1024, (q & 1) ? voff_odd : voff_even, q * 8 * K + k0);
+    for (int i = 0; i < CP; ++i) {
+      const int q = wave + i * NW;  // wave-uniform
+      if (CP * NW == QT || q < QT) {
+        const uint32_t voff = (q & 1) ? voff_odd : voff_even;
+        if (q < QA)
+          bdma16(ra, sb + q * 1024, voff, q * 8 * K + k0);
+        else
+          bdma16(rw, sb + BM * ROWB + (q - QA) * 1024, voff, (q - QA) * 8 * K + k0);
+      }
     }
     if constexpr (WS_INS > 0) {
       if (wave < WS_INS)
@@ -369,15 +374,16 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     }
   };
   // Make stage kt visible to every wave. Copies return in issue order, so
-  // waiting until at most L·later copies (the stages issued after kt) remain is
-  // enough even for the waves that also copy scales.
+  // waiting until at most QMIN·later copies (the stages issued after kt)
+  // remain is enough for every wave, also those that issue more copies per
+  // stage (code rows or scales): they wait for a few later copies as well.
   auto stage_ready = [&](int kt) {
     if constexpr (STAGES >= 3) {
       const int later = min(STAGES - 2, KT - 1 - kt);
       if (later >= 2) {
-        WAIT_VMCNT(L * 2);
+        WAIT_VMCNT(QMIN * 2);
       } else if (later == 1) {
-        WAIT_VMCNT(L);
+        WAIT_VMCNT(QMIN);
       } else {
         WAIT_VMCNT(0);
       }
@@ -440,9 +446,11 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   // one MFMA later: MFMA(u+1) is issued before the 32 VALU instructions that
   // fold tile u, so the MFMA of the next tile runs while the VALU folds the
   // previous one. The pending tile of a block is folded at the start of the
-  // next block. sched_barrier(0) fences keep this issue order.
+  // next block. sched_barrier(0) fences keep this issue order. Tile u of
+  // block B (B = block index mod 4) uses set (B·T + u) & 1; a loop iteration
+  // covers 4·STAGES blocks, an even count, so the sets alternate across
+  // iterations too.
   constexpr int T = TM * TN;
-  static_assert(!SCALED || (T % 2) == 0, "even tile count per wave");
   intx16 ires[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) ires[0][r] = ires[1][r] = 0;
@@ -461,7 +469,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     constexpr int NS = (B == 3) ? (S + 1) % STAGES : S, NB = (B + 1) & 3;
     const int gn = g + 1;
     if constexpr (B == 3) {
-      if (gn < KB) {
+      if (gn < NBLK) {
         const int kt = gn >> 2;
         stage_ready(kt);
         if (kt + STAGES - 1 < KT) issue(ic<S>{}, kt + STAGES - 1);
@@ -478,43 +486,52 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
         for (int j = 0; j < TN; ++j)
           iacc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][i], bf[CUR][j], iacc[i][j], 0, 0, 0);
     } else {
-      // The next block's fragments are read from LDS first (register set
-      // NXT is free: its MFMAs were all issued in the previous step), then
-      // tile 0 of this block, then the fold of the previous block's last tile.
+      // Tile 0 of this block first: its wait covers only the fragments read
+      // in the previous step. Then the next block's fragments are read from
+      // LDS (register set NXT is free: its MFMAs were all issued in the
+      // previous step) and have a whole step to arrive, then the fold of the
+      // previous block's last tile.
+      constexpr int P0 = (B * T) & 1;
       const float dlast = dsc[CUR][TN - 1];
+      ires[P0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bf[CUR][0], intx16{}, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
       load_frags(ic<NXT>{}, ic<NS>{}, ic<NB>{});
       __builtin_amdgcn_sched_barrier(0);
-      ires[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bf[CUR][0], intx16{}, 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      fold(ic<1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+      fold(ic<P0 ^ 1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
       __builtin_amdgcn_sched_barrier(0);
       // Tiles 1..T-1: MFMA of tile u, then the fold of tile u-1.
       static_for<T - 1>([&](auto uc) {
         constexpr int u = decltype(uc)::value + 1;
         constexpr int I = u / TN, J = u % TN;
         constexpr int PI = (u - 1) / TN, PJ = (u - 1) % TN;
-        ires[u & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][I], bf[CUR][J], intx16{}, 0, 0, 0);
+        ires[(P0 + u) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][I], bf[CUR][J], intx16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        fold(ic<(u - 1) & 1>{}, ic<PI>{}, ic<PJ>{}, dsc[CUR][PJ]);
+        fold(ic<(P0 + u - 1) & 1>{}, ic<PI>{}, ic<PJ>{}, dsc[CUR][PJ]);
         __builtin_amdgcn_sched_barrier(0);
       });
       dpend = dlast;
     }
   };
 
-  for (int g0 = 0; g0 < KB; g0 += 4 * STAGES) {
+  for (int g0 = 0; g0 < NBLK; g0 += 4 * STAGES) {
     auto stage = [&](auto s_c) {
       const int gs = g0 + 4 * decltype(s_c)::value;
-      if (gs + 0 < KB) step(gs + 0, s_c, ic<0>{});
-      if (gs + 1 < KB) step(gs + 1, s_c, ic<1>{});
-      if (gs + 2 < KB) step(gs + 2, s_c, ic<2>{});
-      if (gs + 3 < KB) step(gs + 3, s_c, ic<3>{});
+      if (gs + 0 < NBLK) step(gs + 0, s_c, ic<0>{});
+      if (gs + 1 < NBLK) step(gs + 1, s_c, ic<1>{});
+      if (gs + 2 < NBLK) step(gs + 2, s_c, ic<2>{});
+      if (gs + 3 < NBLK) step(gs + 3, s_c, ic<3>{});
     };
     stage(ic<0>{});
     if constexpr (STAGES > 1) stage(ic<1>{});
     if constexpr (STAGES > 2) stage(ic<2>{});
   }
-  if constexpr (SCALED) fold(ic<1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+  if constexpr (SCALED) {
+    // The last block's last tile sits in set ((NBLK-1)·T + T-1) & 1.
+    if (((NBLK * T - 1) & 1) != 0)
+      fold(ic<1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+    else
+      fold(ic<0>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+  }
 
   // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of column lane%32.
 #pragma unroll
@@ -564,13 +581,18 @@ static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Tile configurations of the per-token Q8_0 kernel. Default: 128x128 tiles on
-// 8 waves (2 workgroups and 4 waves per SIMD) when that fills every CU, else
-// 128x64 tiles on 4 waves. RK_Q8_TILE selects a configuration by number.
+// Tile configurations of the per-token Q8_0 kernel. Default, by the number of
+// 128x128 tiles against the CU count (measured on MI355X at M=3633: up
+// 3072x1024 29.9 us with 10, down 1024x3072 29.4 us with 15):
+//   >= 1 per CU:   128x128 tiles on 8 waves, 2 workgroups (4 waves per SIMD);
+//   >= 3/4 per CU: 128x128 tiles on 16 waves, one tile per CU (4 waves per SIMD);
+//   fewer:         128x64 tiles on 4 waves.
+// RK_Q8_TILE selects a configuration by number.
 template <bool OUT_F16>
 static hipError_t launch_q8_cfg(const I8GemmArgs &g, hipStream_t st) {
   const long t128 = ((g.M + 127) / 128) * (long)((g.N + 127) / 128);
-  switch (rk_knob("RK_Q8_TILE", t128 >= g.num_cus ? 10 : 0)) {
+  const int dflt = t128 >= g.num_cus ? 10 : (4 * t128 >= 3L * g.num_cus ? 15 : 0);
+  switch (rk_knob("RK_Q8_TILE", dflt)) {
     case 1:
       return launch_q8<128, 64, 2, 2, 3, MODE_PER_TOKEN, OUT_F16>(g, st);
     case 2:
@@ -595,6 +617,28 @@ static hipError_t launch_q8_cfg(const I8GemmArgs &g, hipStream_t st) {
       return launch_q8<256, 128, 4, 4, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
     case 12:
       return launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 13:
+      return launch_q8<256, 192, 8, 2, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 14:
+      return launch_q8<256, 64, 8, 2, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 15:
+      return launch_q8<128, 128, 4, 4, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 16:
+      return launch_q8<192, 128, 6, 2, 2, MODE_PER_TOKEN, OUT_F16, 3>(g, st);
+    case 17:
+      return launch_q8<128, 192, 4, 2, 2, MODE_PER_TOKEN, OUT_F16, 2>(g, st);
+    case 18:
+      return launch_q8<256, 128, 8, 2, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 19:
+      return launch_q8<128, 128, 4, 4, 3, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 20:
+      return launch_q8<256, 64, 8, 2, 3, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 21:
+      return launch_q8<256, 128, 8, 2, 3, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 22:
+      return launch_q8<128, 256, 4, 4, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
+    case 23:
+      return launch_q8<128, 128, 2, 4, 3, MODE_PER_TOKEN, OUT_F16, 2>(g, st);
     default:
       return launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
   }

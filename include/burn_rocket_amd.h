@@ -293,6 +293,8 @@ int rk_device_alloc(size_t bytes, void **ptr);
 int rk_device_free(void *ptr);
 int rk_memcpy_htod(void *dst, const void *src, size_t bytes);
 int rk_memcpy_dtoh(void *dst, const void *src, size_t bytes);
+/* Device-to-device copy, ordered on `stream` (NULL: the library stream). */
+int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_stream stream);
 int rk_memset_dev(void *dst, int value, size_t bytes);
 int rk_stream_get(rk_stream *stream);    /* the library stream */
 int rk_stream_sync(rk_stream stream);

@@ -170,6 +170,33 @@ def test_w8a8_edge_shapes(rk, orc, m, k, n):
     check(orc, got, ref)
 
 
+# Every tile configuration of the per-token Q8_0 kernel (RK_Q8_TILE): ragged
+# M and N against every tile size, an odd and an even number of 32-value
+# blocks (the pipeline alternates register sets per block) and a K tail that
+# ends inside a 128-value stage.
+Q8_TILES = list(range(24))
+
+
+@pytest.mark.parametrize("tile", Q8_TILES)
+def test_w8a8_every_tile_config(rk, orc, tile, monkeypatch):
+    monkeypatch.setenv("RK_Q8_TILE", str(tile))
+    for m, k, n in ((300, 416, 200), (257, 1024, 392)):
+        note(f"W8A8 RK_Q8_TILE={tile} m={m} k={k} n={n}")
+        r = np.random.default_rng(tile * 7 + m + k + n)
+        x = r.standard_normal((m, k)).astype(np.float32)
+        w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+        wq, wd = orc.q8_0_quantize(w)
+        wid = rk.pack_q8_0(orc.q8_0_blocks(wq, wd), n, k)
+        aq, a_s = orc.quantize_rows(x, k)
+        dq, ds = quantize_dev(rk, x, k)
+        ref = orc.emu_matmul_gw(aq, a_s, k, wq, wd.view(np.float16).astype(np.float32), 32)
+        for f16out in (False, True):
+            got = w8a8_dev(rk, wid, dq, ds, k, m, k, f16out)
+            check(orc, got, ref)
+            if not f16out:
+                assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
 @pytest.mark.parametrize("in_scale,out_scale", [(0.02, 0.0), (0.0, 0.0), (0.02, 0.05)])
 def test_qat_matmul_is_bit_exact(rk, orc, in_scale, out_scale):
     note(f"QAT in_scale={in_scale} out_scale={out_scale}")
