@@ -470,8 +470,8 @@ extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_
   HIP_TRY(hipMemsetAsync(wt.scales, 0, (size_t)n * wt.ws_stride * 4, g_eng->stream), "rk_pack_q8_0_f32");
   HIP_TRY(hipMemcpyAsync(x32, w, (size_t)n * k * 4, hipMemcpyHostToDevice, g_eng->stream),
           "rk_pack_q8_0_f32");
-  HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, n, k, 32, 0, (int8_t *)wt.codes, wt.scales,
-                                  wt.ws_stride, g_eng->stream),
+  HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, n, k, 16, 0, (int8_t *)wt.codes, wt.scales,
+                                  wt.ws_stride, false, g_eng->stream),
           "rk_pack_q8_0_f32");
   HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack_q8_0_f32");
   wt.bytes = (size_t)n * k + (size_t)n * wt.ws_stride * 4;
@@ -898,6 +898,26 @@ extern "C" int rk_moe_route(const float *logits, int64_t s, int n_experts, int t
   return RK_OK;
 }
 
+namespace {
+// Bytes of one expert's fragment-major codes (blocks per row padded to a
+// multiple of 4, q8_code_offset in kernels.hpp).
+int64_t moe_gu_code_stride(const Weight &w) { return 2 * w.inter * w.gu_ws_stride * 32; }
+int64_t moe_dn_code_stride(const Weight &w) { return w.hidden * w.dn_ws_stride * 32; }
+
+// Row-major codes [n, k] and scales [n, ws_stride] → fragment-major.
+void to_fragment_major(const int8_t *codes, const float *scales, int64_t n, int64_t k,
+                       int ws_stride, int8_t *fcodes, float *fscales) {
+  std::fill(fcodes, fcodes + n * ws_stride * 32, (int8_t)0);
+  std::fill(fscales, fscales + n * ws_stride, 0.f);
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t b = 0; b < k / 32; ++b) {
+      for (int j = 0; j < 32; ++j)
+        fcodes[q8_code_offset(r, b, j, k, ws_stride, 1)] = codes[r * k + b * 32 + j];
+      fscales[q8_scale_offset(r, b, ws_stride, 1)] = scales[r * ws_stride + b];
+    }
+}
+}  // namespace
+
 extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
                                 int n_experts, int64_t hidden, int64_t inter, rk_weight_id *id) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -915,17 +935,19 @@ extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const ui
   w.group = 32;
   w.gu_ws_stride = ws_stride_for(H);
   w.dn_ws_stride = ws_stride_for(I);
-  const size_t gu_codes = (size_t)E * 2 * I * H, dn_codes = (size_t)E * H * I;
+  const size_t gu_codes = (size_t)E * moe_gu_code_stride(w), dn_codes = (size_t)E * moe_dn_code_stride(w);
   const size_t gu_sc = (size_t)E * 2 * I * w.gu_ws_stride, dn_sc = (size_t)E * H * w.dn_ws_stride;
   HIP_TRY(hipMalloc((void **)&w.gu_codes, gu_codes), "rk_pack_moe_q8_0");
   HIP_TRY(hipMalloc((void **)&w.dn_codes, dn_codes), "rk_pack_moe_q8_0");
   HIP_TRY(hipMalloc((void **)&w.gu_scales, gu_sc * 4), "rk_pack_moe_q8_0");
   HIP_TRY(hipMalloc((void **)&w.dn_scales, dn_sc * 4), "rk_pack_moe_q8_0");
   w.bytes = gu_codes + dn_codes + (gu_sc + dn_sc) * 4;
-  // Per expert: parse gate/up/down, interleave gate|up per 32-row slice.
+  // Per expert: parse gate/up/down, interleave gate|up per 16-row slice.
   std::vector<int8_t> gc(I * H), uc(I * H), dc(H * I), guc(2 * I * H);
   std::vector<float> gs(I * (H / 32)), us(I * (H / 32)), ds(H * (I / 32));
   std::vector<float> gus((size_t)2 * I * w.gu_ws_stride), dss((size_t)H * w.dn_ws_stride);
+  std::vector<int8_t> guf(moe_gu_code_stride(w)), dnf(moe_dn_code_stride(w));
+  std::vector<float> gusf(gus.size()), dssf(dss.size());
   const size_t gblk = (size_t)I * (H / 32) * 34, dblk = (size_t)H * (I / 32) * 34;
   for (int64_t e = 0; e < E; ++e) {
     parse_q8_0(gate + e * gblk, I, H, gc.data(), gs.data());
@@ -934,8 +956,8 @@ extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const ui
     std::fill(gus.begin(), gus.end(), 0.f);
     std::fill(dss.begin(), dss.end(), 0.f);
     for (int64_t r = 0; r < I; ++r) {
-      const int64_t t = r / 32, j = r % 32;
-      const int64_t rg = 64 * t + j, ru = 64 * t + 32 + j;
+      const int64_t t = r / 16, j = r % 16;
+      const int64_t rg = 32 * t + j, ru = 32 * t + 16 + j;
       std::memcpy(&guc[rg * H], &gc[r * H], H);
       std::memcpy(&guc[ru * H], &uc[r * H], H);
       std::memcpy(&gus[rg * w.gu_ws_stride], &gs[r * (H / 32)], 4 * (H / 32));
@@ -943,14 +965,16 @@ extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const ui
     }
     for (int64_t r = 0; r < H; ++r)
       std::memcpy(&dss[r * w.dn_ws_stride], &ds[r * (I / 32)], 4 * (I / 32));
-    HIP_TRY(hipMemcpy(w.gu_codes + e * 2 * I * H, guc.data(), guc.size(), hipMemcpyHostToDevice),
+    to_fragment_major(guc.data(), gus.data(), 2 * I, H, w.gu_ws_stride, guf.data(), gusf.data());
+    to_fragment_major(dc.data(), dss.data(), H, I, w.dn_ws_stride, dnf.data(), dssf.data());
+    HIP_TRY(hipMemcpy(w.gu_codes + e * guf.size(), guf.data(), guf.size(), hipMemcpyHostToDevice),
             "rk_pack_moe_q8_0");
-    HIP_TRY(hipMemcpy(w.dn_codes + e * H * I, dc.data(), dc.size(), hipMemcpyHostToDevice),
+    HIP_TRY(hipMemcpy(w.dn_codes + e * dnf.size(), dnf.data(), dnf.size(), hipMemcpyHostToDevice),
             "rk_pack_moe_q8_0");
-    HIP_TRY(hipMemcpy(w.gu_scales + e * 2 * I * w.gu_ws_stride, gus.data(), gus.size() * 4,
+    HIP_TRY(hipMemcpy(w.gu_scales + e * 2 * I * w.gu_ws_stride, gusf.data(), gusf.size() * 4,
                       hipMemcpyHostToDevice),
             "rk_pack_moe_q8_0");
-    HIP_TRY(hipMemcpy(w.dn_scales + e * H * w.dn_ws_stride, dss.data(), dss.size() * 4,
+    HIP_TRY(hipMemcpy(w.dn_scales + e * H * w.dn_ws_stride, dssf.data(), dssf.size() * 4,
                       hipMemcpyHostToDevice),
             "rk_pack_moe_q8_0");
   }
@@ -970,12 +994,15 @@ int moe_alloc(Weight &w, int n_experts, int64_t H, int64_t I, const char *op) {
   w.gu_ws_stride = ws_stride_for(H);
   w.dn_ws_stride = ws_stride_for(I);
   const int64_t E = n_experts;
-  const size_t gu_codes = (size_t)E * 2 * I * H, dn_codes = (size_t)E * H * I;
+  const size_t gu_codes = (size_t)E * moe_gu_code_stride(w), dn_codes = (size_t)E * moe_dn_code_stride(w);
   const size_t gu_sc = (size_t)E * 2 * I * w.gu_ws_stride, dn_sc = (size_t)E * H * w.dn_ws_stride;
   HIP_TRY(hipMalloc((void **)&w.gu_codes, gu_codes), op);
   HIP_TRY(hipMalloc((void **)&w.dn_codes, dn_codes), op);
   HIP_TRY(hipMalloc((void **)&w.gu_scales, gu_sc * 4), op);
   HIP_TRY(hipMalloc((void **)&w.dn_scales, dn_sc * 4), op);
+  // Padding blocks of the fragment-major layout stay zero.
+  HIP_TRY(hipMemset(w.gu_codes, 0, gu_codes), op);
+  HIP_TRY(hipMemset(w.dn_codes, 0, dn_codes), op);
   HIP_TRY(hipMemset(w.gu_scales, 0, gu_sc * 4), op);
   HIP_TRY(hipMemset(w.dn_scales, 0, dn_sc * 4), op);
   w.bytes = gu_codes + dn_codes + (gu_sc + dn_sc) * 4;
@@ -995,20 +1022,22 @@ extern "C" int rk_pack_moe_f32(const float *gate, const float *up, const float *
   void *x32;
   RK_TRY(scratch("pack_f32", (size_t)I * H * 4, &x32));
   hipStream_t st = g_eng->stream;
+  const int64_t gu_stride = moe_gu_code_stride(w), dn_stride = moe_dn_code_stride(w);
   for (int64_t e = 0; e < E; ++e) {
-    int8_t *guc = w.gu_codes + e * 2 * I * H;
+    int8_t *guc = w.gu_codes + e * gu_stride;
     float *gus = w.gu_scales + e * 2 * I * w.gu_ws_stride;
     const float *src[3] = {gate + e * I * H, up + e * I * H, down + e * H * I};
     for (int part = 0; part < 3; ++part) {
       HIP_TRY(hipMemcpyAsync(x32, src[part], (size_t)I * H * 4, hipMemcpyHostToDevice, st),
               "rk_pack_moe_f32");
       if (part < 2)
-        HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, I, H, 64, 32 * part, guc, gus,
-                                        w.gu_ws_stride, st),
+        HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, I, H, 32, 16 * part, guc, gus,
+                                        w.gu_ws_stride, true, st),
                 "rk_pack_moe_f32");
       else
-        HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, H, I, 32, 0, w.dn_codes + e * H * I,
-                                        w.dn_scales + e * H * w.dn_ws_stride, w.dn_ws_stride, st),
+        HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, H, I, 16, 0, w.dn_codes + e * dn_stride,
+                                        w.dn_scales + e * H * w.dn_ws_stride, w.dn_ws_stride, true,
+                                        st),
                 "rk_pack_moe_f32");
     }
   }
@@ -1110,15 +1139,15 @@ int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipS
   RK_TRY(scratch("moe_yb", (size_t)std::max<int64_t>(R, 1) * H * 4, &yb));
   const char *op = "rk_moe_experts_dev";
   HIP_TRY(rk_launch_quantize_rows(x, S, H, H, (int8_t *)xq, (float *)xs, st), op);
-  HIP_TRY(rk_launch_moe_gemm_gu((const int8_t *)xq, (const float *)xs, plan.tok, plan.tiles,
-                                plan.n_tiles, w.gu_codes, w.gu_scales, 2 * I * H,
+  HIP_TRY(rk_launch_moe_gemm_gu((const int8_t *)xq, (const float *)xs, plan.tok, S, plan.tiles,
+                                plan.n_tiles, w.gu_codes, w.gu_scales, moe_gu_code_stride(w),
                                 2 * I * w.gu_ws_stride, w.gu_ws_stride, (int)(2 * I), (int)H,
                                 (float *)act, g_eng->num_cus, st),
           op);
   if (!y) return RK_OK;  // stage 1 only
   HIP_TRY(rk_launch_quantize_rows((const float *)act, R, I, I, (int8_t *)aq, (float *)as, st), op);
-  HIP_TRY(rk_launch_moe_gemm_down((const int8_t *)aq, (const float *)as, plan.tiles, plan.n_tiles,
-                                  w.dn_codes, w.dn_scales, H * I, H * w.dn_ws_stride,
+  HIP_TRY(rk_launch_moe_gemm_down((const int8_t *)aq, (const float *)as, R, plan.tiles, plan.n_tiles,
+                                  w.dn_codes, w.dn_scales, moe_dn_code_stride(w), H * w.dn_ws_stride,
                                   w.dn_ws_stride, (int)H, (int)I, plan.roww, (float *)yb,
                                   g_eng->num_cus, st),
           op);

@@ -50,10 +50,28 @@ hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t
 hipError_t rk_launch_quantize_static(const float *x, int64_t m, int64_t k, float in_scale,
                                      int8_t *q, float *row_scale, hipStream_t st);
 // GGUF Q8_0 quantization of f32 rows into codes + per-block f32 scales, with
-// rows remapped as (r/32)·grp_stride + grp_off + r%32.
+// rows remapped as (r/16)·grp_stride + grp_off + r%16 ((16, 0): unchanged).
+// frag: write the fragment-major layout of the MoE expert stacks (below)
+// instead of row-major codes [n, k] and scales [n, ws_stride].
 hipError_t rk_launch_q8_0_quantize(const float *w, int64_t n, int64_t k, int grp_stride,
                                    int grp_off, int8_t *codes, float *scales, int ws_stride,
-                                   hipStream_t st);
+                                   bool frag, hipStream_t st);
+
+// Fragment-major Q8_0 layout of the MoE expert weights: per 32-row block
+// (r/32) and 128-value stage (b/4), 4 KB of codes [block b%4][lane][16 bytes]
+// with lane 32·h + r%32 holding values 16h..16h+15 of block b of row r, and
+// 512 bytes of scales [r%32][b%4]. ws_stride: blocks per row rounded up to a
+// multiple of 4 (padding blocks hold zero codes and zero scales).
+__host__ __device__ inline int64_t q8_code_offset(int64_t r, int64_t b, int j, int64_t k,
+                                                  int ws_stride, int frag) {
+  if (!frag) return r * k + b * 32 + j;
+  return ((r / 32) * (ws_stride / 4) + b / 4) * 4096 + (b % 4) * 1024 +
+         ((j / 16) * 32 + r % 32) * 16 + j % 16;
+}
+__host__ __device__ inline int64_t q8_scale_offset(int64_t r, int64_t b, int ws_stride, int frag) {
+  if (!frag) return r * ws_stride + b;
+  return ((r / 32) * (ws_stride / 4) + b / 4) * 128 + (r % 32) * 4 + b % 4;
+}
 // QAT epilogue: y = acc·(row_scale[m]·w_scale[n]), optionally rounded to the
 // out_scale grid.
 hipError_t rk_launch_qat_epilogue(const int32_t *acc, const float *row_scale,
@@ -90,13 +108,15 @@ struct MoeTile {
   int row0;     // first bucket row of the tile
   int rows;     // rows in the tile
 };
+// a_rows: rows of the activation buffer (s tokens for gate|up, bucket rows
+// for down); offsets into it are 32-bit, so a_rows·K < 2^31.
 hipError_t rk_launch_moe_gemm_gu(const int8_t *xq, const float *xs, const int32_t *tok,
-                                 const MoeTile *tiles, int n_tiles, const int8_t *w,
+                                 int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
                                  const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                  int ws_stride, int N, int K, float *act, int num_cus,
                                  hipStream_t st);
-hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, const MoeTile *tiles,
-                                   int n_tiles, const int8_t *w, const float *ws,
+hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, int64_t rows,
+                                   const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
                                    int64_t w_stride_e, int64_t ws_stride_e, int ws_stride,
                                    int N, int K, const float *row_w, float *yb, int num_cus,
                                    hipStream_t st);

@@ -78,9 +78,59 @@ __global__ __launch_bounds__(QROW_THREADS) void quantize_rows_kernel(
   }
 }
 
+// Per-token form (one scale per row, k % 4 == 0): one wave per row, four
+// rows per workgroup. The row is read once into registers as float4s, the
+// maximum is reduced across the wave (max is exact in any order), and the
+// codes are written four to a 32-bit store. Same arithmetic as above.
+constexpr int QTOK_MAX_VEC = 16;  // float4 per lane: rows up to 4096 values
+__global__ __launch_bounds__(256) void quantize_tokens_kernel(const float *__restrict__ x,
+                                                              int64_t m, int64_t k,
+                                                              int8_t *__restrict__ q,
+                                                              float *__restrict__ scale) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= m) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int nv = (int)(k / 4);
+  const floatx4 *xr = (const floatx4 *)(x + row * k);
+  floatx4 v[QTOK_MAX_VEC];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < QTOK_MAX_VEC; ++i) {
+    const int j = lane + 64 * i;
+    v[i] = j < nv ? xr[j] : floatx4{0.f, 0.f, 0.f, 0.f};
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  const float s = fmaxf(amax / 127.0f, 1e-12f);
+  const float inv = 1.0f / s;
+  if (lane == 0) scale[row] = s;
+  uint32_t *qr = (uint32_t *)(q + row * k);
+#pragma unroll
+  for (int i = 0; i < QTOK_MAX_VEC; ++i) {
+    const int j = lane + 64 * i;
+    if (j < nv) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float c = roundf(v[i][e] * inv);
+        c = fminf(fmaxf(c, -127.0f), 127.0f);
+        packed |= (uint32_t)(uint8_t)(int8_t)(int)c << (8 * e);
+      }
+      qr[j] = packed;
+    }
+  }
+}
+
 hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,
                                    int8_t *q, float *scale, hipStream_t st) {
   if (m <= 0) return hipSuccess;
+  if (group == k && k % 4 == 0 && k <= 4 * 64 * QTOK_MAX_VEC &&
+      ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 4) == 0) {
+    hipLaunchKernelGGL(quantize_tokens_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, st, x,
+                       m, k, q, scale);
+    return hipGetLastError();
+  }
   if (k / group > QROW_MAX_GROUPS) return hipErrorInvalidValue;
   hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)m), dim3(QROW_THREADS), 0, st, x, k,
                      group, q, scale);
@@ -159,7 +209,7 @@ hipError_t rk_launch_qat_epilogue(const int32_t *acc, const float *row_scale,
 // projections of an expert interleave per 32-row slice.
 __global__ void q8_0_quantize_kernel(const float *__restrict__ w, int64_t n, int64_t k,
                                      int grp_stride, int grp_off, int8_t *__restrict__ codes,
-                                     float *__restrict__ scales, int ws_stride) {
+                                     float *__restrict__ scales, int ws_stride, int frag) {
   const int64_t nb = k / 32;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n * nb) return;
@@ -169,22 +219,21 @@ __global__ void q8_0_quantize_kernel(const float *__restrict__ w, int64_t n, int
   for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(src[j]));
   const float scale = (float)(f16)(amax / 127.0f);
   const float inv = scale > 0.f ? 1.0f / scale : 0.f;
-  const int64_t dr = (r / 32) * grp_stride + grp_off + (r % 32);
-  int8_t *dst = codes + dr * k + b * 32;
+  const int64_t dr = (r / 16) * grp_stride + grp_off + (r % 16);
   for (int j = 0; j < 32; ++j) {
     float v = roundf(src[j] * inv);
     v = fminf(fmaxf(v, -127.0f), 127.0f);
-    dst[j] = (int8_t)(int)v;
+    codes[q8_code_offset(dr, b, j, k, ws_stride, frag)] = (int8_t)(int)v;
   }
-  scales[dr * ws_stride + b] = scale;
+  scales[q8_scale_offset(dr, b, ws_stride, frag)] = scale;
 }
 
 hipError_t rk_launch_q8_0_quantize(const float *w, int64_t n, int64_t k, int grp_stride,
                                    int grp_off, int8_t *codes, float *scales, int ws_stride,
-                                   hipStream_t st) {
+                                   bool frag, hipStream_t st) {
   const int64_t total = n * (k / 32);
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL(q8_0_quantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                     w, n, k, grp_stride, grp_off, codes, scales, ws_stride);
+                     w, n, k, grp_stride, grp_off, codes, scales, ws_stride, (int)frag);
   return hipGetLastError();
 }

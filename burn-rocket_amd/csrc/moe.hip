@@ -4,195 +4,375 @@
 // gate|up matmul_gw, silu·up on the host, down matmul_gw, one expert per NPU
 // core) and the per-token combine (src/clef/engine.rs:317-338). Tokens are
 // bucketed per expert on the host (engine.rs:284-313); a tile table lists
-// (expert, first bucket row, rows ≤ 128) entries, and the grid is tiles × N/64.
+// (expert, first bucket row, rows ≤ 128) entries.
 //
-// Each workgroup streams one 64-column slice of one expert's weight through a
-// 3-stage LDS ring while 4 waves each hold 32 gathered token rows, so an
-// expert's weight bytes leave HBM once per row chunk. Waves past the tile's
-// rows still move data and pass barriers but skip the MFMAs.
+// The expert GEMMs are HBM-bound: 128 experts of Q8_0 weights are read once
+// per call while each expert sees ~64 token rows. One workgroup takes one
+// tile of ≤128 rows of one expert and a slice of BN = 32·NW weight columns;
+// wave w owns the 32 columns [32w, 32w+32) for every 32-row block of the
+// tile, so no wave idles on short tiles (only the row blocks that hold rows
+// are computed: the body is instantiated for 1..4 row blocks).
 //
-//   gate|up: weight rows are interleaved per 64-column slice t as
-//            [gate 32t..32t+31 | up 32t..32t+31], so the lane holding gate
-//            column j also holds up column j and the epilogue writes
-//            act = silu(xs·g) · (xs·u) directly (silu(x) = x / (1 + e^-x),
-//            src/clef/model.rs:491).
+// No two waves read the same weight bytes, so the weight codes and scales
+// go straight from HBM into registers (buffer loads, 16 bytes per lane per
+// block), PD stages of 128 K-values ahead of the MFMAs: with ~4 KB per wave
+// and stage that keeps the HBM pipe full. The token rows of the tile, which
+// every wave reads, are gathered into a (PD+1)-slot LDS ring by buffer→LDS
+// copies with per-lane row offsets (16-byte chunks, swizzled by
+// (row >> 1) & 7); rows past the tile read as zeros.
+//
+// One v_mfma_i32_32x32x32_i8 covers one Q8_0 block (exact int32); each
+// result is folded into an f32 accumulator with the block's f32 scale
+// (convert + FMA), and the MFMA of row block u+1 is issued before the fold
+// of row block u so the two overlap.
+//
+//   gate|up: weight rows are interleaved per 16-row slice t as
+//            [gate 16t..16t+15 | up 16t..16t+15], so the lane holding gate
+//            column j and the lane 16 above it holding up column j swap
+//            through ds_bpermute and the epilogue writes
+//            act = silu(xs·g) · (xs·u) (silu(x) = x / (1 + e^-x),
+//            src/clef/model.rs:491; computed as x·rcp(1 + e^-x), within
+//            2 ulp of the division).
 //   down:    yb[row] = (as·acc) · router weight of the row.
-// Codes use one v_mfma_i32_32x32x32_i8 per Q8_0 block (exact int32) and one
-// convert + FMA per element and block with the block's f32 scale.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace {
-constexpr int BM = 128, BN = 64, NW = 4, STAGES = 3;
-constexpr int ROWB = 128;
-constexpr int CODE_BYTES = (BM + BN) * ROWB;
-constexpr int WS_BYTES = BN * 16;
-constexpr int STAGE_BYTES = CODE_BYTES + WS_BYTES;
-constexpr int A_PER = BM / 8 / NW;         // 4
-constexpr int B_PER = BN / 8 / NW;         // 2
-constexpr int WS_PER = BN * 4 / 64 / NW;   // 1
-constexpr int L = A_PER + B_PER + WS_PER;  // 7
+constexpr int MOE_BM = 128;  // rows per tile (the host lists tiles of ≤128 rows)
+constexpr int MOE_ROWB = 128;
+
+// LDS: the (PD+1)-slot ring of token-row stages, then the activation scale
+// and the router weight of each tile row.
+template <int PD>
+constexpr int moe_smem() {
+  return (PD + 1) * MOE_BM * MOE_ROWB + MOE_BM * 8;
+}
 }  // namespace
 
-__device__ __forceinline__ void dma4_moe(const void *gsrc, void *lds_base) {
-  __builtin_amdgcn_global_load_lds(gsrc, LDS_PTR(lds_base), 4, 0, 0);
-}
-
-template <bool GU>
-__global__ __launch_bounds__(NW * 64) void moe_gemm_kernel(
+template <bool GU, int NW, int PD, int NRB>
+__device__ __forceinline__ void moe_body(
     const int8_t *__restrict__ A, const float *__restrict__ AS, const int32_t *__restrict__ tok,
-    const MoeTile *__restrict__ tiles, const int8_t *__restrict__ W,
-    const float *__restrict__ WS, int64_t w_stride_e, int64_t ws_stride_e, int ws_stride,
-    int N, int K, const float *__restrict__ row_w, float *__restrict__ out, int out_ld) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const MoeTile tile = tiles[blockIdx.y];
-  const int n0 = blockIdx.x * BN;
+    int64_t a_rows, const MoeTile &tile, const int8_t *__restrict__ We,
+    const float *__restrict__ WSe, int ws_stride, int N, int K, int n0,
+    const float *__restrict__ row_w, float *__restrict__ out, int out_ld, uint8_t *smem) {
+  constexpr int BM = MOE_BM, ROWB = MOE_ROWB, NSLOT = PD + 1;
+  constexpr int A_STAGE = BM * ROWB;
+  constexpr int QA = BM / 8;     // 8-row copies of token rows per stage
+  constexpr int CPA = QA / NW;   // of them per wave
+  constexpr int VM = CPA + 4 + 1;  // memory ops per wave and stage: A copies, 4 weight loads, scales
+  static_assert(CPA * NW == QA, "token-row copies per wave");
+
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KT = (K + 127) / 128;
   const int KB = K / 32;
-  const int8_t *We = W + (int64_t)tile.expert * w_stride_e;
-  const float *WSe = WS + (int64_t)tile.expert * ws_stride_e;
 
-  const int r8 = lane >> 3;
-  const int lchunk = (lane & 7) ^ r8;
-  const int8_t *a_src[A_PER];
-  const int8_t *b_src[B_PER];
-#pragma unroll
-  for (int i = 0; i < A_PER; ++i) {
-    const int row = min((wave * A_PER + i) * 8 + r8, tile.rows - 1);
-    const int64_t src_row = GU ? (int64_t)tok[tile.row0 + row] : (int64_t)(tile.row0 + row);
-    a_src[i] = A + src_row * K + lchunk * 16;
+  // Row scales (and router weights) for the epilogue, loaded now (visible
+  // after the first stage's barrier) so the epilogue reads them from LDS.
+  float *s_rf = (float *)(smem + NSLOT * A_STAGE);
+  float *s_rw = s_rf + BM;
+  for (int row = threadIdx.x; row < BM; row += NW * 64) {
+    float f = 0.f, rw_ = 0.f;
+    if (row < tile.rows) {
+      const int br = tile.row0 + row;
+      f = GU ? AS[tok[br]] : AS[br];
+      if constexpr (!GU) rw_ = row_w[br];
+    }
+    s_rf[row] = f;
+    s_rw[row] = rw_;
   }
-#pragma unroll
-  for (int i = 0; i < B_PER; ++i) {
-    const int row = (wave * B_PER + i) * 8 + r8;
-    b_src[i] = We + (int64_t)min(n0 + row, N - 1) * K + lchunk * 16;
-  }
-  const int e_ws = wave * 64 + lane;
-  const float *ws_src = WSe + (int64_t)min(n0 + e_ws / 4, N - 1) * ws_stride + (e_ws & 3);
 
-  auto issue = [&](int kt) {
-    uint8_t *sb = smem + (kt % STAGES) * STAGE_BYTES;
-    const int k0 = kt * 128;
-    const bool in = (k0 + lchunk * 16) < K;
+  // Expert weights are stored fragment-major: per 32-column block cb and
+  // 128-value stage kt, 4 KB = [block b][lane][16 bytes] where lane
+  // 32·h + j holds W[32cb + j][32(4kt + b) + 16h .. +16], and 512 bytes of
+  // scales [j][b]. A wave's load of one block is one contiguous 1 KB read.
+  const int KS = ws_stride / 4;  // stages per row (blocks padded to a multiple of 4)
+  const int cb0 = n0 / 32, ncb = (N + 31) / 32;
+  const rsrc_t ra = make_rsrc(A, a_rows * K);
+  const rsrc_t rw = make_rsrc(We + (size_t)cb0 * KS * 4096, (int64_t)(ncb - cb0) * KS * 4096);
+  const rsrc_t rs = make_rsrc(WSe + (size_t)cb0 * KS * 128, (int64_t)(ncb - cb0) * KS * 512);
+
+  // Token-row copy q covers stage rows 8q..8q+7: lane → row 8q + lane/8,
+  // physical chunk lane%8 holding logical chunk (lane%8) ^ ((row >> 1) & 7).
+  const int r8 = lane >> 3, p8 = lane & 7;
+  uint32_t voff_a[CPA];
 #pragma unroll
-    for (int i = 0; i < A_PER; ++i)
-      dma16(in ? (const void *)(a_src[i] + k0) : (const void *)g_zero_chunk,
-            sb + (wave * A_PER + i) * 1024);
+  for (int i = 0; i < CPA; ++i) {
+    const int q = wave + i * NW;
+    const int row = 8 * q + r8;
+    const uint32_t ch = (uint32_t)((p8 ^ ((row >> 1) & 7)) << 4);
+    int64_t src = -1;
+    if (row < tile.rows) src = GU ? (int64_t)tok[tile.row0 + row] : (int64_t)(tile.row0 + row);
+    voff_a[i] = src >= 0 ? (uint32_t)(src * K) + ch : OOB_OFFSET;
+  }
+  const int fcol = lane & 31, fh = lane >> 5;
+  const uint32_t voff_w = (uint32_t)(wave * KS * 4096 + lane * 16);
+  const uint32_t voff_s = (uint32_t)(wave * KS * 512 + fcol * 16);
+
+  intx4 bq[NSLOT][4];
+  floatx4 sq[NSLOT];
+  auto issue = [&](auto slot_c, int kt) {
+    constexpr int slot = decltype(slot_c)::value;
+    uint8_t *sb = smem + slot * A_STAGE;
+    const uint32_t k0 = kt * 128;
 #pragma unroll
-    for (int i = 0; i < B_PER; ++i)
-      dma16(in ? (const void *)(b_src[i] + k0) : (const void *)g_zero_chunk,
-            sb + BM * ROWB + (wave * B_PER + i) * 1024);
-    dma4_moe(ws_src + kt * 4, sb + CODE_BYTES + wave * 256);
+    for (int i = 0; i < CPA; ++i) bdma16(ra, sb + (wave + i * NW) * 1024, voff_a[i], k0);
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      bq[slot][b] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + 1024 * b, kt * 4096, 0);
+    sq[slot] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff_s, kt * 512, 0));
   };
 
-  const bool active = wave * 32 < tile.rows;
-  const int fcol = lane & 31, fh = lane >> 5;
-  floatx16 facc[2];
+  const int swz = (fcol >> 1) & 7;
+  uint32_t a_off[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) facc[j][r] = 0.f;
+  for (int b = 0; b < 4; ++b) a_off[b] = fcol * ROWB + ((((2 * b + fh) ^ swz)) << 4);
 
+  intx4 af[2][NRB];
+  auto load_afrag = [&](auto buf_c, auto slot_c, auto b_c) {
+    constexpr int buf = decltype(buf_c)::value, slot = decltype(slot_c)::value,
+                  b = decltype(b_c)::value;
+    const uint8_t *base = smem + slot * A_STAGE;
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < KT) issue(s);
+    for (int i = 0; i < NRB; ++i) af[buf][i] = *(const intx4 *)(base + a_off[b] + i * 32 * ROWB);
+  };
 
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) {
-      WAIT_VMCNT(L);
+  floatx16 facc[NRB];
+#pragma unroll
+  for (int i = 0; i < NRB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) facc[i][r] = 0.f;
+  intx16 ires[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ires[0][r] = ires[1][r] = 0;
+  float dpend = 0.f;
+  auto fold = [&](auto p_c, auto i_c, float d) {
+    constexpr int P = decltype(p_c)::value, I = decltype(i_c)::value;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) facc[I][r] = __builtin_fmaf((float)ires[P][r], d, facc[I][r]);
+  };
+
+  // Row block u of block b (b = block index within its stage) uses result set
+  // (b·NRB + u) & 1; stages hold 4 blocks, so the sets alternate across stages.
+  auto block = [&](auto s_c, auto b_c) {
+    constexpr int S = decltype(s_c)::value, B = decltype(b_c)::value;
+    constexpr int CUR = B & 1, NXT = CUR ^ 1;
+    constexpr int P0 = (B * NRB) & 1;
+    const float d = sq[S][B];
+    ires[P0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bq[S][B], intx16{}, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (B < 3) load_afrag(ic<NXT>{}, ic<S>{}, ic<B + 1>{});
+    __builtin_amdgcn_sched_barrier(0);
+    fold(ic<P0 ^ 1>{}, ic<NRB - 1>{}, dpend);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<NRB - 1>([&](auto uc) {
+      constexpr int u = decltype(uc)::value + 1;
+      ires[(P0 + u) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][u], bq[S][B], intx16{}, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      fold(ic<(P0 + u - 1) & 1>{}, ic<u - 1>{}, d);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    dpend = d;
+  };
+
+  // Stage kt is ready once at most `later` stages' memory ops (those issued
+  // after it) are outstanding; then the slot of stage kt-1 is free for kt+PD.
+  auto stage = [&](auto s_c, int kt) {
+    constexpr int S = decltype(s_c)::value;
+    const int later = min(PD - 1, KT - 1 - kt);
+    if constexpr (PD >= 4) {
+      if (later >= 3) {
+        WAIT_VMCNT(3 * VM);
+      } else if (later == 2) {
+        WAIT_VMCNT(2 * VM);
+      } else if (later == 1) {
+        WAIT_VMCNT(VM);
+      } else {
+        WAIT_VMCNT(0);
+      }
+    } else if constexpr (PD == 3) {
+      if (later >= 2) {
+        WAIT_VMCNT(2 * VM);
+      } else if (later == 1) {
+        WAIT_VMCNT(VM);
+      } else {
+        WAIT_VMCNT(0);
+      }
     } else {
-      WAIT_VMCNT(0);
+      if (later >= 1) {
+        WAIT_VMCNT(VM);
+      } else {
+        WAIT_VMCNT(0);
+      }
     }
     WAIT_LGKMCNT0();
     BARRIER();
-    if (kt + STAGES - 1 < KT) issue(kt + STAGES - 1);
-    if (!active) continue;
+    if (kt + PD < KT) issue(ic<(S + PD) % NSLOT>{}, kt + PD);
+    load_afrag(ic<0>{}, ic<S>{}, ic<0>{});
+    // One branch per block keeps each block's MFMAs and folds in their own
+    // basic block, in the issue order written here.
+    const int g = kt * 4;
+    block(s_c, ic<0>{});
+    if (g + 1 < KB) block(s_c, ic<1>{});
+    if (g + 2 < KB) block(s_c, ic<2>{});
+    if (g + 3 < KB) block(s_c, ic<3>{});
+  };
 
-    const uint8_t *sa = smem + (kt % STAGES) * STAGE_BYTES;
-    const uint8_t *sbm = sa + BM * ROWB;
-    const float *sws = (const float *)(sa + CODE_BYTES);
-    const int nblk = min(4, KB - kt * 4);
+  static_for<PD>([&](auto s_c) {
+    if (decltype(s_c)::value < KT) issue(s_c, decltype(s_c)::value);
+  });
+  for (int kt0 = 0; kt0 < KT; kt0 += NSLOT) {
+    static_for<NSLOT>([&](auto s_c) {
+      const int kt = kt0 + decltype(s_c)::value;
+      if (kt < KT) stage(s_c, kt);
+    });
+  }
+  if (((KB * NRB - 1) & 1) != 0)
+    fold(ic<1>{}, ic<NRB - 1>{}, dpend);
+  else
+    fold(ic<0>{}, ic<NRB - 1>{}, dpend);
+  WAIT_VMCNT(0);  // no copy may still be writing LDS when the workgroup ends
+
+  // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of each 32-row
+  // block, column lane%32 of the wave's 32 columns.
+  const int col = n0 + wave * 32 + fcol;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      if (b >= nblk) break;
-      const int c = 2 * b + fh;
-      const int arow = wave * 32 + fcol;
-      const intx4 af = *(const intx4 *)(sa + arow * ROWB + ((c ^ (arow & 7)) << 4));
+  for (int i = 0; i < NRB; ++i) {
+    if constexpr (GU) {
+      // Gate column j is in lane j, up column j in lane j + 16 (of each half
+      // wave). For the row pair (r, r+1) the lower lanes finish row r and the
+      // upper lanes row r+1: one swap across the 16-lane halves gives each
+      // lane the gate and up values of its row, so every lane computes one
+      // output. silu(g)·u = g·u / (1 + e^-g).
+      const bool lo = (fcol & 16) == 0;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int brow = j * 32 + fcol;
-        const intx4 bf = *(const intx4 *)(sbm + brow * ROWB + ((c ^ (brow & 7)) << 4));
-        const intx16 p = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, intx16{}, 0, 0, 0);
-        const float d = sws[brow * 4 + b];
+      for (int r = 0; r < 16; r += 2) {
+        const int rr = lo ? r : r + 1;
+        const int row = i * 32 + (rr >> 2) * 8 + fh * 4 + (rr & 3);
+        const float v0 = s_rf[i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3)] * facc[i][r];
+        const float v1 = s_rf[i * 32 + ((r + 1) >> 2) * 8 + fh * 4 + ((r + 1) & 3)] * facc[i][r + 1];
+        // lower lanes send the gate of row r+1, upper lanes the up of row r
+        const float x = __int_as_float(
+            __builtin_amdgcn_ds_bpermute((lane ^ 16) << 2, __float_as_int(lo ? v1 : v0)));
+        const float g = lo ? v0 : x, u = lo ? x : v1;
+        if (row < tile.rows && col < N) {
+          const int c = (n0 + wave * 32) / 2 + (fcol & 15);
+          out[(int64_t)(tile.row0 + row) * out_ld + c] =
+              g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+        }
+      }
+    } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) facc[j][r] = __builtin_fmaf((float)p[r], d, facc[j][r]);
+      for (int r = 0; r < 16; ++r) {
+        const int row = i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+        if (row < tile.rows && col < N)
+          out[(int64_t)(tile.row0 + row) * out_ld + col] = s_rf[row] * facc[i][r] * s_rw[row];
       }
     }
   }
-  if (!active) return;
+}
 
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = wave * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
-    if (row >= tile.rows) continue;
-    const int brow = tile.row0 + row;
-    if (GU) {
-      const float xs = AS[tok[brow]];
-      const float g = xs * facc[0][r];
-      const float u = xs * facc[1][r];
-      const int col = blockIdx.x * 32 + fcol;
-      out[(int64_t)brow * out_ld + col] = g / (1.0f + expf(-g)) * u;
-    } else {
-      const int col = n0 + fcol;
-      const float v0 = AS[brow] * facc[0][r];
-      const float v1 = AS[brow] * facc[1][r];
-      const float w = row_w[brow];
-      if (col < N) out[(int64_t)brow * out_ld + col] = v0 * w;
-      if (col + 32 < N) out[(int64_t)brow * out_ld + col + 32] = v1 * w;
-    }
+template <bool GU, int NW, int PD>
+__global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
+    const int8_t *__restrict__ A, const float *__restrict__ AS, const int32_t *__restrict__ tok,
+    int64_t a_rows, const MoeTile *__restrict__ tiles, int n_col_tiles,
+    const int8_t *__restrict__ W, const float *__restrict__ WS, int64_t w_stride_e,
+    int64_t ws_stride_e, int ws_stride, int N, int K, const float *__restrict__ row_w,
+    float *__restrict__ out, int out_ld) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // Consecutive logical indices (the column slices of one tile) share an XCD
+  // and so the tile's token rows in that XCD's L2.
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const MoeTile tile = tiles[L / n_col_tiles];
+  const int n0 = (L % n_col_tiles) * 32 * NW;
+  const int8_t *We = W + (int64_t)tile.expert * w_stride_e;
+  const float *WSe = WS + (int64_t)tile.expert * ws_stride_e;
+  switch ((tile.rows + 31) >> 5) {
+    case 1:
+      moe_body<GU, NW, PD, 1>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
+                              out_ld, smem);
+      break;
+    case 2:
+      moe_body<GU, NW, PD, 2>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
+                              out_ld, smem);
+      break;
+    case 3:
+      moe_body<GU, NW, PD, 3>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
+                              out_ld, smem);
+      break;
+    default:
+      moe_body<GU, NW, PD, 4>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
+                              out_ld, smem);
+      break;
   }
 }
 
-static hipError_t launch_moe(bool gu, const int8_t *A, const float *AS, const int32_t *tok,
-                             const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
-                             int64_t w_stride_e, int64_t ws_stride_e, int ws_stride, int N,
-                             int K, const float *row_w, float *out, int out_ld,
-                             hipStream_t st) {
-  if (n_tiles == 0) return hipSuccess;
-  constexpr int smem = STAGES * STAGE_BYTES;
-  static bool attr_set[2] = {false, false};
-  auto kern = gu ? moe_gemm_kernel<true> : moe_gemm_kernel<false>;
-  if (!attr_set[gu]) {
+template <bool GU, int NW, int PD>
+static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, const int32_t *tok,
+                                 int64_t a_rows, const MoeTile *tiles, int n_tiles,
+                                 const int8_t *w, const float *ws, int64_t w_stride_e,
+                                 int64_t ws_stride_e, int ws_stride, int N, int K,
+                                 const float *row_w, float *out, int out_ld, hipStream_t st) {
+  constexpr int smem = moe_smem<PD>();
+  static_assert(smem <= 80 * 1024 + MOE_BM * 8, "LDS per workgroup");
+  auto kern = moe_q8_kernel<GU, NW, PD>;
+  static bool attr_set = false;
+  if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     if (e != hipSuccess) return e;
-    attr_set[gu] = true;
+    attr_set = true;
   }
-  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)n_tiles);
-  hipLaunchKernelGGL(kern, grid, dim3(NW * 64), smem, st, A, AS, tok, tiles, w, ws, w_stride_e,
-                     ws_stride_e, ws_stride, N, K, row_w, out, out_ld);
+  const int n_col = (N + 32 * NW - 1) / (32 * NW);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(n_tiles * n_col)), dim3(NW * 64), smem, st, A, AS, tok,
+                     a_rows, tiles, n_col, w, ws, w_stride_e, ws_stride_e, ws_stride, N, K,
+                     row_w, out, out_ld);
   return hipGetLastError();
 }
 
+// Workgroup shapes (RK_MOE_TILE): 0 = 4 waves × 128 columns, weights 2
+// stages ahead (two workgroups per CU); 1 = 8 waves × 256 columns, 3 ahead;
+// 2 = 4 waves, 3 ahead; 3 = 4 waves, 4 ahead.
+template <bool GU>
+static hipError_t launch_moe(const int8_t *A, const float *AS, const int32_t *tok, int64_t a_rows,
+                             const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
+                             int64_t w_stride_e, int64_t ws_stride_e, int ws_stride, int N,
+                             int K, const float *row_w, float *out, int out_ld, hipStream_t st) {
+  if (n_tiles == 0) return hipSuccess;
+  switch (rk_knob("RK_MOE_TILE", 0)) {
+    case 1:
+      return launch_moe_cfg<GU, 8, 3>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
+    case 2:
+      return launch_moe_cfg<GU, 4, 3>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
+    case 3:
+      return launch_moe_cfg<GU, 4, 4>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
+    default:
+      return launch_moe_cfg<GU, 4, 2>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
+  }
+}
+
 hipError_t rk_launch_moe_gemm_gu(const int8_t *xq, const float *xs, const int32_t *tok,
-                                 const MoeTile *tiles, int n_tiles, const int8_t *w,
+                                 int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
                                  const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                  int ws_stride, int N, int K, float *act, int num_cus,
                                  hipStream_t st) {
   (void)num_cus;
-  return launch_moe(true, xq, xs, tok, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e, ws_stride,
-                    N, K, nullptr, act, N / 2, st);
+  return launch_moe<true>(xq, xs, tok, s, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
+                          ws_stride, N, K, nullptr, act, N / 2, st);
 }
 
-hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, const MoeTile *tiles,
-                                   int n_tiles, const int8_t *w, const float *ws,
-                                   int64_t w_stride_e, int64_t ws_stride_e, int ws_stride,
-                                   int N, int K, const float *row_w, float *yb, int num_cus,
-                                   hipStream_t st) {
+hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, int64_t rows,
+                                   const MoeTile *tiles, int n_tiles, const int8_t *w,
+                                   const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
+                                   int ws_stride, int N, int K, const float *row_w, float *yb,
+                                   int num_cus, hipStream_t st) {
   (void)num_cus;
-  return launch_moe(false, aq, as, nullptr, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
-                    ws_stride, N, K, row_w, yb, N, st);
+  return launch_moe<false>(aq, as, nullptr, rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
+                           ws_stride, N, K, row_w, yb, N, st);
 }
 
 // y[t] = Σ_j yb[slot_rows[t, j]] with the slots of a token already sorted by

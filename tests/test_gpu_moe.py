@@ -180,3 +180,19 @@ def test_pack_moe_f32_equals_pack_from_blocks(rk, orc):
     a1, y1 = run(rk, w1, x, ids, wts)
     a2, y2 = run(rk, w2, x, ids, wts)
     assert (a1 == a2).all() and (y1 == y2).all()
+
+
+# Every workgroup shape of the expert kernels (RK_MOE_TILE): 4 or 8 waves,
+# 2 or 3 stages; tiles of 1..4 row blocks, several tiles per expert, and a
+# gate|up width (2·inter = 128) below one 256-column slice.
+@pytest.mark.parametrize("tile", [0, 1, 2, 3])
+def test_moe_every_tile_config(rk, orc, tile, monkeypatch):
+    monkeypatch.setenv("RK_MOE_TILE", str(tile))
+    note(f"MoE RK_MOE_TILE={tile}")
+    r = np.random.default_rng(40 + tile)
+    ids, wts = rk.moe_route(r.standard_normal((300, 8)).astype(np.float32), 8)
+    check_pipeline(rk, orc, 300, 256, 128, 8, ids, wts, 1200 + tile)
+    S = 200
+    ids = np.tile(np.array([[2, 0]], np.uint32), (S, 1))
+    wts = np.tile(np.array([[0.6, 0.4]], np.float32), (S, 1))
+    check_pipeline(rk, orc, S, 128, 64, 4, ids, wts, 1300 + tile)
