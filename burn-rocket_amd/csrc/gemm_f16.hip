@@ -15,10 +15,11 @@
 //     staging. Rows past M/N and chunks past K are read at an out-of-range
 //     offset, which the buffer unit returns as zeros, so ragged edges need no
 //     extra code.
-//   * Chunk c (16 bytes) of row r sits at chunk c ^ f(r), f(r) = (r & 7) ^
-//     ((r >> 3) & 1): any 8 consecutive rows of one fragment read cover the 8
-//     16-byte bank groups of a 128-byte bank row and any 16 rows cover the 16
-//     groups of a 256-byte row, so fragment reads are conflict-free.
+//   * Chunk c (16 bytes) of row r sits at chunk c ^ (r & 7). A fragment read
+//     (16 rows, 4 chunks) is then free of LDS bank conflicts: measured on
+//     MI355X with SQ_LDS_BANK_CONFLICT for both sub-steps' chunk sets, while
+//     the unswizzled layout costs 12 and a (r & 7) ^ ((r >> 3) & 1) swizzle
+//     4 conflict cycles per ds_read_b128.
 //   * A stage is two MFMA sub-steps of 32 K-values. Sub-step 0's MFMAs run
 //     while sub-step 1's fragments are read; then the next stage is waited
 //     for (one barrier per stage), the slot consumed one stage ago is
@@ -66,13 +67,11 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   const rsrc_t rb = make_rsrc(B + (size_t)n0 * K, (int64_t)min(N - n0, BN) * K * 2);
 
   // Copy geometry: copy q covers rows 8q..8q+7; lane → row r = 8q + lane/8,
-  // physical chunk lane%8, which holds logical chunk (lane%8) ^ f(r). f(r)
-  // depends on the parity of q only.
+  // physical chunk lane%8, which holds logical chunk (lane%8) ^ (r & 7) =
+  // (lane%8) ^ (lane/8) for every q.
   const int crow = lane >> 3;
-  const int lch0 = (lane & 7) ^ (crow & 7);        // q even
-  const int lch1 = (lane & 7) ^ ((crow & 7) ^ 1);  // q odd
-  const uint32_t voff0 = (uint32_t)(crow * K * 2 + lch0 * 16);
-  const uint32_t voff1 = (uint32_t)(crow * K * 2 + lch1 * 16);
+  const int lch = (lane & 7) ^ crow;
+  const uint32_t voff0 = (uint32_t)(crow * K * 2 + lch * 16);
   const bool ktail = (K % KS) != 0;
 
   // Copies of stage s; stages past the end copy zeros (into a slot no later
@@ -81,16 +80,15 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
     uint8_t *sb = smem + (s % ST) * STAGE;
     const int k0 = s * KS;
     const bool past = s >= KT;
-    const uint32_t v0 = (past || (ktail && k0 + lch0 * 8 >= K)) ? OOB_OFFSET : voff0;
-    const uint32_t v1 = (past || (ktail && k0 + lch1 * 8 >= K)) ? OOB_OFFSET : voff1;
+    const uint32_t v0 = (past || (ktail && k0 + lch * 8 >= K)) ? OOB_OFFSET : voff0;
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       const int q = wave + NW * i;  // wave-uniform
       if (q < A_INS) {
-        bdma16(ra, sb + q * 1024, (q & 1) ? v1 : v0, (uint32_t)((q * 8 * K + k0) * 2));
+        bdma16(ra, sb + q * 1024, v0, (uint32_t)((q * 8 * K + k0) * 2));
       } else if (q < A_INS + B_INS) {
         const int qb = q - A_INS;
-        bdma16(rb, sb + BM * ROWB + qb * 1024, (qb & 1) ? v1 : v0, (uint32_t)((qb * 8 * K + k0) * 2));
+        bdma16(rb, sb + BM * ROWB + qb * 1024, v0, (uint32_t)((qb * 8 * K + k0) * 2));
       } else {
         bdma16(ra, smem + DUMMY, OOB_OFFSET, 0);
       }
@@ -100,7 +98,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   // Fragment reads: lane → row lane%16 of a 16-row tile, K chunk 4·kk + lane/16.
   const int wm = wave / WN, wn = wave % WN;
   const int frow = lane & 15;
-  const int ff = (frow & 7) ^ (frow >> 3);
+  const int ff = frow & 7;
   const uint32_t fch0 = (uint32_t)((((lane >> 4)) ^ ff) << 4);      // sub-step 0
   const uint32_t fch1 = (uint32_t)((((lane >> 4) + 4) ^ ff) << 4);  // sub-step 1
   const uint32_t a_row = (uint32_t)((wm * WTM + frow) * ROWB);
