@@ -31,11 +31,13 @@
 //   Oᵀ += Vᵀ·Pᵀ A = Vᵀ rows from LDS, B = P hi and lo; Oᵀ keeps the query per
 //               lane, so the online-softmax rescale is a per-lane scalar.
 //
-// LDS: per group two buffers of {K tile: 64 rows of 2·DQ+16 bytes (an odd
-// multiple of 16, so 16 consecutive rows read at one column hit 16 distinct
-// bank groups), Vᵀ tile: DV rows of 64 key slots with 16-byte chunk c of row
-// r at c ^ ((r & 7) ^ ((r >> 3) & 1))}, filled by buffer→LDS copies; keys
-// past n_kv and head columns past D read as zeros.
+// LDS: per group two buffers of {K tile: 64 rows of KPC 16-byte chunks (8
+// for d ≤ 64, else 16: 256-byte rows) with chunk c of row r at
+// c ^ (r & (KPC-1)), Vᵀ tile: DV rows of 64 key slots with chunk c of row r
+// at c ^ (r & 7)}, filled by buffer→LDS copies; keys past n_kv and head
+// columns past D read as zeros. Both layouts were measured free of LDS bank
+// conflicts for these fragment reads on MI355X (SQ_LDS_BANK_CONFLICT), where
+// padded 272-byte K rows cost 4 conflict cycles per ds_read_b128.
 //
 // Masks are predicates on absolute positions (masks.rs:11-114); key tiles
 // that no row of the tile can see are skipped. Scores follow fa_score
@@ -99,12 +101,12 @@ struct AttnGeom {
   static constexpr bool TAIL16 = (DQ % 32) != 0;  // one 16-wide chunk (x16 MFMA)
   static constexpr int DV = DQ;
   static constexpr int NDB = DV / 16;            // 16-row d blocks of Oᵀ
-  static constexpr int KROW = 2 * DQ + 16;       // bytes per K row in LDS
-  static constexpr int KCPR = DQ / 8 + 1;        // 16-byte chunks per K row (last: pad)
+  static constexpr int KPC = DQ <= 64 ? 8 : 16;  // 16-byte chunks per K row in LDS
+  static constexpr int KROW = 16 * KPC;          // bytes per K row in LDS
   static constexpr int K_BYTES = BK * KROW;
   static constexpr int V_BYTES = DV * 128;
   static constexpr int BUF_BYTES = K_BYTES + V_BYTES;
-  static constexpr int K_INS = KCPR;              // 1 KB copies per K tile (64·KCPR chunks)
+  static constexpr int K_INS = BK * KPC / 64;    // 1 KB copies per K tile
   static constexpr int V_INS = DV / 8;            // 8 rows per copy
   static constexpr int CPW = (K_INS + V_INS + 3) / 4;  // copies per wave of a group
   static constexpr int SMEM = 4 * BUF_BYTES;          // 2 groups × 2 buffers
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
   using Gm = AttnGeom<D>;
   constexpr int DQ = Gm::DQ, NQC = Gm::NQC, NDB = Gm::NDB, DV = Gm::DV;
   constexpr bool TAIL16 = Gm::TAIL16;
-  constexpr int KROW = Gm::KROW, KCPR = Gm::KCPR;
+  constexpr int KROW = Gm::KROW, KPC = Gm::KPC;
   constexpr int K_BYTES = Gm::K_BYTES, BUF_BYTES = Gm::BUF_BYTES;
   constexpr int K_INS = Gm::K_INS, V_INS = Gm::V_INS, CPW = Gm::CPW;
   static_assert(Gm::SMEM <= 160 * 1024, "LDS");
@@ -146,11 +148,12 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
   // ops, instead of keeping one VGPR per copy live through the loop).
   auto copy_voff = [&](int c) -> uint32_t {
     if (c < K_INS) {
-      const int p = 64 * c + lane, row = p / KCPR, ch = p - row * KCPR;
+      const int p = 64 * c + lane, row = p / KPC;
+      const int ch = (p % KPC) ^ (row & (KPC - 1));  // logical chunk of this slot
       return (ch < D / 8) ? (uint32_t)row * kstride_b + (uint32_t)(ch * 16) : OOB_OFFSET;
     }
     const int d = 8 * (c - K_INS) + (lane >> 3);
-    const int lch = (lane & 7) ^ ((d & 7) ^ ((d >> 3) & 1));
+    const int lch = (lane & 7) ^ (d & 7);
     return (uint32_t)d * vrow_b + (uint32_t)(lch * 16);
   };
   // Copies of the K part of key tile tk into buffer bk and of the Vᵀ part of
@@ -172,9 +175,13 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
   };
 
   // ---- LDS fragment addresses (within a buffer)
-  const uint32_t k_off = (uint32_t)(l16 * KROW + lg * 16);  // + kb·16·KROW + c·64
-  const uint32_t k_off16 = (uint32_t)(l16 * KROW + NQC * 64 + lg * 8);
-  const int vf = (l16 & 7) ^ (l16 >> 3);
+  const int kf = l16 & (KPC - 1);
+  uint32_t k_off[NQC > 0 ? NQC : 1];  // per 32-wide d chunk c; + kb·16·KROW
+#pragma unroll
+  for (int c = 0; c < NQC; ++c) k_off[c] = (uint32_t)(l16 * KROW + (((4 * c + lg) ^ kf) << 4));
+  const uint32_t k_off16 =
+      (uint32_t)(l16 * KROW + (((4 * NQC + (lg >> 1)) ^ kf) << 4) + (lg & 1) * 8);
+  const int vf = l16 & 7;
   uint32_t v_off[2];  // per 32-key chunk c2; + db·16·128
 #pragma unroll
   for (int c2 = 0; c2 < 2; ++c2) v_off[c2] = (uint32_t)(K_BYTES + l16 * 128 + (((4 * c2 + lg) ^ vf) << 4));
@@ -332,19 +339,19 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
       for (int c = 0; c < NQC; ++c) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          const half8 kf = *(const half8 *)(kbuf + k_off + kb * 16 * KROW + c * 64);
+          const half8 kfr = *(const half8 *)(kbuf + k_off[c] + kb * 16 * KROW);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
-            sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[qb][c], sacc[kb][qb], 0, 0, 0);
+            sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr, qf[qb][c], sacc[kb][qb], 0, 0, 0);
         }
       }
       if constexpr (TAIL16) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          const half4 kf = *(const half4 *)(kbuf + k_off16 + kb * 16 * KROW);
+          const half4 kfr = *(const half4 *)(kbuf + k_off16 + kb * 16 * KROW);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
-            sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x16f16(kf, qt16[qb], sacc[kb][qb], 0, 0, 0);
+            sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x16f16(kfr, qt16[qb], sacc[kb][qb], 0, 0, 0);
         }
       }
       // Each fragment read two reads ahead of its two MFMAs.
