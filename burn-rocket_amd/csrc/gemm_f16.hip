@@ -224,7 +224,7 @@ struct F16Cfg {
 constexpr F16Cfg F16_CFGS[] = {
     {256, 128, 1, .40f}, {192, 192, 1, .38f}, {128, 128, 1, .32f}, {128, 64, 2, .26f},
     {64, 64, 2, .27f},   {128, 256, 1, .41f}, {96, 128, 1, .27f},  {128, 192, 1, .34f},
-    {192, 128, 1, .35f}, {64, 128, 2, .29f},  {192, 192, 1, .41f}, {192, 192, 1, .42f},
+    {192, 128, 1, .35f}, {64, 128, 2, .25f},  {192, 192, 1, .41f}, {192, 192, 1, .42f},
     {128, 128, 1, .33f}, {128, 192, 1, .36f}, {192, 128, 1, .37f},
 };
 constexpr int N_F16_CFGS = sizeof(F16_CFGS) / sizeof(F16_CFGS[0]);
