@@ -132,6 +132,33 @@ def traffic_probe(layers, launches):
     log(f"traffic probe: {launches} copies of {COPY_PROBE_BYTES} B, {launches} launches per projection")
 
 
+def probe_all(launches):
+    """A few launches of every workload's kernels (for rocprofv3 --pmc runs,
+    which serialise and count each dispatch): the W8A8 pair, the fp16 GEMMs,
+    the three attentions and the MoE experts."""
+    layers = setup_w8a8()
+    for L in layers:
+        for _ in range(launches):
+            gemm_w8a8(L)
+    rk.synchronize()
+    lib = rk.lib()
+    for (m, k, n) in ((512, 1024, 3072), (2394, 1152, 3456), (2394, 1152, 1152), (2394, 1152, 4304),
+                      (2394, 4304, 1152)):
+        a = synth.normal_f16(11, (m, k))
+        b = synth.normal_f16(12, (n, k), 0.02)
+        wid, da, dc = rk.pack(b), dev(a.view(np.uint16)), rk.DeviceBuffer(m * n * 2)
+        for _ in range(launches):
+            call(lib.rk_matmul_f16_dev(int(wid), da.ptr, m, k, dc.ptr, None), "f16")
+    rk.synchronize()
+    for (s, h, kv, d, causal, seeds) in ((synth.GQA_CAUSAL["s"], 16, 8, 128, True, synth.SEEDS["gqa"]),
+                                         (synth.VISION["s"], 16, 16, 72, False, synth.SEEDS["vision"][6:9]),
+                                         (synth.MOE["s"], 32, 4, 128, True, synth.SEEDS["moe"][6:9])):
+        time_attention(s, h, kv, d, causal, seeds, launches)
+    extra_moe(launches)
+    rk.synchronize()
+    log(f"probe-all: {launches} launches of each workload")
+
+
 def pmc_summary(paths):
     """Per-kernel HBM bytes per launch from rocprofv3 --pmc CSVs (FETCH_SIZE
     and WRITE_SIZE in KiB per dispatch), each counter scaled by what it reads
@@ -361,6 +388,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the launches the rocprofv3 --pmc byte counts are taken from")
+    ap.add_argument("--probe-all", action="store_true",
+                    help="a few launches of every workload (for rocprofv3 --pmc counter runs)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="summarise rocprofv3 --pmc counter CSVs into profiles/traffic.json (no GPU)")
     a = ap.parse_args()
@@ -375,6 +404,9 @@ def main():
     rk.init(0)
     name, cus, clk = rk.device_info()
     log(f"device {name}, {cus} CUs, {clk / 1e3:.0f} MHz")
+    if a.probe_all:
+        probe_all(5)
+        return
     layers = setup_w8a8()
     if a.traffic_probe:
         traffic_probe(layers, TRAFFIC_LAUNCHES)

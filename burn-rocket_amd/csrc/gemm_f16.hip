@@ -206,8 +206,12 @@ static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, f16 *C, int M, int
     attr_set = true;
   }
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  // Tiles in groups of 3 tile rows (row-fastest inside a group): one XCD's
+  // run of consecutive tiles then shares a few A row-blocks instead of
+  // streaming all of A (vision fc2 2394x4304x1152: 40.6 -> 37.3 us on MI355X,
+  // 185 MB fetched per launch row-fastest over the whole grid).
   hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, A, B, C, M, N, K, tm, tn,
-                     rk_knob("RK_TILE_GROUP_M", 0));
+                     rk_knob("RK_TILE_GROUP_M", 3));
   return hipGetLastError();
 }
 
