@@ -84,6 +84,20 @@ __device__ __forceinline__ void vis_range(int mode, int64_t w, int64_t t, int64_
   }
 }
 
+// x - f32(h) for the low / high fp16 half of h in one v_fma_mix_f32 (the f16
+// operand is widened exactly and the difference of a value and its
+// truncation to fp16 is exact in f32), instead of a convert and a subtract.
+__device__ __forceinline__ float minus_half_lo(unsigned h, float x) {
+  float r;
+  asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+  return r;
+}
+__device__ __forceinline__ float minus_half_hi(unsigned h, float x) {
+  float r;
+  asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+  return r;
+}
+
 // max over lanes l, l^16, l^32, l^48 (the four lane groups holding one query).
 __device__ __forceinline__ float max4groups(float x) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -441,10 +455,10 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
             const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][e], C, nm));
             const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][qb][e + 1], C, nm));
             lsum += e0 + e1;
-            const auto h = __builtin_amdgcn_cvt_pkrtz(e0, e1);
-            hw[jj] = __builtin_bit_cast(unsigned int, h);
-            lw[jj] = __builtin_bit_cast(unsigned int,
-                                        __builtin_amdgcn_cvt_pkrtz(e0 - (float)h[0], e1 - (float)h[1]));
+            const unsigned int h = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(e0, e1));
+            hw[jj] = h;
+            lw[jj] = __builtin_bit_cast(unsigned int, __builtin_amdgcn_cvt_pkrtz(minus_half_lo(h, e0),
+                                                                                minus_half_hi(h, e1)));
           }
           phi[qb][c2] = __builtin_bit_cast(half8, hw);
           plo[qb][c2] = __builtin_bit_cast(half8, lw);
