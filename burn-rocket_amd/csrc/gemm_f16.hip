@@ -22,9 +22,10 @@
 //     4 conflict cycles per ds_read_b128.
 //   * A stage is two MFMA sub-steps of 32 K-values. Sub-step 0's MFMAs run
 //     while sub-step 1's fragments are read; then the next stage is waited
-//     for (one barrier per stage), the slot consumed one stage ago is
-//     refilled, and sub-step 1's MFMAs run while the next stage's first
-//     fragments are read (two register sets).
+//     for (one barrier per stage), the slot of the stage just read is
+//     refilled at once (ST-2 stages of copy latency hidden), and sub-step 1's
+//     MFMAs run while the next stage's first fragments are read (two
+//     register sets).
 //   * The MFMA computes Cᵀ tiles (B fragment as the A operand), so a lane
 //     holds four consecutive columns of one row of C: 8-byte stores.
 #include <algorithm>
@@ -45,14 +46,16 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   constexpr int STAGE = (BM + BN) * ROWB;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 16, TN = WTN / 16;
-  // One stage is A_INS + B_INS copies of 8 rows; wave w issues copies w,
-  // w + NW, ...; when they do not divide evenly the last ones copy zeros into
-  // a dummy 1 KB area past the ring, so every wave issues L copies.
+  // One stage is A_INS + B_INS copies of 8 rows; wave w issues A copies w,
+  // w + NW, ... and B copies likewise: LA of A then L - LA of B, the same
+  // count on every wave and known at compile time, so the issue is straight
+  // scalar code with no branches.
   constexpr int A_INS = BM / 8, B_INS = BN / 8;
-  constexpr int L = (A_INS + B_INS + NW - 1) / NW;
-  constexpr int DUMMY = ST * STAGE;
+  static_assert(A_INS % NW == 0 && B_INS % NW == 0, "copies split evenly over the waves");
+  constexpr int LA = A_INS / NW;
+  constexpr int L = (A_INS + B_INS) / NW;
   static_assert(TM * 16 * WM == BM && TN * 16 * WN == BN, "mfma split");
-  static_assert(ST >= 3 && (ST - 2) * L <= 63, "pipeline depth");
+  static_assert(ST >= 2 && (ST - 1) * L <= 63, "pipeline depth");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
@@ -81,18 +84,16 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
     const int k0 = s * KS;
     const bool past = s >= KT;
     const uint32_t v0 = (past || (ktail && k0 + lch * 8 >= K)) ? OOB_OFFSET : voff0;
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const int q = wave + NW * i;  // wave-uniform
-      if (q < A_INS) {
+    static_for<L>([&](auto i_c) {
+      constexpr int I = decltype(i_c)::value;
+      if constexpr (I < LA) {
+        const int q = wave + NW * I;  // wave-uniform
         bdma16(ra, sb + q * 1024, v0, (uint32_t)((q * 8 * K + k0) * 2));
-      } else if (q < A_INS + B_INS) {
-        const int qb = q - A_INS;
-        bdma16(rb, sb + BM * ROWB + qb * 1024, v0, (uint32_t)((qb * 8 * K + k0) * 2));
       } else {
-        bdma16(ra, smem + DUMMY, OOB_OFFSET, 0);
+        const int q = wave + NW * (I - LA);
+        bdma16(rb, sb + BM * ROWB + q * 1024, v0, (uint32_t)((q * 8 * K + k0) * 2));
       }
-    }
+    });
   };
 
   // Fragment reads: lane → row lane%16 of a 16-row tile, K chunk 4·kk + lane/16.
@@ -144,10 +145,10 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
     }
   };
 
-  // Prologue: stages 0..ST-2 in flight, stage 0 visible, its first fragments read.
+  // Prologue: stages 0..ST-1 in flight, stage 0 visible, its first fragments read.
 #pragma unroll
-  for (int s = 0; s < ST - 1; ++s) issue(s);
-  WAIT_VMCNT((ST - 2) * L);
+  for (int s = 0; s < ST; ++s) issue(s);
+  WAIT_VMCNT((ST - 1) * L);
   BARRIER();
   load_frags(ic<0>{}, 0, fch0);
 
@@ -157,12 +158,15 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
     mfmas(ic<0>{});
     interleave(ic<0>{});
     __builtin_amdgcn_sched_barrier(0);
-    // Stage s+1 visible to all waves (stages up to s+ST-2 were issued); the
-    // slot of stage s-1 is refilled with stage s+ST-1. Sub-step 1 runs while
-    // stage s+1's first fragments are read (past the last stage: stale, unused).
-    WAIT_VMCNT((ST - 3) * L);
+    // Stage s+1 visible to all waves (stages up to s+ST-1 were issued), and
+    // every wave's reads of stage s complete: its slot is refilled at once
+    // with stage s+ST, so a copy has ST-2 full stages to land. Sub-step 1 runs
+    // while stage s+1's first fragments are read (past the last stage: stale,
+    // unused).
+    WAIT_VMCNT((ST - 2) * L);
+    WAIT_LGKMCNT0();
     BARRIER();
-    issue(s + ST - 1);
+    issue(s + ST);
     load_frags(ic<0>{}, s + 1, fch0);
     mfmas(ic<1>{});
     interleave(ic<L>{});
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
 template <int BM, int BN, int WM, int WN, int ST, int MINW>
 static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, f16 *C, int M, int N, int K,
                                   hipStream_t st) {
-  constexpr int smem = ST * (BM + BN) * ROWB + 1024;
+  constexpr int smem = ST * (BM + BN) * ROWB;
   static_assert(smem <= 160 * 1024, "LDS per workgroup");
   auto kern = gemm_f16_kernel<BM, BN, WM, WN, ST, MINW>;
   static bool attr_set = false;

@@ -134,3 +134,21 @@ def test_shape_errors_are_reported(rk):
     assert b"not packed" in lib.rk_last_error()
     ms = rk.mem_stats()
     assert ms.n_weights >= 1 and ms.weights_bytes >= 16 * 64 * 2
+
+
+# Every tile configuration of the fp16 kernel (RK_F16_TILE): ragged M and N,
+# a K tail inside a 64-value stage, and K of one and two stages (fewer stages
+# than the pipeline prologue issues).
+F16_TILES = list(range(15))
+
+
+@pytest.mark.parametrize("tile", F16_TILES)
+def test_gemm_f16_every_tile_config(rk, orc, tile, monkeypatch):
+    monkeypatch.setenv("RK_F16_TILE", str(tile))
+    for m, k, n in ((300, 424, 200), (257, 1024, 392), (70, 64, 130), (129, 128, 260)):
+        note(f"fp16 GEMM RK_F16_TILE={tile} m={m} k={k} n={n}")
+        r = np.random.default_rng(tile * 13 + m + k + n)
+        a = r.standard_normal((m, k)).astype(np.float16)
+        b = (r.standard_normal((n, k)) * 0.05).astype(np.float16)
+        got = run_f16(rk, rk.pack(b), a, n)
+        check(orc, got, orc.gemm_f16(a, b))
