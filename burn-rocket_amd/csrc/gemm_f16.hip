@@ -233,7 +233,8 @@ constexpr F16Cfg F16_CFGS[] = {
     {256, 128, 1, .40f}, {192, 192, 1, .38f}, {128, 128, 1, .32f}, {128, 64, 2, .26f},
     {64, 64, 2, .27f},   {128, 256, 1, .41f}, {96, 128, 1, .27f},  {128, 192, 1, .34f},
     {192, 128, 1, .35f}, {64, 128, 2, .25f},  {192, 192, 1, .41f}, {192, 192, 1, .42f},
-    {128, 128, 1, .33f}, {128, 192, 1, .36f}, {192, 128, 1, .37f},
+    {128, 128, 1, .33f}, {128, 192, 1, .36f}, {192, 128, 1, .37f}, {128, 192, 2, .44f},
+    {192, 128, 2, .44f},
 };
 constexpr int N_F16_CFGS = sizeof(F16_CFGS) / sizeof(F16_CFGS[0]);
 
@@ -255,6 +256,8 @@ hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, i
     case 12: return launch_gemm_f16<128, 128, 2, 4, 4, 2>(a, b, d, M, N, K, st);
     case 13: return launch_gemm_f16<128, 192, 2, 4, 3, 2>(a, b, d, M, N, K, st);
     case 14: return launch_gemm_f16<192, 128, 4, 2, 3, 2>(a, b, d, M, N, K, st);
+    case 15: return launch_gemm_f16<128, 192, 2, 4, 2, 2>(a, b, d, M, N, K, st);
+    case 16: return launch_gemm_f16<192, 128, 4, 2, 2, 2>(a, b, d, M, N, K, st);
   }
   return hipErrorInvalidValue;
 }
