@@ -17,7 +17,9 @@
 // merged through LDS at the end. Two waves per SIMD let one wave's softmax
 // VALU work overlap the other's MFMAs. Query tiles are dispatched from the
 // last one down, so under a causal mask the longest tiles start first and the
-// short ones fill in behind them.
+// short ones fill in behind them. Unmasked calls with head dims up to 80 may
+// instead use 192-row tiles on two groups of 6 waves (3 per SIMD) when that
+// takes fewer rounds of one workgroup per CU (launch_attn below).
 //
 // Per wave and 64-key tile (v_mfma_f32_16x16x32_f16 throughout):
 //   Sᵀ = K·Qᵀ   A = K rows from LDS, B = Q fragments held in VGPRs; a lane
@@ -55,8 +57,7 @@ namespace {
 // 1, 2, 3, 4 and 6 reads ahead (no spills up to d=128 at 6).
 constexpr int LA = 6;
 constexpr int BK = 64;          // keys per tile
-constexpr int ROWS = 128;       // query rows per workgroup tile
-constexpr int NWAVES = 8;       // 2 key groups × 4 waves
+constexpr int ROWS = 128;       // query rows per workgroup tile (4 waves per key group)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float MASKED_SCORE = -30000.0f;  // fa_score clamp (attn/softmax.rs:59)
 constexpr float RESCALE = 8.0f;  // log2 headroom before the running max is raised
@@ -126,21 +127,24 @@ struct AttnGeom {
   static constexpr int BUF_BYTES = K_BYTES + V_BYTES;
   static constexpr int K_INS = BK * KPC / 64;    // 1 KB copies per K tile
   static constexpr int V_INS = DV / 8;            // 8 rows per copy
-  static constexpr int CPW = (K_INS + V_INS + 3) / 4;  // copies per wave of a group
   static constexpr int SMEM = 4 * BUF_BYTES;          // 2 groups × 2 buffers
 };
 
 }  // namespace
 
-template <int D, bool SOFTCAP>
-__global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int G, int BQ,
-                                                                 int n_qtiles) {
+template <int D, bool SOFTCAP, int NWG>
+__global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel(AttnArgs a, int G,
+                                                                                int BQ,
+                                                                                int n_qtiles) {
   using Gm = AttnGeom<D>;
   constexpr int DQ = Gm::DQ, NQC = Gm::NQC, NDB = Gm::NDB, DV = Gm::DV;
   constexpr bool TAIL16 = Gm::TAIL16;
   constexpr int KROW = Gm::KROW, KPC = Gm::KPC;
   constexpr int K_BYTES = Gm::K_BYTES, BUF_BYTES = Gm::BUF_BYTES;
-  constexpr int K_INS = Gm::K_INS, V_INS = Gm::V_INS, CPW = Gm::CPW;
+  constexpr int K_INS = Gm::K_INS, V_INS = Gm::V_INS;
+  constexpr int CPW = (K_INS + V_INS + NWG - 1) / NWG;  // copies per wave of a group
+  // Reads ahead: fewer with 3 waves per SIMD, whose register budget is 168.
+  constexpr int LAW = NWG == 4 ? LA : 3;
   static_assert(Gm::SMEM <= 160 * 1024, "LDS");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -148,7 +152,7 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2, wq = wave & 3;
+  const int grp = (int)((unsigned)wave / NWG), wq = (int)((unsigned)wave % NWG);
   const int KV = a.n_kv_heads;
   const int kvh = blockIdx.x % KV;
   const int qt = n_qtiles - 1 - (int)(blockIdx.x / KV);  // longest causal tiles first
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
   auto issue = [&](int tk, int bk, int tv, int bv) {
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
-      const int c = wq + 4 * i;  // wave-uniform
+      const int c = wq + NWG * i;  // wave-uniform
       if (c < K_INS) {
         if (tk >= 0)
           bdma16(rk, smem + (grp * 2 + bk) * BUF_BYTES + c * 1024, copy_voff(c),
@@ -335,13 +339,13 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
         }
         vprev = vcur;
       });
-      // Each fragment read LA reads ahead of its four MFMAs.
-      __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
-      static_for<NF - LA>([&](auto) {
+      // Each fragment read LAW reads ahead of its four MFMAs.
+      __builtin_amdgcn_sched_group_barrier(0x100, LAW, 0);
+      static_for<NF - LAW>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       });
-      __builtin_amdgcn_sched_group_barrier(0x008, 4 * LA, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * LAW, 0);
     }
     // P of tile j-1 dies here, before S of tile j is produced (keeps the two
     // register sets from overlapping).
@@ -372,14 +376,14 @@ __global__ __launch_bounds__(NWAVES * 64, 2) void attn_fa_kernel(AttnArgs a, int
             sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x16f16(kfr, qt16[qb], sacc[kb][qb], 0, 0, 0);
         }
       }
-      // Each fragment read LA reads ahead of its two MFMAs.
+      // Each fragment read LAW reads ahead of its two MFMAs.
       constexpr int NR = 4 * (NQC + (TAIL16 ? 1 : 0));
-      __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);
-      static_for<NR - LA>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x100, LAW, 0);
+      static_for<NR - LAW>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       });
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * LA, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * LAW, 0);
     }
     };
     // VALU slot j: online softmax of tile j. Scores stay in the raw domain s
@@ -618,14 +622,14 @@ hipError_t rk_launch_v_transpose_strided(const void *v, int64_t tok_stride, int6
   return hipGetLastError();
 }
 
-template <int D>
-static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
+template <int D, int NWG>
+static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
   const int G = a.n_head / a.n_kv_heads;
-  const int BQ = ROWS / G;
+  const int BQ = 32 * NWG / G;
   const int n_qtiles = (a.n_q + BQ - 1) / BQ;
   const int grid = n_qtiles * a.n_kv_heads;
-  auto kern0 = attn_fa_kernel<D, false>;
-  auto kern1 = attn_fa_kernel<D, true>;
+  auto kern0 = attn_fa_kernel<D, false, NWG>;
+  auto kern1 = attn_fa_kernel<D, true, NWG>;
   constexpr int smem = AttnGeom<D>::SMEM;
   static bool attr_set = false;
   if (!attr_set) {
@@ -638,12 +642,36 @@ static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
     attr_set = true;
   }
   if (a.softcap != 0.f)
-    hipLaunchKernelGGL(kern1, dim3((unsigned)grid), dim3(NWAVES * 64), smem, st, a, G, BQ,
+    hipLaunchKernelGGL(kern1, dim3((unsigned)grid), dim3(2 * NWG * 64), smem, st, a, G, BQ,
                        n_qtiles);
   else
-    hipLaunchKernelGGL(kern0, dim3((unsigned)grid), dim3(NWAVES * 64), smem, st, a, G, BQ,
+    hipLaunchKernelGGL(kern0, dim3((unsigned)grid), dim3(2 * NWG * 64), smem, st, a, G, BQ,
                        n_qtiles);
   return hipGetLastError();
+}
+
+// One workgroup per CU (LDS). Without a mask every workgroup walks all keys,
+// so a grid of slightly more tiles than CUs runs a short second round on few
+// CUs; 192-row tiles (6 waves per key group, 3 per SIMD) then cover the
+// queries in fewer rounds (vision S=2394, 16 heads: 304 tiles of 128 rows =
+// 2 rounds, 208 tiles of 192 rows = 1). Head dims up to 80 fit 3 waves per
+// SIMD in registers.
+template <int D>
+static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
+  if constexpr (D <= 80) {
+    // RK_ATTN_ROWS = 128 or 192 forces the tile height (any mask).
+    const int G = a.n_head / a.n_kv_heads;
+    const int knob = rk_knob("RK_ATTN_ROWS", 0);
+    bool six = knob == 192;
+    if (knob == 0 && a.mask_mode == RK_MASK_NONE) {
+      const long cus = a.num_cus > 0 ? a.num_cus : 256;
+      const long t4 = (long)((a.n_q + 128 / G - 1) / (128 / G)) * a.n_kv_heads;
+      const long t6 = (long)((a.n_q + 192 / G - 1) / (192 / G)) * a.n_kv_heads;
+      six = (t6 + cus - 1) / cus * 192 < (t4 + cus - 1) / cus * 128;
+    }
+    if (six && G <= 192) return launch_attn_nwg<D, 6>(a, st);
+  }
+  return launch_attn_nwg<D, 4>(a, st);
 }
 
 hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st) {

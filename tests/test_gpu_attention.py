@@ -101,6 +101,25 @@ def test_head_dims_and_groups(rk, orc, d, h, kv):
         check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, mode=mode))
 
 
+@pytest.mark.parametrize("d", [64, 72, 80])
+@pytest.mark.parametrize("h,kv", [(4, 4), (8, 2), (6, 3), (16, 16)])
+def test_192_row_tiles(rk, orc, d, h, kv, monkeypatch):
+    """Head dims up to 80 also run on 192-row query tiles (6 waves per key
+    group), the default for unmasked calls whose 128-row grid needs an extra
+    round on the CUs; forced here for every mask mode, ragged query and key
+    counts and a softcap."""
+    monkeypatch.setenv("RK_ATTN_ROWS", "192")
+    r = np.random.default_rng(d * 17 + h + kv)
+    n_q, n_kv = 407, 390
+    q = r.standard_normal((n_q, h * d)).astype(np.float16)
+    k = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    v = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    for mode, window, softcap in ((0, -1, 0.0), (1, -1, 0.0), (2, 25, 0.0), (3, 60, 0.0), (0, -1, 20.0)):
+        note(f"192-row tiles d={d} h={h} kv={kv} mode={mode} window={window} softcap={softcap}")
+        got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, softcap=softcap, mode=mode, window=window)
+        check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, softcap, mode, window))
+
+
 @pytest.mark.parametrize("mode,window,n_q,n_kv,q0,k0", [
     (2, 17, 200, 200, 0, 0),      # band
     (3, 33, 200, 200, 0, 0),      # causal sliding window
