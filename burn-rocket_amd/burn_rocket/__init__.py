@@ -25,6 +25,7 @@ RK_E_SHAPE, RK_E_TILING, RK_E_NOMEM, RK_E_DEVICE = -1, -2, -3, -4
 RK_E_UNSUPPORTED, RK_E_RANGE, RK_E_IO = -5, -6, -7
 RK_WEIGHT_F16, RK_WEIGHT_I8, RK_WEIGHT_QAT = 1, 2, 3
 MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_CAUSAL_WINDOW = 0, 1, 2, 3
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 # Every entry point of include/burn_rocket_amd.h with its ctypes signature.
 _c = ctypes
@@ -71,6 +72,10 @@ SIGNATURES = {
     "rk_memcpy_htod": (_i, [_p, _p, _sz]),
     "rk_memcpy_dtoh": (_i, [_p, _p, _sz]),
     "rk_memcpy_dtod": (_i, [_p, _p, _sz, _p]),
+    "rk_silu_mul_dev": (_i, [_p, _p, _p, _i64, _i, _p]),
+    "rk_gelu_mul_dev": (_i, [_p, _p, _p, _i64, _i, _p]),
+    "rk_silu_mul": (_i, [_p, _p, _p, _i64]),
+    "rk_gelu_mul": (_i, [_p, _p, _p, _i64]),
     "rk_memset_dev": (_i, [_p, _i, _sz]),
     "rk_stream_get": (_i, [_p]),
     "rk_stream_sync": (_i, [_p]),
@@ -259,6 +264,45 @@ def matmul(x, wid):
     y = np.empty((m, n), dtype=np.float32)
     _check(_lib.rk_matmul(int(wid), _ptr(xf), m, k, _ptr(y)), "rocket_matmul", m, k, n)
     return y.reshape(*x.shape[:-1], n).astype(x.dtype if x.dtype in (np.float16, np.float32) else np.float32)
+
+
+def _glue(fn_name, op_name, a, b, bf16):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.dtype == b.dtype, f"{op_name} inputs must share a dtype"
+    assert a.shape == b.shape, f"{op_name} inputs must share a shape"
+    if bf16:
+        assert a.dtype == np.uint16, "bf16 values are passed as their uint16 bits"
+        dt = DTYPE_BF16
+    elif a.dtype == np.float16:
+        dt = DTYPE_F16
+    elif a.dtype == np.float32:
+        dt = DTYPE_F32
+    else:
+        raise AssertionError(f"unsupported glue dtype {a.dtype} (f32/f16/bf16)")
+    if a.size == 0:
+        return a.copy()
+    ac, bc = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    da, db = DeviceBuffer.from_array(ac), DeviceBuffer.from_array(bc)
+    do = DeviceBuffer(max(ac.nbytes, 1))
+    try:
+        _check(getattr(_lib, fn_name)(da.ptr, db.ptr, do.ptr, ac.size, dt, None), op_name)
+        synchronize()
+        return do.download(a.shape, a.dtype)
+    finally:
+        for buf in (da, db, do):
+            buf.free()
+
+
+def silu_mul(a, b, bf16=False):
+    """`silu(a) * b` (`rocket_silu_mul`, ext.rs:607-608): f32 or f16 arrays, or
+    bf16 as uint16 bits with bf16=True; computed in f32, returned in the input
+    dtype."""
+    return _glue("rk_silu_mul_dev", "rocket_silu_mul", a, b, bf16)
+
+
+def gelu_mul(a, b, bf16=False):
+    """`gelu_approximate(a) * b` (`rocket_gelu_mul`, ext.rs:603-604); as silu_mul."""
+    return _glue("rk_gelu_mul_dev", "rocket_gelu_mul", a, b, bf16)
 
 
 def _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, mode, window, q0, k0):

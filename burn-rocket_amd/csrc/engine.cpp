@@ -1266,6 +1266,56 @@ extern "C" int rk_memcpy_dtoh(void *dst, const void *src, size_t bytes) {
   HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "rk_memcpy_dtoh");
   return RK_OK;
 }
+// =========================================================================
+// MLP glue
+// =========================================================================
+namespace {
+int glue_dev(int op, const void *a, const void *b, void *out, int64_t n, int dtype,
+             rk_stream stream, const char *name) {
+  RK_TRY(ensure(name));
+  if (n < 0) return fail(RK_E_SHAPE, name, "negative element count");
+  if (dtype < RK_DTYPE_F32 || dtype > RK_DTYPE_BF16) return fail(RK_E_SHAPE, name, "unknown dtype");
+  if (n > 0 && (!a || !b || !out)) return fail(RK_E_SHAPE, name, "null buffer");
+  HIP_TRY(rk_launch_glue(op, a, b, out, n, dtype, pick(stream)), name);
+  return RK_OK;
+}
+int glue_host(int op, const float *a, const float *b, float *out, int64_t n, const char *name) {
+  RK_TRY(ensure(name));
+  if (n < 0) return fail(RK_E_SHAPE, name, "negative element count");
+  if (n == 0) return RK_OK;
+  if (!a || !b || !out) return fail(RK_E_SHAPE, name, "null buffer");
+  void *d = nullptr;
+  RK_TRY(scratch("glue", (size_t)n * 12, &d));
+  float *da = (float *)d, *db = da + n, *dout = db + n;
+  hipStream_t st = g_eng->stream;
+  HIP_TRY(hipMemcpyAsync(da, a, (size_t)n * 4, hipMemcpyHostToDevice, st), name);
+  HIP_TRY(hipMemcpyAsync(db, b, (size_t)n * 4, hipMemcpyHostToDevice, st), name);
+  HIP_TRY(rk_launch_glue(op, da, db, dout, n, RK_DTYPE_F32, st), name);
+  HIP_TRY(hipMemcpyAsync(out, dout, (size_t)n * 4, hipMemcpyDeviceToHost, st), name);
+  HIP_TRY(hipStreamSynchronize(st), name);
+  return RK_OK;
+}
+}  // namespace
+
+extern "C" int rk_silu_mul_dev(const void *a, const void *b, void *out, int64_t n, int dtype,
+                               rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return glue_dev(0, a, b, out, n, dtype, stream, "rk_silu_mul_dev");
+}
+extern "C" int rk_gelu_mul_dev(const void *a, const void *b, void *out, int64_t n, int dtype,
+                               rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return glue_dev(1, a, b, out, n, dtype, stream, "rk_gelu_mul_dev");
+}
+extern "C" int rk_silu_mul(const float *a, const float *b, float *out, int64_t n) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return glue_host(0, a, b, out, n, "rk_silu_mul");
+}
+extern "C" int rk_gelu_mul(const float *a, const float *b, float *out, int64_t n) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return glue_host(1, a, b, out, n, "rk_gelu_mul");
+}
+
 extern "C" int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_stream stream) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_memcpy_dtod"));

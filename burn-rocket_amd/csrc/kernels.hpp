@@ -42,6 +42,10 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st);
 hipError_t rk_launch_f32_to_f16(const float *x, void *y, int64_t n, hipStream_t st);
 hipError_t rk_launch_f16_to_f32(const void *x, float *y, int64_t n, hipStream_t st);
 
+// MLP glue: op 0 silu_mul, 1 gelu_mul; dtype RK_DTYPE_*.
+hipError_t rk_launch_glue(int op, const void *a, const void *b, void *out, int64_t n, int dtype,
+                          hipStream_t st);
+
 // Per-row symmetric quantizer (scale = max(amax/127, 1e-12), codes
 // round-half-away(x·(1/scale)) clamped to ±127), `group` values per scale.
 hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,

@@ -4,6 +4,8 @@
 // (f32_to_f16_par / f16_to_f32_par ext.rs:2144-2170, quantize_i8_rows
 // ext.rs:1017-1029 with quantize_row_groups host.rs:77-90, the QAT static
 // quantizer and epilogue ext.rs:1236-1373), moved next to the data.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -236,4 +238,122 @@ hipError_t rk_launch_q8_0_quantize(const float *w, int64_t n, int64_t k, int grp
   hipLaunchKernelGGL(q8_0_quantize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
                      w, n, k, grp_stride, grp_off, codes, scales, ws_stride, (int)frag);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// MLP glue: out = silu(gate)·up or gelu_tanh(gate)·up elementwise
+// (rocket_silu_mul / rocket_gelu_mul, ext.rs:603-608 and 1057-1090, with the
+// formulas of host.rs:12-39), computed in f32 in the reference's order with
+// no FMA contraction, inputs and output in f32, fp16 or bf16 (the output in
+// the input type, rounded to nearest even). Each thread handles 16 bytes of
+// each input when all three pointers are 16-byte aligned, else one element.
+// ---------------------------------------------------------------------------
+namespace {
+__device__ __forceinline__ float glue_silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  const float sigmoid = 1.0f / (1.0f + expf(-g));
+  return g * sigmoid * u;
+}
+// sqrt(2/π) as the f64 product FRAC_2_SQRT_PI·FRAC_1_SQRT_2 rounded to f32.
+constexpr float GLUE_SQRT_2_OVER_PI = (float)(1.12837916709551257390 * 0.70710678118654752440);
+__device__ __forceinline__ float glue_gelu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  const float inner = (g + g * g * g * 0.044715f) * GLUE_SQRT_2_OVER_PI;
+  return ((g * (tanhf(inner) + 1.0f)) * 0.5f) * u;
+}
+
+template <int DT>
+__device__ __forceinline__ float glue_load(const void *p, int64_t i) {
+  if constexpr (DT == RK_DTYPE_F32) return ((const float *)p)[i];
+  if constexpr (DT == RK_DTYPE_F16) return (float)((const f16 *)p)[i];
+  return __uint_as_float((uint32_t)((const uint16_t *)p)[i] << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+template <int DT>
+__device__ __forceinline__ void glue_store(void *p, int64_t i, float v) {
+  if constexpr (DT == RK_DTYPE_F32) ((float *)p)[i] = v;
+  else if constexpr (DT == RK_DTYPE_F16) ((f16 *)p)[i] = (f16)v;
+  else ((uint16_t *)p)[i] = f32_to_bf16_rne(v);
+}
+}  // namespace
+
+template <int OP, int DT, bool VEC>
+__global__ __launch_bounds__(256) void glue_kernel(const void *__restrict__ a,
+                                                   const void *__restrict__ b,
+                                                   void *__restrict__ out, int64_t n) {
+  constexpr int V = VEC ? (DT == RK_DTYPE_F32 ? 4 : 8) : 1;  // elements per thread
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * V;
+  for (int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V; i0 < n; i0 += stride) {
+    if (VEC && i0 + V <= n) {
+      // 16-byte loads and store; elements in registers as f32
+      const uintx4 av = *(const uintx4 *)((const uint8_t *)a + i0 * (16 / V));
+      const uintx4 bv = *(const uintx4 *)((const uint8_t *)b + i0 * (16 / V));
+      uintx4 ov;
+      if constexpr (DT == RK_DTYPE_F32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float g = __uint_as_float(av[e]), u = __uint_as_float(bv[e]);
+          ov[e] = __float_as_uint(OP == 0 ? glue_silu_mul(g, u) : glue_gelu_mul(g, u));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint16_t ga = (uint16_t)(av[e] >> (16 * h)), ub = (uint16_t)(bv[e] >> (16 * h));
+            float g, u;
+            if constexpr (DT == RK_DTYPE_F16) {
+              g = (float)__builtin_bit_cast(f16, ga);
+              u = (float)__builtin_bit_cast(f16, ub);
+            } else {
+              g = __uint_as_float((uint32_t)ga << 16);
+              u = __uint_as_float((uint32_t)ub << 16);
+            }
+            const float r = OP == 0 ? glue_silu_mul(g, u) : glue_gelu_mul(g, u);
+            const uint16_t rb = DT == RK_DTYPE_F16 ? __builtin_bit_cast(uint16_t, (f16)r) : f32_to_bf16_rne(r);
+            w |= (uint32_t)rb << (16 * h);
+          }
+          ov[e] = w;
+        }
+      }
+      *(uintx4 *)((uint8_t *)out + i0 * (16 / V)) = ov;
+    } else {
+      for (int64_t i = i0; i < n && i < i0 + V; ++i) {
+        const float g = glue_load<DT>(a, i), u = glue_load<DT>(b, i);
+        glue_store<DT>(out, i, OP == 0 ? glue_silu_mul(g, u) : glue_gelu_mul(g, u));
+      }
+    }
+  }
+}
+
+template <int OP, int DT>
+static hipError_t launch_glue_t(const void *a, const void *b, void *out, int64_t n, hipStream_t st) {
+  const bool vec = (((uintptr_t)a | (uintptr_t)b | (uintptr_t)out) & 15) == 0;
+  const int V = vec ? (DT == RK_DTYPE_F32 ? 4 : 8) : 1;
+  const int64_t chunks = (n + V - 1) / V;
+  const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 8192);
+  if (vec)
+    hipLaunchKernelGGL((glue_kernel<OP, DT, true>), dim3(blocks), dim3(256), 0, st, a, b, out, n);
+  else
+    hipLaunchKernelGGL((glue_kernel<OP, DT, false>), dim3(blocks), dim3(256), 0, st, a, b, out, n);
+  return hipGetLastError();
+}
+
+hipError_t rk_launch_glue(int op, const void *a, const void *b, void *out, int64_t n, int dtype,
+                          hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  switch (op * 3 + dtype) {
+    case 0: return launch_glue_t<0, RK_DTYPE_F32>(a, b, out, n, st);
+    case 1: return launch_glue_t<0, RK_DTYPE_F16>(a, b, out, n, st);
+    case 2: return launch_glue_t<0, RK_DTYPE_BF16>(a, b, out, n, st);
+    case 3: return launch_glue_t<1, RK_DTYPE_F32>(a, b, out, n, st);
+    case 4: return launch_glue_t<1, RK_DTYPE_F16>(a, b, out, n, st);
+    case 5: return launch_glue_t<1, RK_DTYPE_BF16>(a, b, out, n, st);
+  }
+  return hipErrorInvalidValue;
 }

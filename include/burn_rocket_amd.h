@@ -63,6 +63,12 @@ extern "C" {
 #define RK_MASK_WINDOW 2
 #define RK_MASK_CAUSAL_WINDOW 3
 
+/* Element types of the MLP glue ops (the f32 / f16 / bf16 inputs the
+ * reference's glue accepts, ext.rs:1040-1050). */
+#define RK_DTYPE_F32 0
+#define RK_DTYPE_F16 1
+#define RK_DTYPE_BF16 2
+
 typedef uint64_t rk_weight_id;
 typedef void *rk_stream; /* a hipStream_t; NULL selects the library stream */
 
@@ -285,6 +291,25 @@ int rk_moe_plan_destroy(void *plan);
  * within an expert, by token (the bucket order of engine.rs:292-305). */
 int rk_moe_gate_up_dev(rk_weight_id id, const void *plan, const float *x,
                        float *act, rk_stream stream);
+
+/* ======================================================================== *
+ * MLP glue                                                                 *
+ * ======================================================================== */
+/* out = silu(a)·b = a·(1/(1 + exp(-a)))·b elementwise over n values
+ * (`rocket_silu_mul`, ext.rs:72, 607-608, silu_mul_impl ext.rs:1076-1090,
+ * formula host.rs:30-39): computed in f32, inputs and output of type dtype
+ * (RK_DTYPE_*), the output rounded to nearest even. Device buffers; out may
+ * be a or b. */
+int rk_silu_mul_dev(const void *a, const void *b, void *out, int64_t n, int dtype,
+                    rk_stream stream);
+/* out = gelu_tanh(a)·b, gelu_tanh(x) = (x·(tanh((x + x·x·x·0.044715)·√(2/π)) + 1))·0.5
+ * (`rocket_gelu_mul`, ext.rs:70, 603-604, gelu_mul_impl ext.rs:1057-1072,
+ * formula host.rs:12-28). Same conventions as rk_silu_mul_dev. */
+int rk_gelu_mul_dev(const void *a, const void *b, void *out, int64_t n, int dtype,
+                    rk_stream stream);
+/* Host-buffer forms on f32 arrays (synchronous). */
+int rk_silu_mul(const float *a, const float *b, float *out, int64_t n);
+int rk_gelu_mul(const float *a, const float *b, float *out, int64_t n);
 
 /* ======================================================================== *
  * Device plumbing for callers without their own HIP runtime bindings       *

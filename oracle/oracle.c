@@ -566,4 +566,33 @@ void orc_moe_experts(const float *x, int64_t s, int64_t H, int64_t I, int E, int
   free(xs);
 }
 
+/* ------------------------------------------------------------ MLP glue --- */
+/* sqrt(2/π) as gelu_tanh uses it: the f64 product of FRAC_2_SQRT_PI and
+ * FRAC_1_SQRT_2, rounded to f32 (host.rs:9-10, host.rs:16). */
+static float sqrt_2_over_pi_f32(void) {
+  return (float)(1.12837916709551257390 * 0.70710678118654752440);
+}
+
+/* Burn's gelu_approximate, tanh form (host.rs:12-18):
+ * (x·(tanh((x + x·x·x·0.044715)·√(2/π)) + 1))·0.5, left to right in f32. */
+float orc_gelu_tanh(float x) {
+  const float inner = (x + x * x * x * 0.044715f) * sqrt_2_over_pi_f32();
+  return (x * (tanhf(inner) + 1.0f)) * 0.5f;
+}
+
+/* out = gelu_tanh(gate)·up, elementwise (gelu_mul, host.rs:20-28). */
+void orc_gelu_mul(const float *gate, const float *up, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = orc_gelu_tanh(gate[i]) * up[i];
+}
+
+/* out = gate·sigmoid(gate)·up with sigmoid(x) = 1/(1 + exp(-x)), evaluated
+ * (gate·sigmoid)·up (silu_mul, host.rs:30-39). */
+void orc_silu_mul(const float *gate, const float *up, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float g = gate[i];
+    const float sigmoid = 1.0f / (1.0f + expf(-g));
+    out[i] = g * sigmoid * up[i];
+  }
+}
+
 int orc_max_threads(void) { return omp_get_max_threads(); }

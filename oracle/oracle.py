@@ -36,6 +36,9 @@ _SIG = {
     "orc_attention_flex": (None, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _i]),
     "orc_route": (None, [_p, _i64, _i, _i, _i, _p, _p]),
     "orc_moe_experts": (None, [_p, _i64, _i64, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i]),
+    "orc_gelu_tanh": (_f, [_f]),
+    "orc_gelu_mul": (None, [_p, _p, _p, _i64]),
+    "orc_silu_mul": (None, [_p, _p, _p, _i64]),
     "orc_max_threads": (_i, []),
 }
 
@@ -248,6 +251,47 @@ def moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds, threads=None):
 
 
 # ------------------------------------------------------------- metrics ----
+def f32_to_bf16(x):
+    """f32 → bf16 bits with round-to-nearest-even, NaN kept quiet (the `half`
+    crate 2.7.1 bf16::from_f32 behind floats_tensor, ext.rs:1040-1050)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    r = ((u.astype(np.uint64) + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(h):
+    """bf16 bits → f32 (exact)."""
+    return (np.ascontiguousarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def gelu_tanh(x):
+    """orc_gelu_tanh elementwise over f32 (host.rs:12-18)."""
+    x = np.ascontiguousarray(x, np.float32)
+    f = lib().orc_gelu_tanh
+    return np.array([f(float(v)) for v in x.ravel()], np.float32).reshape(x.shape)
+
+
+def _glue(fn, gate, up):
+    g = np.ascontiguousarray(gate, np.float32)
+    u = np.ascontiguousarray(up, np.float32)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    fn(_ptr(g), _ptr(u), _ptr(out), ctypes.c_int64(g.size))
+    return out
+
+
+def silu_mul(gate, up):
+    """silu(gate)·up in f32 (host.rs:30-39)."""
+    return _glue(lib().orc_silu_mul, gate, up)
+
+
+def gelu_mul(gate, up):
+    """gelu_tanh(gate)·up in f32 (host.rs:20-28)."""
+    return _glue(lib().orc_gelu_mul, gate, up)
+
+
 def cosine(a, b):
     a = np.asarray(a, dtype=np.float64).ravel()
     b = np.asarray(b, dtype=np.float64).ravel()

@@ -377,3 +377,49 @@ def test_moe_emulation_against_dequantised_f64(orc):
     peak = np.abs(want).max()
     assert np.abs(y - want).max() <= 2e-2 * peak
     assert orc.cosine(y, want) > 0.999
+
+
+# ---- MLP glue (host.rs:12-39) ----------------------------------------------
+
+def _gelu_composite(x):
+    """Burn's gelu_approximate composite with powf, in f32 (host.rs:96-102)."""
+    x = np.asarray(x, np.float32)
+    inner = x + np.power(x, np.float32(3.0)) * np.float32(0.044715)
+    inner = inner * np.float32(np.sqrt(2.0 / np.pi))
+    return (x * (np.tanh(inner.astype(np.float64)).astype(np.float32) + np.float32(1.0))) * np.float32(0.5)
+
+
+def test_gelu_tanh_matches_the_composite(orc):
+    # host.rs:104-115: -30..30 in steps of 0.05, within 1e-6·max(|want|, 1)
+    xs = (np.arange(-600, 601) * 0.05).astype(np.float32)
+    got, want = orc.gelu_tanh(xs), _gelu_composite(xs)
+    assert (np.abs(got - want) <= 1e-6 * np.maximum(np.abs(want), 1.0)).all()
+    # gelu(x) - gelu(-x) = x (tanh is odd) and gelu(0) = 0
+    assert np.abs((got - orc.gelu_tanh(-xs)) - xs).max() <= 4e-6 * np.abs(xs).max()
+    assert orc.gelu_tanh(np.zeros(1, np.float32))[0] == 0.0
+
+
+def test_gelu_mul_and_silu_mul_known_answers(orc):
+    # host.rs:117-144 (same gate/up vectors)
+    gate = np.array([0.0, 1.0, -1.0, 3.7, -12.5], np.float32)
+    up = np.array([2.0, -1.0, 0.5, 0.25, 8.0], np.float32)
+    assert (orc.gelu_mul(gate, up) == orc.gelu_tanh(gate) * up).all()
+    want = gate.astype(np.float64) / (1.0 + np.exp(-gate.astype(np.float64))) * up
+    got = orc.silu_mul(gate, up)
+    assert (np.abs(got - want) <= 1e-6 * np.maximum(np.abs(want), 1.0)).all()
+    # limits: silu(g)·u → g·u for large g, → 0 for very negative g; silu(0) = 0
+    big = np.array([30.0, -30.0, 0.0], np.float32)
+    assert np.allclose(orc.silu_mul(big, np.ones(3, np.float32)), [30.0, 0.0, 0.0], atol=1e-9)
+
+
+def test_bf16_round_to_nearest_even(orc):
+    import torch
+    r = _rng(16)
+    x = np.concatenate([r.standard_normal(4096).astype(np.float32) * 10,
+                        # exact ties (low 16 bits 0x8000), both parities, and signed zero
+                        (np.arange(64, dtype=np.uint32) * 0x10000 + 0x3F808000).view(np.float32),
+                        np.array([0.0, -0.0, 65504.0, 1e-40, -3.0e38], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = orc.f32_to_bf16(x)
+    assert (got == want).all()
+    assert (orc.bf16_to_f32(got) == torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy()).all()
