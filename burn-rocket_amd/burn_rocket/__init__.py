@@ -26,6 +26,7 @@ RK_E_UNSUPPORTED, RK_E_RANGE, RK_E_IO = -5, -6, -7
 RK_WEIGHT_F16, RK_WEIGHT_I8, RK_WEIGHT_QAT = 1, 2, 3
 MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_CAUSAL_WINDOW = 0, 1, 2, 3
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+GLU_SILU, GLU_GELU = 1, 2
 
 # Every entry point of include/burn_rocket_amd.h with its ctypes signature.
 _c = ctypes
@@ -75,6 +76,9 @@ SIGNATURES = {
     "rk_silu_mul_dev": (_i, [_p, _p, _p, _i64, _i, _p]),
     "rk_gelu_mul_dev": (_i, [_p, _p, _p, _i64, _i, _p]),
     "rk_silu_mul": (_i, [_p, _p, _p, _i64]),
+    "rk_pack_q8_0_glu": (_i, [_p, _p, _i64, _i64, _p]),
+    "rk_pack_q8_0_glu_f32": (_i, [_p, _p, _i64, _i64, _p]),
+    "rk_matmul_w8a8_glu_dev": (_i, [_u64, _p, _p, _i64, _i64, _i, _p, _i, _p]),
     "rk_gelu_mul": (_i, [_p, _p, _p, _i64]),
     "rk_memset_dev": (_i, [_p, _i, _sz]),
     "rk_stream_get": (_i, [_p]),
@@ -221,6 +225,26 @@ def pack_q8_0(blocks, n, k):
     assert blocks.size == n * (k // 32) * 34, "Q8_0 blob size"
     out = ctypes.c_uint64()
     _check(_lib.rk_pack_q8_0(_ptr(blocks), n, k, ctypes.byref(out)), "rocket_q8_0_pack", 0, k, n)
+    return WeightId(out.value)
+
+
+def pack_q8_0_glu(gate_blocks, up_blocks, n, k):
+    """Fused gate|up weight from the GGUF Q8_0 blocks of gate [n, k] and up [n, k]."""
+    g = np.ascontiguousarray(gate_blocks, dtype=np.uint8)
+    u = np.ascontiguousarray(up_blocks, dtype=np.uint8)
+    assert g.size == n * (k // 32) * 34 and u.size == g.size, "Q8_0 blob size"
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_q8_0_glu(_ptr(g), _ptr(u), n, k, ctypes.byref(out)), "rocket_q8_0_glu_pack", 0, k, n)
+    return WeightId(out.value)
+
+
+def pack_q8_0_glu_f32(gate, up):
+    """Fused gate|up weight quantized to Q8_0 on the device from f32 gate, up [n, k]."""
+    g, u = _f32(gate), _f32(up)
+    assert g.shape == u.shape and g.ndim == 2
+    n, k = g.shape
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_q8_0_glu_f32(_ptr(g), _ptr(u), n, k, ctypes.byref(out)), "rocket_q8_0_glu_pack", 0, k, n)
     return WeightId(out.value)
 
 

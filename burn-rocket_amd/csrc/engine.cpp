@@ -74,6 +74,7 @@ struct Weight {
   void *codes = nullptr;     // fp16 [N,K] or int8 [N,K]
   float *scales = nullptr;   // I8: [N, ws_stride] per 32-block; QAT: [N]
   int ws_stride = 0;
+  int64_t glu_n = 0;  // > 0: gate|up rows interleaved for rk_matmul_w8a8_glu_dev, n = glu_n outputs
   float in_scale = 0.f, out_scale = 0.f;
   size_t bytes = 0;
   // MoE expert stack (kind 0, moe = true)
@@ -479,6 +480,70 @@ extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_
   return RK_OK;
 }
 
+// Gate and up Q8_0 weights of one gated MLP as one resident weight whose rows
+// alternate 16 gate rows and the same 16 up rows (32·ceil(n/16) rows, padding
+// rows zero), the layout rk_matmul_w8a8_glu_dev pairs in its epilogue.
+namespace {
+int64_t glu_rows(int64_t n) { return 32 * ((n + 15) / 16); }
+int64_t glu_row(int64_t r, int part) { return (r / 16) * 32 + 16 * part + r % 16; }
+}  // namespace
+
+extern "C" int rk_pack_q8_0_glu(const uint8_t *gate_blocks, const uint8_t *up_blocks, int64_t n,
+                                int64_t k, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_q8_0_glu"));
+  RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_glu"));
+  const int64_t rows = glu_rows(n), kb = k / 32;
+  std::vector<int8_t> codes((size_t)n * k), all((size_t)rows * k, 0);
+  std::vector<float> scales((size_t)n * kb), all_s((size_t)rows * kb, 0.f);
+  for (int part = 0; part < 2; ++part) {
+    parse_q8_0(part ? up_blocks : gate_blocks, n, k, codes.data(), scales.data());
+    for (int64_t r = 0; r < n; ++r) {
+      const int64_t d = glu_row(r, part);
+      memcpy(&all[d * k], &codes[r * k], (size_t)k);
+      memcpy(&all_s[d * kb], &scales[r * kb], (size_t)kb * 4);
+    }
+  }
+  RK_TRY(pack_i8_host(all.data(), all_s, rows, k, 32, id, "rk_pack_q8_0_glu"));
+  g_eng->weights[*id].glu_n = n;
+  return RK_OK;
+}
+
+extern "C" int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t n, int64_t k,
+                                    rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_pack_q8_0_glu_f32"));
+  RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_glu_f32"));
+  const int64_t rows = glu_rows(n);
+  Weight wt;
+  wt.kind = RK_WEIGHT_I8;
+  wt.n = rows;
+  wt.k = k;
+  wt.group = 32;
+  wt.glu_n = n;
+  wt.ws_stride = ws_stride_for(k);
+  void *x32;
+  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
+  HIP_TRY(hipMalloc(&wt.codes, (size_t)rows * k), "rk_pack_q8_0_glu_f32");
+  HIP_TRY(hipMalloc((void **)&wt.scales, (size_t)rows * wt.ws_stride * 4), "rk_pack_q8_0_glu_f32");
+  HIP_TRY(hipMemsetAsync(wt.codes, 0, (size_t)rows * k, g_eng->stream), "rk_pack_q8_0_glu_f32");
+  HIP_TRY(hipMemsetAsync(wt.scales, 0, (size_t)rows * wt.ws_stride * 4, g_eng->stream),
+          "rk_pack_q8_0_glu_f32");
+  for (int part = 0; part < 2; ++part) {
+    HIP_TRY(hipMemcpyAsync(x32, part ? up : gate, (size_t)n * k * 4, hipMemcpyHostToDevice,
+                           g_eng->stream),
+            "rk_pack_q8_0_glu_f32");
+    // rows land at (r/16)·32 + 16·part + r%16
+    HIP_TRY(rk_launch_q8_0_quantize((const float *)x32, n, k, 32, 16 * part, (int8_t *)wt.codes,
+                                    wt.scales, wt.ws_stride, false, g_eng->stream),
+            "rk_pack_q8_0_glu_f32");
+  }
+  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack_q8_0_glu_f32");
+  wt.bytes = (size_t)rows * k + (size_t)rows * wt.ws_stride * 4;
+  *id = insert(wt);
+  return RK_OK;
+}
+
 extern "C" int rk_pack_qat(const int8_t *codes, const float *w_scale, int64_t n, int64_t k,
                            float in_scale, float out_scale, rk_weight_id *id) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -558,6 +623,8 @@ extern "C" int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, 
   Weight *w = find(id);
   RK_TRY(check_m(m, k, w, "rk_matmul"));
   if (w->moe) return fail(RK_E_UNSUPPORTED, "rk_matmul", "an expert stack is not a matmul weight");
+  if (w->glu_n > 0)
+    return fail(RK_E_UNSUPPORTED, "rk_matmul", "gate|up weight: use rk_matmul_w8a8_glu_dev");
   const auto t0 = Clock::now();
   hipStream_t st = g_eng->stream;
   const int64_t n = w->n;
@@ -636,6 +703,7 @@ int w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale, int64_t a_g
   Weight *w = find(id);
   RK_TRY(check_m(m, k, w, op));
   if (w->kind != RK_WEIGHT_I8 || w->moe) return fail(RK_E_UNSUPPORTED, op, "weight is not group-wise int8");
+  if (w->glu_n > 0) return fail(RK_E_UNSUPPORTED, op, "gate|up weight: use rk_matmul_w8a8_glu_dev");
   int mode;
   if (a_group == k)
     mode = I8_PER_TOKEN;
@@ -649,6 +717,39 @@ int w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale, int64_t a_g
   return RK_OK;
 }
 }  // namespace
+
+extern "C" int rk_matmul_w8a8_glu_dev(rk_weight_id id, const int8_t *a, const float *a_scale,
+                                      int64_t m, int64_t k, int glu, void *out, int out_f16,
+                                      rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_matmul_w8a8_glu_dev";
+  RK_TRY(ensure(op));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, op));
+  if (w->glu_n <= 0) return fail(RK_E_UNSUPPORTED, op, "weight was not packed by rk_pack_q8_0_glu");
+  if (glu != RK_GLU_SILU && glu != RK_GLU_GELU) return fail(RK_E_SHAPE, op, "unknown glu kind");
+  I8GemmArgs g;
+  g.A = a;
+  g.AS = a_scale;
+  g.as_stride = 1;
+  g.a_gb = (int)(k / 32);
+  g.W = (const int8_t *)w->codes;
+  g.WS = w->scales;
+  g.ws_stride = w->ws_stride;
+  g.gb = 1;
+  g.C = out;
+  g.M = (int)m;
+  g.N = (int)w->n;
+  g.K = (int)w->k;
+  g.mode = I8_PER_TOKEN;
+  g.out_f16 = out_f16 != 0;
+  g.num_cus = g_eng->num_cus;
+  g.glu = glu;
+  g.n_out = (int)w->glu_n;
+  HIP_TRY(rk_launch_gemm_i8(g, pick(stream)), op);
+  g_eng->calls++;
+  return RK_OK;
+}
 
 extern "C" int rk_matmul_w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale,
                                   int64_t a_group, int64_t m, int64_t k, float *c,

@@ -300,11 +300,32 @@ static hipError_t launch_i8(const I8GemmArgs &g, hipStream_t st) {
 // scaled mode is VALU-bound at 1/4 of the int8 MFMA rate.
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2>
+// MLP glue applied to column pairs in the epilogue (GLU_SILU: silu(g)·u,
+// GLU_GELU: gelu_tanh(g)·u, the formulas of host.rs:12-39 in f32 without FMA
+// contraction). The weight rows come interleaved in 16-row groups, gate rows
+// 16q..16q+15 at 32q..32q+15 and the matching up rows at 32q+16..32q+31, so
+// in a 32-column MFMA tile lane l (l%32 < 16) holds a gate value and lane
+// l+16 the up value of the same output (row m, column 16q + l%32).
+enum { GLU_NONE = 0, GLU_SILU = 1, GLU_GELU = 2 };
+template <int GLU>
+__device__ __forceinline__ float glu_apply(float g, float u) {
+#pragma clang fp contract(off)
+  if constexpr (GLU == GLU_SILU) {
+    const float sigmoid = 1.0f / (1.0f + expf(-g));
+    return g * sigmoid * u;
+  } else {
+    constexpr float k = (float)(1.12837916709551257390 * 0.70710678118654752440);  // sqrt(2/pi)
+    const float inner = (g + g * g * g * 0.044715f) * k;
+    return ((g * (tanhf(inner) + 1.0f)) * 0.5f) * u;
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2,
+          int GLU = GLU_NONE>
 __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     const int8_t *__restrict__ A, const float *__restrict__ AS, const int8_t *__restrict__ W,
     const float *__restrict__ WS, int ws_stride, void *__restrict__ Cout, int M, int N, int K,
-    int tiles_m, int tiles_n, int group_m) {
+    int tiles_m, int tiles_n, int group_m, int n_out) {
   static_assert(MODE == MODE_PER_TOKEN || MODE == MODE_RAW, "per-token or raw");
   constexpr int NW = WM * WN;
   constexpr int NT = NW * 64;
@@ -544,6 +565,26 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn * WTN + j * 32 + fcol;
+      if constexpr (GLU != GLU_NONE) {
+        // gate lanes (fcol < 16) take the up value from lane + 16; output
+        // column 16·(n/32) + fcol of an [M, n_out] matrix
+        const int oc = ((n0 + wn * WTN + j * 32) >> 1) + fcol;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * WTM + i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
+          const float v = as4[r >> 2][r & 3] * facc[i][j][r];
+          const float u = __int_as_float(
+              __builtin_amdgcn_ds_bpermute((lane ^ 16) << 2, __float_as_int(v)));
+          if (fcol < 16 && m < M && oc < n_out) {
+            const float y = glu_apply<GLU>(v, u);
+            if constexpr (OUT_F16)
+              ((f16 *)Cout)[(size_t)m * n_out + oc] = (f16)y;
+            else
+              ((float *)Cout)[(size_t)m * n_out + oc] = y;
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * WTM + i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
@@ -563,11 +604,12 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2>
+template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2,
+          int GLU = GLU_NONE>
 static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   constexpr int smem =
       STAGES * ((BM + BN) * 128 + (MODE == MODE_PER_TOKEN ? BN * 16 : 0)) + BM * 4;
-  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16, MINW>;
+  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16, MINW, GLU>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -577,7 +619,8 @@ static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   }
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, g.A, g.AS, g.W, g.WS,
-                     g.ws_stride, g.C, g.M, g.N, g.K, tm, tn, rk_knob("RK_TILE_GROUP_M", 0));
+                     g.ws_stride, g.C, g.M, g.N, g.K, tm, tn, rk_knob("RK_TILE_GROUP_M", 0),
+                     GLU != GLU_NONE ? g.n_out : g.N);
   return hipGetLastError();
 }
 
@@ -588,6 +631,18 @@ static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
 //   >= 3/4 per CU: 128x128 tiles on 16 waves, one tile per CU (4 waves per SIMD);
 //   fewer:         128x64 tiles on 4 waves.
 // RK_Q8_TILE selects a configuration by number.
+// GLU epilogue launches: the three default configurations of launch_q8_cfg
+// (below), chosen by the same tile count.
+template <bool OUT_F16, int GLU>
+static hipError_t launch_q8_glu(const I8GemmArgs &g, hipStream_t st) {
+  const long t128 = ((g.M + 127) / 128) * (long)((g.N + 127) / 128);
+  if (t128 >= g.num_cus)
+    return launch_q8<128, 128, 2, 4, 2, MODE_PER_TOKEN, OUT_F16, 4, GLU>(g, st);
+  if (4 * t128 >= 3L * g.num_cus)
+    return launch_q8<128, 128, 4, 4, 2, MODE_PER_TOKEN, OUT_F16, 4, GLU>(g, st);
+  return launch_q8<128, 64, 2, 2, 3, MODE_PER_TOKEN, OUT_F16, 2, GLU>(g, st);
+}
+
 template <bool OUT_F16>
 static hipError_t launch_q8_cfg(const I8GemmArgs &g, hipStream_t st) {
   const long t128 = ((g.M + 127) / 128) * (long)((g.N + 127) / 128);
@@ -662,8 +717,14 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
   switch (g.mode) {
     case I8_PER_TOKEN:
       // One scale per 32-value block (GGUF Q8_0 / group 32): pipelined kernel.
-      if (g.gb == 1)
+      if (g.gb == 1) {
+        if (g.glu == GLU_SILU)
+          return g.out_f16 ? launch_q8_glu<true, GLU_SILU>(g, st) : launch_q8_glu<false, GLU_SILU>(g, st);
+        if (g.glu == GLU_GELU)
+          return g.out_f16 ? launch_q8_glu<true, GLU_GELU>(g, st) : launch_q8_glu<false, GLU_GELU>(g, st);
         return g.out_f16 ? launch_q8_cfg<true>(g, st) : launch_q8_cfg<false>(g, st);
+      }
+      if (g.glu != 0) return hipErrorInvalidValue;
       return dispatch_scaled<MODE_PER_TOKEN>(g, st);
     case I8_PER_GROUP:
       return dispatch_scaled<MODE_PER_GROUP>(g, st);

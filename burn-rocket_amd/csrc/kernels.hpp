@@ -35,6 +35,10 @@ struct I8GemmArgs {
   int mode;            // I8Mode
   bool out_f16;
   int num_cus;
+  // Per-token Q8_0 only: 1 silu·up, 2 gelu·up over gate/up rows interleaved
+  // in 16-row groups (N = 32·ceil(n_out/16) rows), output C [M, n_out].
+  int glu = 0;
+  int n_out = 0;
 };
 hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st);
 

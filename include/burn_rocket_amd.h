@@ -69,6 +69,10 @@ extern "C" {
 #define RK_DTYPE_F16 1
 #define RK_DTYPE_BF16 2
 
+/* Glue of the fused gate|up GEMM (rk_matmul_w8a8_glu_dev). */
+#define RK_GLU_SILU 1
+#define RK_GLU_GELU 2
+
 typedef uint64_t rk_weight_id;
 typedef void *rk_stream; /* a hipStream_t; NULL selects the library stream */
 
@@ -310,6 +314,24 @@ int rk_gelu_mul_dev(const void *a, const void *b, void *out, int64_t n, int dtyp
 /* Host-buffer forms on f32 arrays (synchronous). */
 int rk_silu_mul(const float *a, const float *b, float *out, int64_t n);
 int rk_gelu_mul(const float *a, const float *b, float *out, int64_t n);
+
+/* A gated MLP's first projection in one W8A8 GEMM with the glue in its
+ * epilogue: out [M, n] = glue(gate·x, up·x), glue = silu_mul (RK_GLU_SILU)
+ * or gelu_mul (RK_GLU_GELU). It fuses what the reference runs as two
+ * matmuls and a glue op (`matmul_impl` ext.rs:1184-1232 on the gate and up
+ * weights, then `rocket_silu_mul` / `rocket_gelu_mul` ext.rs:603-608; the
+ * glue formulas host.rs:12-39): the gate and up products are the per-token
+ * W8A8 results of rk_matmul_w8a8_dev (a int8 [M, K] with one scale per row,
+ * a_scale [M]), the glue is computed in f32 and out is f32 or fp16
+ * (out_f16). The weight comes from rk_pack_q8_0_glu (GGUF Q8_0 blocks of the
+ * gate and up matrices, each [n, K]) or rk_pack_q8_0_glu_f32 (f32 gate and
+ * up, quantized to Q8_0 on the device); such a weight is only accepted here. */
+int rk_pack_q8_0_glu(const uint8_t *gate_blocks, const uint8_t *up_blocks, int64_t n,
+                     int64_t k, rk_weight_id *id);
+int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t n, int64_t k,
+                         rk_weight_id *id);
+int rk_matmul_w8a8_glu_dev(rk_weight_id id, const int8_t *a, const float *a_scale, int64_t m,
+                           int64_t k, int glu, void *out, int out_f16, rk_stream stream);
 
 /* ======================================================================== *
  * Device plumbing for callers without their own HIP runtime bindings       *

@@ -249,3 +249,51 @@ def test_device_q8_0_packer_equals_gguf_blocks(rk, orc):
     assert (s1 == s2).all()
     d32 = wd.view(np.float16).astype(np.float32)
     assert (s2 == (wq.astype(np.float32) * np.repeat(d32, 32, axis=1)).T).all()
+
+
+# Fused gate|up GEMM with the MLP glue in the epilogue: glue(gate·x, up·x)
+# against the oracle's two W8A8 products and its glue (host.rs:12-39).
+# Shapes select each tile configuration of the fused launch on a 256-CU
+# MI355X: 2 / 224 / 256 tiles of 128x128 over the interleaved rows (n = 100
+# also leaves padding rows in the last 16-row group).
+@pytest.mark.parametrize("glu", ["silu", "gelu"])
+@pytest.mark.parametrize("m,k,n", [(70, 512, 100), (1700, 256, 1024), (2048, 256, 1024)])
+def test_w8a8_glu_fused(rk, orc, glu, m, k, n):
+    r = np.random.default_rng(m + k + n + len(glu))
+    x = r.standard_normal((m, k)).astype(np.float32)
+    gate = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    up = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    gq, gd = orc.q8_0_quantize(gate)
+    uq, ud = orc.q8_0_quantize(up)
+    aq, a_s = orc.quantize_rows(x, k)
+    f = lambda d: d.view(np.float16).astype(np.float32)
+    g_ref = orc.emu_matmul_gw(aq, a_s, k, gq, f(gd), 32)
+    u_ref = orc.emu_matmul_gw(aq, a_s, k, uq, f(ud), 32)
+    ref = (orc.silu_mul if glu == "silu" else orc.gelu_mul)(g_ref, u_ref)
+    kind = rk.GLU_SILU if glu == "silu" else rk.GLU_GELU
+    dq, ds = quantize_dev(rk, x, k)
+    lib = _lib(rk)
+    for packer in ("blocks", "f32"):
+        if packer == "blocks":
+            wid = rk.pack_q8_0_glu(orc.q8_0_blocks(gq, gd), orc.q8_0_blocks(uq, ud), n, k)
+        else:
+            wid = rk.pack_q8_0_glu_f32(gate, up)
+        for f16out in (False, True):
+            note(f"W8A8 fused {glu} m={m} k={k} n={n} packer={packer} f16out={f16out}")
+            dc = rk.DeviceBuffer(m * n * (2 if f16out else 4))
+            rc = lib.rk_matmul_w8a8_glu_dev(int(wid), dq.ptr, ds.ptr, m, k, kind, dc.ptr, int(f16out), None)
+            assert rc == 0, lib.rk_last_error()
+            rk.synchronize()
+            if f16out:
+                got = dc.download((m, n), np.uint16).view(np.float16).astype(np.float32)
+            else:
+                got = dc.download((m, n), np.float32)
+                assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+            check(orc, got, ref)
+            dc.free()
+        # a fused weight is only accepted by the fused entry point, and vice versa
+        dc = rk.DeviceBuffer(m * 2 * n * 4)
+        assert lib.rk_matmul_w8a8_dev(int(wid), dq.ptr, ds.ptr, k, m, k, dc.ptr, None) == rk.RK_E_UNSUPPORTED
+        dc.free()
+    plain = rk.pack_q8_0(orc.q8_0_blocks(gq, gd), n, k)
+    assert lib.rk_matmul_w8a8_glu_dev(int(plain), dq.ptr, ds.ptr, m, k, kind, None, 0, None) == rk.RK_E_UNSUPPORTED
