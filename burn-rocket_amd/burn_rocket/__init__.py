@@ -80,6 +80,12 @@ SIGNATURES = {
     "rk_pack_q8_0_glu_f32": (_i, [_p, _p, _i64, _i64, _p]),
     "rk_matmul_w8a8_glu_dev": (_i, [_u64, _p, _p, _i64, _i64, _i, _p, _i, _p]),
     "rk_gelu_mul": (_i, [_p, _p, _p, _i64]),
+    "rk_rms_norm_dev": (_i, [_p, _p, _i, _p, _i64, _i64, _c.c_double, _i, _p]),
+    "rk_rms_norm_noscale_dev": (_i, [_p, _p, _i64, _i64, _c.c_double, _i, _p]),
+    "rk_rope_dev": (_i, [_p, _p, _p, _i, _p, _i64, _i64, _i64, _i64, _i, _p]),
+    "rk_rms_norm": (_i, [_p, _p, _p, _i64, _i64, _c.c_double]),
+    "rk_rms_norm_noscale": (_i, [_p, _p, _i64, _i64, _c.c_double]),
+    "rk_rope": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64]),
     "rk_memset_dev": (_i, [_p, _i, _sz]),
     "rk_stream_get": (_i, [_p]),
     "rk_stream_sync": (_i, [_p]),
@@ -327,6 +333,74 @@ def silu_mul(a, b, bf16=False):
 def gelu_mul(a, b, bf16=False):
     """`gelu_approximate(a) * b` (`rocket_gelu_mul`, ext.rs:603-604); as silu_mul."""
     return _glue("rk_gelu_mul_dev", "rocket_gelu_mul", a, b, bf16)
+
+
+def _float_dtype(a, bf16, op_name):
+    if bf16:
+        assert a.dtype == np.uint16, "bf16 values are passed as their uint16 bits"
+        return DTYPE_BF16
+    if a.dtype == np.float16:
+        return DTYPE_F16
+    if a.dtype == np.float32:
+        return DTYPE_F32
+    raise AssertionError(f"unsupported {op_name} dtype {a.dtype} (f32/f16/bf16)")
+
+
+def _run_dev(fn_name, op_name, out_like, inputs, build_args):
+    """Upload `inputs`, call `fn_name` with build_args(device pointers, out pointer),
+    return the output shaped and typed like out_like."""
+    bufs = [DeviceBuffer.from_array(np.ascontiguousarray(a)) for a in inputs]
+    do = DeviceBuffer(max(out_like.nbytes, 1))
+    try:
+        _check(getattr(_lib, fn_name)(*build_args([b.ptr for b in bufs], do.ptr)), op_name)
+        synchronize()
+        return do.download(out_like.shape, out_like.dtype)
+    finally:
+        for buf in bufs + [do]:
+            buf.free()
+
+
+def rms_norm(x, w, eps, bf16=False):
+    """Weighted RMSNorm over the last dim, `x * (mean(x^2) + eps)^-0.5 * w`
+    (`burn_rocket::rms_norm`, ext.rs:2112-2119): x f32/f16 (or bf16 bits with
+    bf16=True), w [D] of the same type; computed in f32, returned in x's type."""
+    x, w = np.asarray(x), np.asarray(w)
+    dt = _float_dtype(x, bf16, "rocket_rms_norm")
+    assert x.ndim >= 1, "rms_norm needs at least one dim"
+    d = x.shape[-1]
+    assert w.shape == (d,) and w.dtype == x.dtype, "rms_norm: the weight has the last dim's size"
+    if x.size == 0:
+        return x.copy()
+    return _run_dev("rk_rms_norm_dev", "rocket_rms_norm", x, [x, w],
+                    lambda p, o: (p[0], p[1], dt, o, x.size // d, d, float(eps), dt, None))
+
+
+def rms_norm_noscale(x, eps, bf16=False):
+    """Scale-free RMSNorm over the last dim (`burn_rocket::rms_norm_noscale`,
+    ext.rs:2121-2128); as rms_norm."""
+    x = np.asarray(x)
+    dt = _float_dtype(x, bf16, "rocket_rms_norm_noscale")
+    d = x.shape[-1]
+    if x.size == 0:
+        return x.copy()
+    return _run_dev("rk_rms_norm_noscale_dev", "rocket_rms_norm_noscale", x, [x],
+                    lambda p, o: (p[0], o, x.size // d, d, float(eps), dt, None))
+
+
+def rope_apply(x, cos, sin, bf16=False):
+    """Rotate-half RoPE (`burn_rocket::rope_apply`, ext.rs:2130-2137): x
+    [B, S, H, D], cos/sin [S, D/2] of x's type; returned in x's type."""
+    x, cos, sin = np.asarray(x), np.asarray(cos), np.asarray(sin)
+    dt = _float_dtype(x, bf16, "rocket_rope")
+    assert x.ndim == 4, "rope: x must be [B, S, H, D]"
+    b, s, h, d = x.shape
+    assert d % 2 == 0, "rope: the head dim must be even"
+    assert cos.shape == (s, d // 2) and cos.dtype == x.dtype, "rope: cos must be [S, D/2]"
+    assert sin.shape == (s, d // 2) and sin.dtype == x.dtype, "rope: sin must be [S, D/2]"
+    if x.size == 0:
+        return x.copy()
+    return _run_dev("rk_rope_dev", "rocket_rope", x, [x, cos, sin],
+                    lambda p, o: (p[0], p[1], p[2], dt, o, b, s, h, d, dt, None))
 
 
 def _attention(q, k, v, n_head, n_kv_heads, head_dim, scale, softcap, mode, window, q0, k0):

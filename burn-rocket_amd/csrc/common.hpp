@@ -119,3 +119,72 @@ __device__ __forceinline__ void static_for(F &&f) {
 
 static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+
+// ---- element types of the float ops (RK_DTYPE_*) -----------------------------
+// f32 → bf16 bits, round to nearest even; a NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+template <int DT>
+using dt_storage = std::conditional_t<DT == RK_DTYPE_F32, uint32_t, uint16_t>;
+// Storage bits → f32 (the argument is a scalar: see dt_load_vec).
+template <int DT>
+__device__ __forceinline__ float dt_decode(dt_storage<DT> s) {
+  if constexpr (DT == RK_DTYPE_F32) return __uint_as_float(s);
+  else if constexpr (DT == RK_DTYPE_F16) return (float)__builtin_bit_cast(f16, s);
+  else return __uint_as_float((uint32_t)s << 16);
+}
+template <int DT>
+__device__ __forceinline__ dt_storage<DT> dt_encode(float v) {
+  if constexpr (DT == RK_DTYPE_F32) return __float_as_uint(v);
+  else if constexpr (DT == RK_DTYPE_F16) return __builtin_bit_cast(uint16_t, (f16)v);
+  else return f32_to_bf16_rne(v);
+}
+template <int DT>
+__device__ __forceinline__ float dt_load(const void *p, int64_t i) {
+  return dt_decode<DT>(((const dt_storage<DT> *)p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void dt_store(void *p, int64_t i, float v) {
+  ((dt_storage<DT> *)p)[i] = dt_encode<DT>(v);
+}
+// Element type known only at run time (a wave-uniform branch).
+__device__ __forceinline__ float dt_load_any(const void *p, int64_t i, int dt) {
+  if (dt == RK_DTYPE_F32) return dt_load<RK_DTYPE_F32>(p, i);
+  if (dt == RK_DTYPE_F16) return dt_load<RK_DTYPE_F16>(p, i);
+  return dt_load<RK_DTYPE_BF16>(p, i);
+}
+// N consecutive elements from element i in one access; p + i must be aligned
+// to N elements. Each element is copied to a scalar before it is decoded:
+// hipcc 7.2 miscompiles a bit cast applied directly to a vector subscript.
+template <int DT, int N>
+__device__ __forceinline__ void dt_load_vec(const void *p, int64_t i, float *f) {
+  using S = dt_storage<DT>;
+  if constexpr (N == 1) {
+    f[0] = dt_decode<DT>(((const S *)p)[i]);
+  } else {
+    typedef S SV __attribute__((ext_vector_type(N)));
+    const SV v = *(const SV *)((const S *)p + i);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const S s = v[e];
+      f[e] = dt_decode<DT>(s);
+    }
+  }
+}
+template <int DT, int N>
+__device__ __forceinline__ void dt_store_vec(void *p, int64_t i, const float *f) {
+  using S = dt_storage<DT>;
+  if constexpr (N == 1) {
+    ((S *)p)[i] = dt_encode<DT>(f[0]);
+  } else {
+    typedef S SV __attribute__((ext_vector_type(N)));
+    SV v;
+#pragma unroll
+    for (int e = 0; e < N; ++e) v[e] = dt_encode<DT>(f[e]);
+    *(SV *)((S *)p + i) = v;
+  }
+}

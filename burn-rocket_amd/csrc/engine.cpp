@@ -1417,6 +1417,117 @@ extern "C" int rk_gelu_mul(const float *a, const float *b, float *out, int64_t n
   return glue_host(1, a, b, out, n, "rk_gelu_mul");
 }
 
+// =========================================================================
+// RMSNorm and RoPE
+// =========================================================================
+namespace {
+bool float_dtype(int dt) { return dt >= RK_DTYPE_F32 && dt <= RK_DTYPE_BF16; }
+size_t dtype_bytes(int dt) { return dt == RK_DTYPE_F32 ? 4 : 2; }
+
+int rms_check(const void *x, const void *out, int64_t rows, int64_t d, int dtype,
+              const char *name) {
+  if (rows < 0) return fail(RK_E_SHAPE, name, "negative row count");
+  if (d <= 0 || d > INT32_MAX) return fail(RK_E_SHAPE, name, "the last dim must be in [1, 2^31)");
+  if (!float_dtype(dtype)) return fail(RK_E_SHAPE, name, "unknown dtype");
+  if (rows > 0 && (!x || !out)) return fail(RK_E_SHAPE, name, "null buffer");
+  return RK_OK;
+}
+int rope_check(const void *x, const void *cs, const void *sn, const void *out, int64_t b,
+               int64_t s, int64_t h, int64_t d, int dtype, int cs_dtype, const char *name) {
+  if (b < 0 || s < 0 || h < 0 || d < 0) return fail(RK_E_SHAPE, name, "x must be [B, S, H, D]");
+  if (d % 2 != 0) return fail(RK_E_SHAPE, name, "the head dim must be even");
+  if (!float_dtype(dtype) || !float_dtype(cs_dtype)) return fail(RK_E_SHAPE, name, "unknown dtype");
+  if (b * s * h > INT32_MAX || d > INT32_MAX)
+    return fail(RK_E_SHAPE, name, "B·S·H and D must be below 2^31");
+  if (b * s * h * d > 0 && (!x || !cs || !sn || !out)) return fail(RK_E_SHAPE, name, "null buffer");
+  return RK_OK;
+}
+int rms_host(const float *x, const float *w, float *out, int64_t rows, int64_t d, double eps,
+             const char *name) {
+  RK_TRY(ensure(name));
+  RK_TRY(rms_check(x, out, rows, d, RK_DTYPE_F32, name));
+  if (rows == 0) return RK_OK;
+  const size_t n = (size_t)(rows * d);
+  void *buf = nullptr;
+  RK_TRY(scratch("norm", (n + (size_t)d) * 4, &buf));
+  float *dx = (float *)buf, *dw = dx + n;
+  hipStream_t st = g_eng->stream;
+  HIP_TRY(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, st), name);
+  if (w) HIP_TRY(hipMemcpyAsync(dw, w, (size_t)d * 4, hipMemcpyHostToDevice, st), name);
+  HIP_TRY(rk_launch_rms_norm(dx, w ? dw : nullptr, RK_DTYPE_F32, dx, rows, (int)d, (float)eps,
+                             RK_DTYPE_F32, st), name);
+  HIP_TRY(hipMemcpyAsync(out, dx, n * 4, hipMemcpyDeviceToHost, st), name);
+  HIP_TRY(hipStreamSynchronize(st), name);
+  return RK_OK;
+}
+}  // namespace
+
+extern "C" int rk_rms_norm_dev(const void *x, const void *w, int w_dtype, void *out, int64_t rows,
+                               int64_t d, double eps, int dtype, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_rms_norm_dev";
+  RK_TRY(ensure(name));
+  RK_TRY(rms_check(x, out, rows, d, dtype, name));
+  if (!float_dtype(w_dtype)) return fail(RK_E_SHAPE, name, "unknown weight dtype");
+  if (rows > 0 && !w) return fail(RK_E_SHAPE, name, "null weight");
+  HIP_TRY(rk_launch_rms_norm(x, w, w_dtype, out, rows, (int)d, (float)eps, dtype, pick(stream)),
+          name);
+  return RK_OK;
+}
+extern "C" int rk_rms_norm_noscale_dev(const void *x, void *out, int64_t rows, int64_t d,
+                                       double eps, int dtype, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_rms_norm_noscale_dev";
+  RK_TRY(ensure(name));
+  RK_TRY(rms_check(x, out, rows, d, dtype, name));
+  HIP_TRY(rk_launch_rms_norm(x, nullptr, RK_DTYPE_F32, out, rows, (int)d, (float)eps, dtype,
+                             pick(stream)), name);
+  return RK_OK;
+}
+extern "C" int rk_rope_dev(const void *x, const void *cos, const void *sin, int cs_dtype, void *out,
+                           int64_t b, int64_t s, int64_t h, int64_t d, int dtype,
+                           rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_rope_dev";
+  RK_TRY(ensure(name));
+  RK_TRY(rope_check(x, cos, sin, out, b, s, h, d, dtype, cs_dtype, name));
+  HIP_TRY(rk_launch_rope(x, cos, sin, cs_dtype, out, (int)(b * s * h), (int)s, (int)h, (int)(d / 2),
+                         dtype, pick(stream)), name);
+  return RK_OK;
+}
+extern "C" int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d,
+                           double eps) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (rows > 0 && !w) return fail(RK_E_SHAPE, "rk_rms_norm", "null weight");
+  return rms_host(x, w, out, rows, d, eps, "rk_rms_norm");
+}
+extern "C" int rk_rms_norm_noscale(const float *x, float *out, int64_t rows, int64_t d,
+                                   double eps) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return rms_host(x, nullptr, out, rows, d, eps, "rk_rms_norm_noscale");
+}
+extern "C" int rk_rope(const float *x, const float *cos, const float *sin, float *out, int64_t b,
+                       int64_t s, int64_t h, int64_t d) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_rope";
+  RK_TRY(ensure(name));
+  RK_TRY(rope_check(x, cos, sin, out, b, s, h, d, RK_DTYPE_F32, RK_DTYPE_F32, name));
+  const size_t n = (size_t)(b * s * h * d), nt = (size_t)(s * (d / 2));
+  if (n == 0) return RK_OK;
+  void *buf = nullptr;
+  RK_TRY(scratch("rope", (n + 2 * nt) * 4, &buf));
+  float *dx = (float *)buf, *dc = dx + n, *ds = dc + nt;
+  hipStream_t st = g_eng->stream;
+  HIP_TRY(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, st), name);
+  HIP_TRY(hipMemcpyAsync(dc, cos, nt * 4, hipMemcpyHostToDevice, st), name);
+  HIP_TRY(hipMemcpyAsync(ds, sin, nt * 4, hipMemcpyHostToDevice, st), name);
+  HIP_TRY(rk_launch_rope(dx, dc, ds, RK_DTYPE_F32, dx, (int)(b * s * h), (int)s, (int)h,
+                         (int)(d / 2), RK_DTYPE_F32, st), name);
+  HIP_TRY(hipMemcpyAsync(out, dx, n * 4, hipMemcpyDeviceToHost, st), name);
+  HIP_TRY(hipStreamSynchronize(st), name);
+  return RK_OK;
+}
+
 extern "C" int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_stream stream) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_memcpy_dtod"));

@@ -50,6 +50,14 @@ hipError_t rk_launch_f16_to_f32(const void *x, float *y, int64_t n, hipStream_t 
 hipError_t rk_launch_glue(int op, const void *a, const void *b, void *out, int64_t n, int dtype,
                           hipStream_t st);
 
+// RMSNorm over rows of d values: w null (no weight) or of type w_dtype.
+hipError_t rk_launch_rms_norm(const void *x, const void *w, int w_dtype, void *out, int64_t rows,
+                              int d, float eps, int dtype, hipStream_t st);
+// Rotate-half RoPE over rows = B·S·H rows of 2·half values; cos/sin [S, half]
+// of type cs_dtype.
+hipError_t rk_launch_rope(const void *x, const void *cs, const void *sn, int cs_dtype, void *out,
+                          int rows, int S, int H, int half, int dtype, hipStream_t st);
+
 // Per-row symmetric quantizer (scale = max(amax/127, 1e-12), codes
 // round-half-away(x·(1/scale)) clamped to ±127), `group` values per scale.
 hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,

@@ -262,23 +262,6 @@ __device__ __forceinline__ float glue_gelu_mul(float g, float u) {
   return ((g * (tanhf(inner) + 1.0f)) * 0.5f) * u;
 }
 
-template <int DT>
-__device__ __forceinline__ float glue_load(const void *p, int64_t i) {
-  if constexpr (DT == RK_DTYPE_F32) return ((const float *)p)[i];
-  if constexpr (DT == RK_DTYPE_F16) return (float)((const f16 *)p)[i];
-  return __uint_as_float((uint32_t)((const uint16_t *)p)[i] << 16);
-}
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
-template <int DT>
-__device__ __forceinline__ void glue_store(void *p, int64_t i, float v) {
-  if constexpr (DT == RK_DTYPE_F32) ((float *)p)[i] = v;
-  else if constexpr (DT == RK_DTYPE_F16) ((f16 *)p)[i] = (f16)v;
-  else ((uint16_t *)p)[i] = f32_to_bf16_rne(v);
-}
 }  // namespace
 
 template <int OP, int DT, bool VEC>
@@ -324,8 +307,8 @@ __global__ __launch_bounds__(256) void glue_kernel(const void *__restrict__ a,
       *(uintx4 *)((uint8_t *)out + i0 * (16 / V)) = ov;
     } else {
       for (int64_t i = i0; i < n && i < i0 + V; ++i) {
-        const float g = glue_load<DT>(a, i), u = glue_load<DT>(b, i);
-        glue_store<DT>(out, i, OP == 0 ? glue_silu_mul(g, u) : glue_gelu_mul(g, u));
+        const float g = dt_load<DT>(a, i), u = dt_load<DT>(b, i);
+        dt_store<DT>(out, i, OP == 0 ? glue_silu_mul(g, u) : glue_gelu_mul(g, u));
       }
     }
   }

@@ -1,0 +1,281 @@
+// Row normalisation and rotary position embedding on the GPU.
+//
+// RMSNorm: out = x·inv·w, or x·inv with no weight, inv = 1/sqrt(Σx²/d + eps)
+// over each row of d values (rocket_rms_norm / rocket_rms_norm_noscale,
+// ext.rs:75-80 and 611-615, rms_norm_impl ext.rs:1093-1123, row formula
+// host.rs:40-56).
+// RoPE, rotate-half form, x [B, S, H, D] with cos/sin [S, D/2]:
+//   out[j]     = x[j]·cos[j] − x[D/2 + j]·sin[j]
+//   out[D/2+j] = x[D/2 + j]·cos[j] + x[j]·sin[j]
+// (rocket_rope, ext.rs:82-84 and 617-619, rope_impl ext.rs:1125-1152, row
+// formula host.rs:58-75).
+//
+// Both compute in f32 in the reference's operation order with no FMA
+// contraction; x and out are f32, fp16 or bf16 (out rounded to nearest even
+// in x's type); the weight and the cos/sin tables may have another float
+// type. out may be the same buffer as x. Both kernels are HBM-bound: each
+// value of x is read once and each value of out written once.
+#include <algorithm>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace {
+constexpr int es_of(int dt) { return dt == RK_DTYPE_F32 ? 4 : 2; }
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// RMSNorm. A row is shared by LPR lanes (a wave holds 64/LPR rows). The row is
+// cut into chunks of CV values (16 bytes when VEC, else one value); lane l
+// takes chunks l, l + LPR, l + 2·LPR, ... With NC > 0 a lane keeps its (at
+// most NC) chunks in registers between the sum and the scaling, so x is read
+// once; NC == 0 is for rows too long for that and reads each row twice, the
+// second time from cache.
+// The sum of squares: each lane adds its values in order (chunk, then value),
+// then the LPR partial sums meet in a butterfly. The order is fixed, so the
+// result is deterministic; it differs from the reference's left-to-right sum
+// only by the rounding of a different summation order.
+// WT: weight element type, or -1 for no weight. The VEC kernels read CV weight
+// values per chunk in one access.
+// ---------------------------------------------------------------------------
+template <int DT, int WT, bool VEC, int LPR, int NC>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const void *__restrict__ x,
+                                                       const void *__restrict__ w,
+                                                       void *__restrict__ out, int64_t rows, int d,
+                                                       float eps) {
+#pragma clang fp contract(off)
+  constexpr int CV = VEC ? 16 / es_of(DT) : 1;
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, li = lane % LPR;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int nch = d / CV;
+  const float fd = (float)d;
+  // the loop bound is the same for every lane of a wave (the shuffles need all 64)
+  for (int64_t r0 = wave * RPW; r0 < rows; r0 += n_waves * RPW) {
+    const int64_t row = r0 + lane / LPR;
+    const bool live = row < rows;
+    const int64_t base = row * (int64_t)d;
+    float acc = 0.f;
+    float v[NC > 0 ? NC : 1][CV];
+    if constexpr (NC > 0) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int ch = li + LPR * i;
+        if (live && ch < nch) {
+          dt_load_vec<DT, CV>(x, base + (int64_t)ch * CV, v[i]);
+#pragma unroll
+          for (int e = 0; e < CV; ++e) acc += v[i][e] * v[i][e];
+        }
+      }
+    } else {
+      if (live)
+        for (int ch = li; ch < nch; ch += LPR) {
+          dt_load_vec<DT, CV>(x, base + (int64_t)ch * CV, v[0]);
+#pragma unroll
+          for (int e = 0; e < CV; ++e) acc += v[0][e] * v[0][e];
+        }
+    }
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    const float inv = 1.0f / sqrtf(acc / fd + eps);
+    auto emit = [&](int ch, float *f) {
+      float o[CV];
+      if constexpr (WT >= 0) {
+        float wv[CV];
+        dt_load_vec<WT, CV>(w, (int64_t)ch * CV, wv);
+#pragma unroll
+        for (int e = 0; e < CV; ++e) o[e] = f[e] * inv * wv[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < CV; ++e) o[e] = f[e] * inv;
+      }
+      dt_store_vec<DT, CV>(out, base + (int64_t)ch * CV, o);
+    };
+    if constexpr (NC > 0) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int ch = li + LPR * i;
+        if (live && ch < nch) emit(ch, v[i]);
+      }
+    } else {
+      if (live)
+        for (int ch = li; ch < nch; ch += LPR) {
+          dt_load_vec<DT, CV>(x, base + (int64_t)ch * CV, v[0]);
+          emit(ch, v[0]);
+        }
+    }
+  }
+}
+
+// Scalar-path kernel for weight types that differ from x's and misaligned
+// buffers: one value per chunk, rows read twice, weight type at run time.
+template <int DT>
+__global__ __launch_bounds__(256) void rms_norm_any_kernel(const void *__restrict__ x,
+                                                           const void *__restrict__ w, int wt,
+                                                           void *__restrict__ out, int64_t rows,
+                                                           int d, float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const float fd = (float)d;
+  for (int64_t row = wave; row < rows; row += n_waves) {
+    const int64_t base = row * (int64_t)d;
+    float acc = 0.f;
+    for (int c = lane; c < d; c += 64) {
+      const float f = dt_load<DT>(x, base + c);
+      acc += f * f;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    const float inv = 1.0f / sqrtf(acc / fd + eps);
+    for (int c = lane; c < d; c += 64) {
+      const float f = dt_load<DT>(x, base + c);
+      dt_store<DT>(out, base + c, w ? f * inv * dt_load_any(w, c, wt) : f * inv);
+    }
+  }
+}
+
+namespace {
+template <int DT, int WT, bool VEC, int LPR, int NC>
+hipError_t launch_rms_cfg(const void *x, const void *w, void *out, int64_t rows, int d, float eps,
+                          hipStream_t st) {
+  const int64_t rows_per_block = 4 * (64 / LPR);
+  const unsigned blocks =
+      (unsigned)std::min<int64_t>((rows + rows_per_block - 1) / rows_per_block, 16384);
+  hipLaunchKernelGGL((rms_norm_kernel<DT, WT, VEC, LPR, NC>), dim3(blocks), dim3(256), 0, st, x,
+                     w, out, rows, d, eps);
+  return hipGetLastError();
+}
+
+// Chunks per row → (lanes per row, chunks per lane); more than 512 chunks
+// (8 KB of f16 values) stream.
+template <int DT, int WT>
+hipError_t launch_rms_vec(const void *x, const void *w, void *out, int64_t rows, int d, float eps,
+                          hipStream_t st) {
+  const int nch = d / (16 / es_of(DT));
+  if (nch <= 8) return launch_rms_cfg<DT, WT, true, 8, 1>(x, w, out, rows, d, eps, st);
+  if (nch <= 16) return launch_rms_cfg<DT, WT, true, 16, 1>(x, w, out, rows, d, eps, st);
+  if (nch <= 32) return launch_rms_cfg<DT, WT, true, 32, 1>(x, w, out, rows, d, eps, st);
+  if (nch <= 64) return launch_rms_cfg<DT, WT, true, 64, 1>(x, w, out, rows, d, eps, st);
+  if (nch <= 128) return launch_rms_cfg<DT, WT, true, 64, 2>(x, w, out, rows, d, eps, st);
+  if (nch <= 256) return launch_rms_cfg<DT, WT, true, 64, 4>(x, w, out, rows, d, eps, st);
+  if (nch <= 512) return launch_rms_cfg<DT, WT, true, 64, 8>(x, w, out, rows, d, eps, st);
+  return launch_rms_cfg<DT, WT, true, 64, 0>(x, w, out, rows, d, eps, st);
+}
+
+template <int DT>
+hipError_t launch_rms_t(const void *x, const void *w, int wt, void *out, int64_t rows, int d,
+                        float eps, hipStream_t st) {
+  constexpr int CV = 16 / es_of(DT);
+  const bool xo_vec = d % CV == 0 && (((uintptr_t)x | (uintptr_t)out) & 15) == 0;
+  if (xo_vec && !w) return launch_rms_vec<DT, -1>(x, w, out, rows, d, eps, st);
+  if (xo_vec && wt == DT && ((uintptr_t)w & 15) == 0)
+    return launch_rms_vec<DT, DT>(x, w, out, rows, d, eps, st);
+  const unsigned blocks = (unsigned)std::min<int64_t>((rows + 3) / 4, 16384);
+  hipLaunchKernelGGL((rms_norm_any_kernel<DT>), dim3(blocks), dim3(256), 0, st, x, w, wt, out,
+                     rows, d, eps);
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t rk_launch_rms_norm(const void *x, const void *w, int w_dtype, void *out, int64_t rows,
+                              int d, float eps, int dtype, hipStream_t st) {
+  if (rows <= 0 || d <= 0) return hipSuccess;
+  switch (dtype) {
+    case RK_DTYPE_F32: return launch_rms_t<RK_DTYPE_F32>(x, w, w_dtype, out, rows, d, eps, st);
+    case RK_DTYPE_F16: return launch_rms_t<RK_DTYPE_F16>(x, w, w_dtype, out, rows, d, eps, st);
+    case RK_DTYPE_BF16: return launch_rms_t<RK_DTYPE_BF16>(x, w, w_dtype, out, rows, d, eps, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// RoPE. A thread rotates CV consecutive pairs (j, D/2 + j) of one row
+// (b, s, h); a block covers 256/hc whole rows, hc = (D/2)/CV, or one row in
+// steps of 256 when hc > 256. Row r = (b·S + s)·H + h reads table row s =
+// (r / H) mod S.
+// ---------------------------------------------------------------------------
+template <int DT, int CT, int CV>
+__global__ __launch_bounds__(256) void rope_kernel(const void *__restrict__ x,
+                                                   const void *__restrict__ cs,
+                                                   const void *__restrict__ sn,
+                                                   void *__restrict__ out, int rows, int S, int H,
+                                                   int half) {
+#pragma clang fp contract(off)
+  const int hc = half / CV;
+  const int rpb = hc >= 256 ? 1 : 256 / hc;
+  const int t = threadIdx.x;
+  const int rl = t / hc;
+  const int row = blockIdx.x * rpb + rl;
+  if (rl >= rpb || row >= rows) return;
+  const int si = (row / H) % S;
+  const int64_t xb = (int64_t)row * (2 * half), tb = (int64_t)si * half;
+  for (int jc = t % hc; jc < hc; jc += 256) {
+    const int j = jc * CV;
+    float x1[CV], x2[CV], c[CV], s[CV], o1[CV], o2[CV];
+    dt_load_vec<DT, CV>(x, xb + j, x1);
+    dt_load_vec<DT, CV>(x, xb + half + j, x2);
+    dt_load_vec<CT, CV>(cs, tb + j, c);
+    dt_load_vec<CT, CV>(sn, tb + j, s);
+#pragma unroll
+    for (int e = 0; e < CV; ++e) {
+      o1[e] = x1[e] * c[e] - x2[e] * s[e];
+      o2[e] = x2[e] * c[e] + x1[e] * s[e];
+    }
+    dt_store_vec<DT, CV>(out, xb + j, o1);
+    dt_store_vec<DT, CV>(out, xb + half + j, o2);
+  }
+}
+
+namespace {
+template <int DT, int CT, int CV>
+hipError_t launch_rope_cfg(const void *x, const void *cs, const void *sn, void *out, int rows,
+                           int S, int H, int half, hipStream_t st) {
+  const int hc = half / CV;
+  const int rpb = hc >= 256 ? 1 : 256 / hc;
+  const unsigned blocks = (unsigned)((rows + rpb - 1) / rpb);
+  hipLaunchKernelGGL((rope_kernel<DT, CT, CV>), dim3(blocks), dim3(256), 0, st, x, cs, sn, out,
+                     rows, S, H, half);
+  return hipGetLastError();
+}
+
+// The widest CV (at most 16 bytes of x) that divides D/2 and that every
+// buffer's alignment allows.
+template <int DT, int CT>
+hipError_t launch_rope_t(const void *x, const void *cs, const void *sn, void *out, int rows, int S,
+                         int H, int half, hipStream_t st) {
+  const uintptr_t xa = (uintptr_t)x | (uintptr_t)out, ca = (uintptr_t)cs | (uintptr_t)sn;
+  auto fits = [&](int cv) {
+    return half % cv == 0 && xa % (cv * es_of(DT)) == 0 && ca % (cv * es_of(CT)) == 0;
+  };
+  if constexpr (DT != RK_DTYPE_F32)
+    if (fits(8)) return launch_rope_cfg<DT, CT, 8>(x, cs, sn, out, rows, S, H, half, st);
+  if (fits(4)) return launch_rope_cfg<DT, CT, 4>(x, cs, sn, out, rows, S, H, half, st);
+  if (fits(2)) return launch_rope_cfg<DT, CT, 2>(x, cs, sn, out, rows, S, H, half, st);
+  return launch_rope_cfg<DT, CT, 1>(x, cs, sn, out, rows, S, H, half, st);
+}
+
+template <int DT>
+hipError_t launch_rope_x(const void *x, const void *cs, const void *sn, int ct, void *out,
+                         int rows, int S, int H, int half, hipStream_t st) {
+  switch (ct) {
+    case RK_DTYPE_F32: return launch_rope_t<DT, RK_DTYPE_F32>(x, cs, sn, out, rows, S, H, half, st);
+    case RK_DTYPE_F16: return launch_rope_t<DT, RK_DTYPE_F16>(x, cs, sn, out, rows, S, H, half, st);
+    case RK_DTYPE_BF16: return launch_rope_t<DT, RK_DTYPE_BF16>(x, cs, sn, out, rows, S, H, half, st);
+  }
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+hipError_t rk_launch_rope(const void *x, const void *cs, const void *sn, int cs_dtype, void *out,
+                          int rows, int S, int H, int half, int dtype, hipStream_t st) {
+  if (rows <= 0 || half <= 0) return hipSuccess;
+  switch (dtype) {
+    case RK_DTYPE_F32: return launch_rope_x<RK_DTYPE_F32>(x, cs, sn, cs_dtype, out, rows, S, H, half, st);
+    case RK_DTYPE_F16: return launch_rope_x<RK_DTYPE_F16>(x, cs, sn, cs_dtype, out, rows, S, H, half, st);
+    case RK_DTYPE_BF16: return launch_rope_x<RK_DTYPE_BF16>(x, cs, sn, cs_dtype, out, rows, S, H, half, st);
+  }
+  return hipErrorInvalidValue;
+}

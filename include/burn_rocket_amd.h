@@ -334,6 +334,38 @@ int rk_matmul_w8a8_glu_dev(rk_weight_id id, const int8_t *a, const float *a_scal
                            int64_t k, int glu, void *out, int out_f16, rk_stream stream);
 
 /* ======================================================================== *
+ * Normalisation and rotary embedding                                       *
+ * ======================================================================== */
+/* Weighted RMSNorm over the last dim: for each of `rows` rows of d values,
+ * out = x·inv·w with inv = 1/sqrt(Σx²/d + eps) (`rocket_rms_norm`,
+ * ext.rs:75-76, 611-612, rms_norm_impl ext.rs:1093-1107, row formula
+ * host.rs:40-56; eps is taken as f64 and used as f32 like the reference).
+ * Computed in f32; x and out of type dtype, w [d] of type w_dtype
+ * (RK_DTYPE_*), out rounded to nearest even. The sum of squares runs in a
+ * fixed parallel order (deterministic; not the reference's left-to-right
+ * order). Device buffers; out may be x. */
+int rk_rms_norm_dev(const void *x, const void *w, int w_dtype, void *out, int64_t rows, int64_t d,
+                    double eps, int dtype, rk_stream stream);
+/* Scale-free RMSNorm, out = x·inv (`rocket_rms_norm_noscale`, ext.rs:78-80,
+ * 613-615, rms_norm_noscale_impl ext.rs:1109-1123). As rk_rms_norm_dev. */
+int rk_rms_norm_noscale_dev(const void *x, void *out, int64_t rows, int64_t d, double eps,
+                            int dtype, rk_stream stream);
+/* Rotate-half RoPE of x [b, s, h, d] (row-major, d even) with cos/sin tables
+ * [s, d/2]: out[j] = x[j]·cos[j] − x[d/2+j]·sin[j], out[d/2+j] =
+ * x[d/2+j]·cos[j] + x[j]·sin[j], table row = the token's position in s
+ * (`rocket_rope`, ext.rs:82-84, 617-619, rope_impl ext.rs:1125-1152, row
+ * formula host.rs:58-75). Computed in f32 with no fused multiply-add; x and
+ * out of type dtype, the tables of type cs_dtype. Device buffers; out may
+ * be x. */
+int rk_rope_dev(const void *x, const void *cos, const void *sin, int cs_dtype, void *out,
+                int64_t b, int64_t s, int64_t h, int64_t d, int dtype, rk_stream stream);
+/* Host-buffer forms on f32 arrays (synchronous). */
+int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d, double eps);
+int rk_rms_norm_noscale(const float *x, float *out, int64_t rows, int64_t d, double eps);
+int rk_rope(const float *x, const float *cos, const float *sin, float *out, int64_t b, int64_t s,
+            int64_t h, int64_t d);
+
+/* ======================================================================== *
  * Device plumbing for callers without their own HIP runtime bindings       *
  * ======================================================================== */
 int rk_device_alloc(size_t bytes, void **ptr);

@@ -595,4 +595,38 @@ void orc_silu_mul(const float *gate, const float *up, float *out, int64_t n) {
   }
 }
 
+/* ------------------------------------------------------ RMSNorm, RoPE ---- */
+/* RMSNorm over rows of d values: ms = (Σ x·x, summed left to right) / d,
+ * inv = 1/sqrt(ms + eps), out = (x·inv)·w, or x·inv when w is NULL
+ * (rms_norm_row, host.rs:40-56; applied per row by rms_norm_impl /
+ * rms_norm_noscale_impl ext.rs:1093-1123). */
+void orc_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d, float eps) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *xr = x + r * d;
+    float *o = out + r * d;
+    float sum = 0.0f;
+    for (int64_t i = 0; i < d; ++i) sum += xr[i] * xr[i];
+    const float ms = sum / (float)d;
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (int64_t i = 0; i < d; ++i) o[i] = w ? xr[i] * inv * w[i] : xr[i] * inv;
+  }
+}
+
+/* Rotate-half RoPE of x [b, s, h, d] with cos/sin [s, d/2]; row r of d values
+ * uses table row (r / h) mod s (rope_impl ext.rs:1125-1152, rope_row
+ * host.rs:58-75). */
+void orc_rope(const float *x, const float *cs, const float *sn, float *out, int64_t b, int64_t s,
+              int64_t h, int64_t d) {
+  const int64_t half = d / 2, rows = b * s * h;
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *xr = x + r * d, *c = cs + ((r / h) % s) * half, *sv = sn + ((r / h) % s) * half;
+    float *o = out + r * d;
+    for (int64_t j = 0; j < half; ++j) {
+      const float x1 = xr[j], x2 = xr[half + j];
+      o[j] = x1 * c[j] - x2 * sv[j];
+      o[half + j] = x2 * c[j] + x1 * sv[j];
+    }
+  }
+}
+
 int orc_max_threads(void) { return omp_get_max_threads(); }

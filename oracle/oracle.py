@@ -39,6 +39,8 @@ _SIG = {
     "orc_gelu_tanh": (_f, [_f]),
     "orc_gelu_mul": (None, [_p, _p, _p, _i64]),
     "orc_silu_mul": (None, [_p, _p, _p, _i64]),
+    "orc_rms_norm": (None, [_p, _p, _p, _i64, _i64, _c.c_float]),
+    "orc_rope": (None, [_p, _p, _p, _p, _i64, _i64, _i64, _i64]),
     "orc_max_threads": (_i, []),
 }
 
@@ -290,6 +292,33 @@ def silu_mul(gate, up):
 def gelu_mul(gate, up):
     """gelu_tanh(gate)·up in f32 (host.rs:20-28)."""
     return _glue(lib().orc_gelu_mul, gate, up)
+
+
+def rms_norm(x, w, eps):
+    """RMSNorm over the last dim in f32 (host.rs:40-56); w None: scale-free."""
+    x = np.ascontiguousarray(x, np.float32)
+    d = x.shape[-1]
+    wp = None
+    if w is not None:
+        w = np.ascontiguousarray(w, np.float32)
+        assert w.shape == (d,)
+        wp = _ptr(w)
+    out = np.empty_like(x)
+    lib().orc_rms_norm(_ptr(x), wp, _ptr(out), _c.c_int64(x.size // d), _c.c_int64(d),
+                       _c.c_float(eps))
+    return out
+
+
+def rope(x, cos, sin):
+    """Rotate-half RoPE of x [B, S, H, D] with cos/sin [S, D/2] in f32 (host.rs:58-75)."""
+    x = np.ascontiguousarray(x, np.float32)
+    b, s, h, d = x.shape
+    cos = np.ascontiguousarray(cos, np.float32)
+    sin = np.ascontiguousarray(sin, np.float32)
+    assert d % 2 == 0 and cos.shape == (s, d // 2) and sin.shape == (s, d // 2)
+    out = np.empty_like(x)
+    lib().orc_rope(_ptr(x), _ptr(cos), _ptr(sin), _ptr(out), b, s, h, d)
+    return out
 
 
 def cosine(a, b):

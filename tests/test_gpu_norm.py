@@ -1,0 +1,263 @@
+"""GPU parity of RMSNorm (weighted and scale-free) and rotate-half RoPE
+(ext.rs:75-84, 611-619, 1093-1152; row formulas host.rs:40-75) against the
+oracle, through the C ABI.
+
+RoPE evaluates the reference's f32 expressions in the same order without FMA
+contraction, so every output type must match the oracle bit for bit.
+
+RMSNorm sums the squares in a fixed parallel order where the reference sums
+left to right. The two sums of d non-negative terms differ by at most
+(d + d/8 + 6)·2^-24 of the sum (each order's rounding bound, added); the
+square root halves that, and the division, square root, reciprocal and the
+two products add at most 4 units of 2^-24 of rounding. So f32 outputs obey
+|got - ref| <= (0.5·(1.125·d + 6) + 4)·2^-24·|ref|, fp16 / bf16 outputs that
+plus one unit in the last place of the 16-bit type, and at least 99 % of the
+16-bit outputs must equal the oracle's encoding. Integer-valued rows whose
+sum of squares is exact in f32 must match bit for bit in every type."""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+DTS = ("f32", "f16", "bf16")
+
+
+def note(msg):
+    print(f"[case] {msg}", file=sys.stderr, flush=True)
+
+
+def _code(rk, dt):
+    return {"f32": rk.DTYPE_F32, "f16": rk.DTYPE_F16, "bf16": rk.DTYPE_BF16}[dt]
+
+
+def _encode(orc, x32, dt):
+    if dt == "f32":
+        return np.ascontiguousarray(x32, np.float32)
+    if dt == "f16":
+        return np.ascontiguousarray(x32.astype(np.float16))
+    return orc.f32_to_bf16(x32)
+
+
+def _decode(orc, x, dt):
+    if dt == "bf16":
+        return orc.bf16_to_f32(x)
+    return x.astype(np.float32)
+
+
+def _ulp16(r, dt):
+    a = np.maximum(np.abs(r), np.float32(2.0 ** -14 if dt == "f16" else 2.0 ** -126))
+    mant = 10 if dt == "f16" else 7
+    return np.exp2(np.floor(np.log2(a)) - mant)
+
+
+class Dev:
+    """Device copies of host arrays, each placed `offset` bytes into its buffer."""
+
+    def __init__(self, rk, offset=0):
+        self.rk, self.lib, self.offset, self.bufs = rk, rk.lib(), offset, []
+
+    def put(self, a):
+        a = np.ascontiguousarray(a)
+        buf = self.rk.DeviceBuffer(a.nbytes + self.offset + 16)
+        self.bufs.append(buf)
+        p = buf.ptr + self.offset
+        if a.nbytes:
+            self.lib.rk_memcpy_htod(ctypes.c_void_p(p), a.ctypes.data_as(ctypes.c_void_p), a.nbytes)
+        return p
+
+    def get(self, p, like):
+        self.rk.synchronize()
+        out = np.empty_like(like)
+        if out.nbytes:
+            self.lib.rk_memcpy_dtoh(out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(p),
+                                    out.nbytes)
+        return out
+
+    def free(self):
+        for b in self.bufs:
+            b.free()
+
+
+def rms_dev(rk, orc, x32, w32, eps, dt, wdt=None, offset=0, inplace=False):
+    wdt = wdt or dt
+    x = _encode(orc, x32, dt)
+    d = x.shape[-1]
+    rows = x.size // d
+    dev = Dev(rk, offset)
+    try:
+        px = dev.put(x)
+        po = px if inplace else dev.put(np.zeros_like(x))
+        if w32 is None:
+            rc = rk.lib().rk_rms_norm_noscale_dev(px, po, rows, d, eps, _code(rk, dt), None)
+        else:
+            pw = dev.put(_encode(orc, w32, wdt))
+            rc = rk.lib().rk_rms_norm_dev(px, pw, _code(rk, wdt), po, rows, d, eps, _code(rk, dt), None)
+        assert rc == 0, rk.lib().rk_last_error()
+        return _decode(orc, dev.get(po, x), dt), x
+    finally:
+        dev.free()
+
+
+def rms_ref(orc, x, w32, eps, dt, wdt=None):
+    """The oracle on the values the device saw (inputs decoded from their type)."""
+    wdt = wdt or dt
+    w = None if w32 is None else _decode(orc, _encode(orc, w32, wdt), wdt)
+    return orc.rms_norm(_decode(orc, x, dt), w, eps)
+
+
+def check_rms(orc, got, ref, d, dt):
+    bound = (0.5 * (1.125 * d + 6) + 4) * 2.0 ** -24 * np.abs(ref)
+    if dt == "f32":
+        assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+        return
+    r16 = _decode(orc, _encode(orc, ref, dt), dt)
+    assert (np.abs(got - ref) <= bound + _ulp16(ref, dt)).all()
+    assert (got == r16).mean() >= 0.99, (got == r16).mean()
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("rows,d", [(1, 1), (3, 4), (37, 7), (129, 64), (100, 72), (64, 128),
+                                    (33, 1152), (17, 2048), (9, 4096), (5, 5000), (3, 8200),
+                                    (2, 20000)])
+def test_rms_norm_matches_oracle(rk, orc, dt, rows, d):
+    note(f"rms_norm {dt} rows={rows} d={d}")
+    r = np.random.default_rng(rows * 7919 + d)
+    x = (r.standard_normal((rows, d)) * 2).astype(np.float32)
+    w = r.standard_normal(d).astype(np.float32)
+    got, xe = rms_dev(rk, orc, x, w, 1e-6, dt)
+    check_rms(orc, got, rms_ref(orc, xe, w, 1e-6, dt), d, dt)
+    got, xe = rms_dev(rk, orc, x, None, 1e-5, dt)
+    check_rms(orc, got, rms_ref(orc, xe, None, 1e-5, dt), d, dt)
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("rows,d", [(5, 4), (70, 128), (19, 1152), (4, 4096), (2, 9000)])
+def test_rms_norm_exact_sums_are_bit_exact(rk, orc, dt, rows, d):
+    note(f"rms_norm exact {dt} rows={rows} d={d}")
+    r = np.random.default_rng(d + rows)
+    x = r.integers(-8, 9, (rows, d)).astype(np.float32)  # Σx² < 2^24: exact in any order
+    w = (r.integers(-64, 65, d) / 16).astype(np.float32)
+    for wv in (w, None):
+        got, xe = rms_dev(rk, orc, x, wv, 1e-6, dt)
+        ref = rms_ref(orc, xe, wv, 1e-6, dt)
+        assert (got == _decode(orc, _encode(orc, ref, dt), dt)).all()
+
+
+def test_rms_norm_mixed_weight_type_misaligned_and_in_place(rk, orc):
+    r = np.random.default_rng(5)
+    x = r.standard_normal((21, 136)).astype(np.float32)
+    w = r.standard_normal(136).astype(np.float32)
+    for dt, wdt, off, inplace in (("f16", "f32", 0, False), ("bf16", "f16", 0, True),
+                                  ("f16", "f16", 2, False), ("f32", "f32", 4, True),
+                                  ("f32", "bf16", 0, False)):
+        note(f"rms_norm x {dt} w {wdt} offset {off} in-place {inplace}")
+        got, xe = rms_dev(rk, orc, x, w, 1e-6, dt, wdt=wdt, offset=off, inplace=inplace)
+        check_rms(orc, got, rms_ref(orc, xe, w, 1e-6, dt, wdt), 136, dt)
+
+
+def test_rms_norm_zero_rows_and_errors(rk, orc):
+    note("rms_norm edge cases")
+    lib = rk.lib()
+    assert lib.rk_rms_norm_noscale_dev(None, None, 0, 16, 1e-6, rk.DTYPE_F32, None) == 0
+    assert lib.rk_rms_norm_noscale_dev(None, None, 4, 0, 1e-6, rk.DTYPE_F32, None) == rk.RK_E_SHAPE
+    assert lib.rk_rms_norm_dev(None, None, rk.DTYPE_F32, None, 4, 8, 1e-6, 7, None) == rk.RK_E_SHAPE
+    # all-zero rows: out = 0·(eps)^-½ = 0
+    got, _ = rms_dev(rk, orc, np.zeros((3, 64), np.float32), np.ones(64, np.float32), 1e-6, "f16")
+    assert (got == 0).all()
+
+
+def test_rms_norm_python_mirror_and_host_form(rk, orc):
+    note("rms_norm python mirror, host form")
+    r = np.random.default_rng(6)
+    x = r.standard_normal((2, 7, 96)).astype(np.float32)
+    w = r.standard_normal(96).astype(np.float32)
+    ref = orc.rms_norm(x, w, 1e-6)
+    check_rms(orc, rk.rms_norm(x, w, 1e-6), ref, 96, "f32")
+    check_rms(orc, rk.rms_norm_noscale(x, 1e-6), orc.rms_norm(x, None, 1e-6), 96, "f32")
+    y16 = rk.rms_norm(x.astype(np.float16), w.astype(np.float16), 1e-6)
+    assert y16.dtype == np.float16 and y16.shape == x.shape
+    out = np.empty_like(x)
+    lib = rk.lib()
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    assert lib.rk_rms_norm(p(x), p(w), p(out), 14, 96, 1e-6) == 0
+    check_rms(orc, out, ref, 96, "f32")
+    assert lib.rk_rms_norm_noscale(p(x), p(out), 14, 96, 1e-6) == 0
+    check_rms(orc, out, orc.rms_norm(x, None, 1e-6), 96, "f32")
+
+
+def rope_dev(rk, orc, x32, c32, s32, dt, cdt=None, offset=0, inplace=False):
+    cdt = cdt or dt
+    x = _encode(orc, x32, dt)
+    c, s = _encode(orc, c32, cdt), _encode(orc, s32, cdt)
+    b, sq, h, d = x.shape
+    dev = Dev(rk, offset)
+    try:
+        px, pc, ps = dev.put(x), dev.put(c), dev.put(s)
+        po = px if inplace else dev.put(np.zeros_like(x))
+        rc = rk.lib().rk_rope_dev(px, pc, ps, _code(rk, cdt), po, b, sq, h, d, _code(rk, dt), None)
+        assert rc == 0, rk.lib().rk_last_error()
+        got = _decode(orc, dev.get(po, x), dt)
+    finally:
+        dev.free()
+    ref = orc.rope(_decode(orc, x, dt), _decode(orc, c, cdt), _decode(orc, s, cdt))
+    return got, _decode(orc, _encode(orc, ref, dt), dt)
+
+
+def _tables(r, s, half):
+    ang = r.uniform(-6, 6, (s, half))
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("shape", [(1, 1, 1, 2), (2, 5, 3, 6), (1, 7, 4, 64), (1, 33, 16, 72),
+                                   (2, 40, 8, 128), (1, 3, 2, 4096), (1, 2, 1, 8200)])
+def test_rope_bit_exact(rk, orc, dt, shape):
+    note(f"rope {dt} shape={shape}")
+    r = np.random.default_rng(sum(shape))
+    x = r.standard_normal(shape).astype(np.float32)
+    c, s = _tables(r, shape[1], shape[3] // 2)
+    got, want = rope_dev(rk, orc, x, c, s, dt)
+    assert (got == want).all()
+
+
+@pytest.mark.parametrize("shape,name", [((1, 3633, 16, 128), "Qwen3 q"), ((1, 3633, 8, 128), "Qwen3 k"),
+                                        ((1, 2394, 16, 72), "vision")])
+def test_rope_full_size(rk, orc, shape, name):
+    note(f"rope full size {name} {shape}")
+    r = np.random.default_rng(77)
+    x = r.standard_normal(shape).astype(np.float32)
+    c, s = _tables(r, shape[1], shape[3] // 2)
+    got, want = rope_dev(rk, orc, x, c, s, "f16")
+    assert (got == want).all()
+
+
+def test_rope_table_types_misaligned_in_place(rk, orc):
+    r = np.random.default_rng(8)
+    x = r.standard_normal((2, 9, 3, 40)).astype(np.float32)
+    c, s = _tables(r, 9, 20)
+    for dt, cdt, off, inplace in (("f16", "f32", 0, False), ("bf16", "f16", 0, True),
+                                  ("f16", "f16", 2, False), ("f32", "bf16", 4, True),
+                                  ("f32", "f32", 8, False)):
+        note(f"rope x {dt} tables {cdt} offset {off} in-place {inplace}")
+        got, want = rope_dev(rk, orc, x, c, s, dt, cdt=cdt, offset=off, inplace=inplace)
+        assert (got == want).all()
+
+
+def test_rope_errors_python_mirror_and_host_form(rk, orc):
+    note("rope errors, python mirror, host form")
+    lib = rk.lib()
+    assert lib.rk_rope_dev(None, None, None, rk.DTYPE_F32, None, 1, 2, 3, 5, rk.DTYPE_F32, None) == rk.RK_E_SHAPE
+    assert lib.rk_rope_dev(None, None, None, rk.DTYPE_F32, None, 0, 2, 3, 4, rk.DTYPE_F32, None) == 0
+    r = np.random.default_rng(9)
+    x = r.standard_normal((1, 6, 2, 16)).astype(np.float32)
+    c, s = _tables(r, 6, 8)
+    want = orc.rope(x, c, s)
+    assert (rk.rope_apply(x, c, s) == want).all()
+    y = rk.rope_apply(x.astype(np.float16), c.astype(np.float16), s.astype(np.float16))
+    assert y.dtype == np.float16
+    out = np.empty_like(x)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    assert lib.rk_rope(p(x), p(c), p(s), p(out), 1, 6, 2, 16) == 0
+    assert (out == want).all()

@@ -423,3 +423,55 @@ def test_bf16_round_to_nearest_even(orc):
     got = orc.f32_to_bf16(x)
     assert (got == want).all()
     assert (orc.bf16_to_f32(got) == torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy()).all()
+
+
+def test_rms_norm_known_answer_and_invariants(orc):
+    # host.rs:146-162: x = [1, 2, 3, 4], w = [1, 0.5, 2, -1], eps = 1e-6
+    x = np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)
+    w = np.array([1.0, 0.5, 2.0, -1.0], np.float32)
+    inv = np.float32(1.0) / np.sqrt(np.float32(30.0 / 4.0) + np.float32(1e-6))
+    assert (np.abs(orc.rms_norm(x, w, 1e-6) - x * inv * w) < 1e-6).all()
+    assert (np.abs(orc.rms_norm(x, None, 1e-6) - x * inv) < 1e-6).all()
+    # against an f64 evaluation over random rows (a dropped eps, a sum over the
+    # wrong axis, or a weight applied per row instead of per column fail here)
+    r = _rng(31)
+    xs = r.standard_normal((37, 200)).astype(np.float32) * 3
+    ws = r.standard_normal(200).astype(np.float32)
+    x64 = xs.astype(np.float64)
+    want = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-5) * ws
+    assert np.abs(orc.rms_norm(xs, ws, 1e-5) - want).max() <= 1e-5 * np.abs(want).max()
+    # eps = 0 and w = 1: each row then has mean square 1
+    y = orc.rms_norm(xs, None, 0.0).astype(np.float64)
+    assert np.abs((y * y).mean(axis=1) - 1.0).max() < 1e-5
+    # eps dominates a tiny row: out ≈ x / sqrt(eps)
+    tiny = np.full((1, 8), 1e-6, np.float32)
+    assert np.allclose(orc.rms_norm(tiny, None, 1.0), tiny, rtol=1e-6)
+
+
+def test_rope_known_answer_and_rotation(orc):
+    # host.rs:164-177: half = 3 with these cos/sin, checked element by element
+    x = np.array([1.0, 2.0, 3.0, -1.0, 0.5, 4.0], np.float32).reshape(1, 1, 1, 6)
+    cos = np.array([[1.0, 0.5, -0.25]], np.float32)
+    sin = np.array([[0.0, 0.5, 0.75]], np.float32)
+    got = orc.rope(x, cos, sin).ravel()
+    x1, x2 = x.ravel()[:3], x.ravel()[3:]
+    assert (got[:3] == x1 * cos[0] - x2 * sin[0]).all()
+    assert (got[3:] == x2 * cos[0] + x1 * sin[0]).all()
+    # as a complex product (x1 + i·x2)·(cos + i·sin) per pair, the table row
+    # picked by the position axis of [B, S, H, D]
+    r = _rng(32)
+    b, s, h, d = 2, 5, 3, 16
+    xs = r.standard_normal((b, s, h, d)).astype(np.float32)
+    ang = r.uniform(-4, 4, (s, d // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    z = (xs[..., :d // 2] + 1j * xs[..., d // 2:].astype(np.float64)) * \
+        (cs[None, :, None, :] + 1j * sn[None, :, None, :].astype(np.float64))
+    want = np.concatenate([z.real, z.imag], axis=-1)
+    got = orc.rope(xs, cs, sn)
+    assert np.abs(got - want).max() < 1e-5
+    # a rotation keeps each pair's length; cos = 1, sin = 0 is the identity
+    n_in = xs[..., :d // 2] ** 2 + xs[..., d // 2:] ** 2
+    n_out = got[..., :d // 2] ** 2 + got[..., d // 2:] ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-5, atol=1e-6)
+    ident = orc.rope(xs, np.ones((s, d // 2), np.float32), np.zeros((s, d // 2), np.float32))
+    assert (ident == xs).all()
