@@ -137,11 +137,21 @@ __device__ __forceinline__ float dt_decode(dt_storage<DT> s) {
   else if constexpr (DT == RK_DTYPE_F16) return (float)__builtin_bit_cast(f16, s);
   else return __uint_as_float((uint32_t)s << 16);
 }
+// f32 → storage bits, rounded to nearest even. For fp16 the value is pinned in
+// a register first: left alone, the compiler folds a multiply that produced v
+// into the conversion (v_fma_mixlo_f16), which rounds the exact product once
+// to fp16 where an f32 result converted to fp16 is rounded twice; the two
+// differ next to fp16 rounding midpoints.
 template <int DT>
 __device__ __forceinline__ dt_storage<DT> dt_encode(float v) {
-  if constexpr (DT == RK_DTYPE_F32) return __float_as_uint(v);
-  else if constexpr (DT == RK_DTYPE_F16) return __builtin_bit_cast(uint16_t, (f16)v);
-  else return f32_to_bf16_rne(v);
+  if constexpr (DT == RK_DTYPE_F32) {
+    return __float_as_uint(v);
+  } else if constexpr (DT == RK_DTYPE_F16) {
+    asm("" : "+v"(v));
+    return __builtin_bit_cast(uint16_t, (f16)v);
+  } else {
+    return f32_to_bf16_rne(v);
+  }
 }
 template <int DT>
 __device__ __forceinline__ float dt_load(const void *p, int64_t i) {

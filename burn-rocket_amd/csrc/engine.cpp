@@ -824,7 +824,7 @@ int attn_check(int64_t n_q, int64_t n_kv, int n_head, int n_kv_heads, int head_d
 int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_q, int64_t n_kv,
              int64_t n_kv_pad, int n_head, int n_kv_heads, int head_dim, float scale, float softcap,
              int mode, int64_t window, int64_t q0, int64_t k0, bool head_major, hipStream_t st,
-             const char *op) {
+             const char *op, int64_t q_ts = 0, int64_t k_ts = 0, int64_t o_ts = 0) {
   AttnArgs a{};
   a.q = q;
   a.k = k;
@@ -838,11 +838,11 @@ int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_
     a.o_tok_stride = head_dim;
     a.o_head_stride = n_q * head_dim;
   } else {
-    a.q_tok_stride = (int64_t)n_head * head_dim;
+    a.q_tok_stride = q_ts ? q_ts : (int64_t)n_head * head_dim;
     a.q_head_stride = head_dim;
-    a.k_tok_stride = (int64_t)n_kv_heads * head_dim;
+    a.k_tok_stride = k_ts ? k_ts : (int64_t)n_kv_heads * head_dim;
     a.k_head_stride = head_dim;
-    a.o_tok_stride = (int64_t)n_head * head_dim;
+    a.o_tok_stride = o_ts ? o_ts : (int64_t)n_head * head_dim;
     a.o_head_stride = head_dim;
   }
   a.n_q = (int)n_q;
@@ -865,17 +865,18 @@ int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_
 int attn_dev_impl(const void *q, const void *k, const void *v, int64_t n_q, int64_t n_kv, int n_head,
                   int n_kv_heads, int head_dim, float scale, float softcap, int mode,
                   int64_t window, int64_t q0, int64_t k0, void *out, hipStream_t st,
-                  const char *op) {
+                  const char *op, int64_t q_ts = 0, int64_t k_ts = 0, int64_t v_ts = 0,
+                  int64_t o_ts = 0) {
   RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, op));
   const int dvp = rk_attn_dv_pad(head_dim);
   const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
   void *vt;
   RK_TRY(scratch("attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
-  HIP_TRY(rk_launch_v_transpose(v, (int64_t)n_kv_heads * head_dim, head_dim, (int)n_kv,
-                                (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
+  HIP_TRY(rk_launch_v_transpose(v, v_ts ? v_ts : (int64_t)n_kv_heads * head_dim, head_dim,
+                                (int)n_kv, (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
           op);
   return attn_run(q, k, vt, out, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale, softcap,
-                  mode, window, q0, k0, false, st, op);
+                  mode, window, q0, k0, false, st, op, q_ts, k_ts, o_ts);
 }
 }  // namespace
 
@@ -887,6 +888,28 @@ extern "C" int rk_attention_dev(const void *q, const void *k, const void *v, int
   RK_TRY(ensure("rk_attention_dev"));
   RK_TRY(attn_dev_impl(q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap, mask_mode,
                        window, q0, k0, out, pick(stream), "rk_attention_dev"));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_attention_strided_dev(const void *q, int64_t q_stride, const void *k,
+                                        int64_t k_stride, const void *v, int64_t v_stride,
+                                        int64_t n_q, int64_t n_kv, int n_head, int n_kv_heads,
+                                        int head_dim, float scale, float softcap, int mask_mode,
+                                        int64_t window, int64_t q0, int64_t k0, void *out,
+                                        int64_t out_stride, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_attention_strided_dev";
+  RK_TRY(ensure(name));
+  const int64_t qw = (int64_t)n_head * head_dim, kw = (int64_t)n_kv_heads * head_dim;
+  if (q_stride < qw || out_stride < qw || k_stride < kw || v_stride < kw)
+    return fail(RK_E_SHAPE, name, "a token stride is shorter than the token's heads");
+  if ((q_stride | k_stride | v_stride | out_stride) % 8 != 0 ||
+      (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) != 0)
+    return fail(RK_E_SHAPE, name, "token strides must be multiples of 8 values, buffers 16-byte aligned");
+  RK_TRY(attn_dev_impl(q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap, mask_mode,
+                       window, q0, k0, out, pick(stream), name, q_stride, k_stride, v_stride,
+                       out_stride));
   g_eng->calls++;
   return RK_OK;
 }
@@ -1493,6 +1516,35 @@ extern "C" int rk_rope_dev(const void *x, const void *cos, const void *sin, int 
   RK_TRY(rope_check(x, cos, sin, out, b, s, h, d, dtype, cs_dtype, name));
   HIP_TRY(rk_launch_rope(x, cos, sin, cs_dtype, out, (int)(b * s * h), (int)s, (int)h, (int)(d / 2),
                          dtype, pick(stream)), name);
+  return RK_OK;
+}
+extern "C" int rk_qk_norm_rope_dev(void *qkv, int64_t s, int64_t row_stride, int n_q_heads,
+                                   int n_kv_heads, int64_t head_dim, const void *q_norm_w,
+                                   const void *k_norm_w, double eps, const void *cos,
+                                   const void *sin, int cs_dtype, int dtype, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_qk_norm_rope_dev";
+  RK_TRY(ensure(name));
+  if (s < 0 || n_q_heads < 0 || n_kv_heads < 0 || s * (n_q_heads + n_kv_heads) > INT32_MAX)
+    return fail(RK_E_SHAPE, name, "negative shape, or s·(q + k heads) of 2^31 or more");
+  if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 4096)
+    return fail(RK_E_SHAPE, name, "the head dim must be even and in [2, 4096]");
+  if (row_stride < (int64_t)(n_q_heads + n_kv_heads) * head_dim)
+    return fail(RK_E_SHAPE, name, "row_stride is shorter than the q and k heads");
+  if (!float_dtype(dtype) || !float_dtype(cs_dtype)) return fail(RK_E_SHAPE, name, "unknown dtype");
+  if (cs_dtype != dtype && cs_dtype != RK_DTYPE_F32)
+    return fail(RK_E_UNSUPPORTED, name, "cos/sin must have the element type of qkv or be f32");
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(RK_E_SHAPE, name, "give both norm weights or neither");
+  if (s == 0 || n_q_heads + n_kv_heads == 0) return RK_OK;
+  if (!qkv || !cos || !sin) return fail(RK_E_SHAPE, name, "null buffer");
+  if (rk_qk_norm_rope_cv(qkv, row_stride, (int)head_dim, dtype, q_norm_w, k_norm_w, cos, sin,
+                         cs_dtype) == 0)
+    return fail(RK_E_UNSUPPORTED, name,
+                "head_dim / row_stride / buffer alignment allow no vector width (head_dim over 64 values per lane?)");
+  HIP_TRY(rk_launch_qk_norm_rope(qkv, row_stride, (int)s, n_q_heads, n_kv_heads, (int)head_dim,
+                                 q_norm_w, k_norm_w, (float)eps, cos, sin, cs_dtype, dtype,
+                                 pick(stream)), name);
   return RK_OK;
 }
 extern "C" int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d,

@@ -58,6 +58,16 @@ hipError_t rk_launch_rms_norm(const void *x, const void *w, int w_dtype, void *o
 hipError_t rk_launch_rope(const void *x, const void *cs, const void *sn, int cs_dtype, void *out,
                           int rows, int S, int H, int half, int dtype, hipStream_t st);
 
+// In-place per-head RMSNorm (weights wq / wk of type dtype, or both null) and
+// RoPE over the HQ q heads and HK k heads at the start of each of S token
+// rows of a q|k|v buffer. rk_qk_norm_rope_cv: the vector width the launch
+// will use, 0 when none fits (then the launch fails).
+int rk_qk_norm_rope_cv(const void *qkv, int64_t row_stride, int D, int dtype, const void *wq,
+                       const void *wk, const void *cs, const void *sn, int cs_dtype);
+hipError_t rk_launch_qk_norm_rope(void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
+                                  const void *wq, const void *wk, float eps, const void *cs,
+                                  const void *sn, int cs_dtype, int dtype, hipStream_t st);
+
 // Per-row symmetric quantizer (scale = max(amax/127, 1e-12), codes
 // round-half-away(x·(1/scale)) clamped to ±127), `group` values per scale.
 hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,

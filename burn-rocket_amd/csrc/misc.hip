@@ -298,7 +298,7 @@ __global__ __launch_bounds__(256) void glue_kernel(const void *__restrict__ a,
               u = __uint_as_float((uint32_t)ub << 16);
             }
             const float r = OP == 0 ? glue_silu_mul(g, u) : glue_gelu_mul(g, u);
-            const uint16_t rb = DT == RK_DTYPE_F16 ? __builtin_bit_cast(uint16_t, (f16)r) : f32_to_bf16_rne(r);
+            const uint16_t rb = dt_encode<DT>(r);
             w |= (uint32_t)rb << (16 * h);
           }
           ov[e] = w;

@@ -279,3 +279,143 @@ hipError_t rk_launch_rope(const void *x, const void *cs, const void *sn, int cs_
   }
   return hipErrorInvalidValue;
 }
+
+// ---------------------------------------------------------------------------
+// Attention prologue of a fused q|k|v projection (the Qwen3 layer,
+// src/qwen3_embedding/model.rs:355-376): per head, RMSNorm over the head dim
+// with the q or k norm weight, the result rounded to the element type (as the
+// reference's separate rms_norm op returns it), then rotate-half RoPE at the
+// token's position; in place, over the HQ q heads and the HK k heads that
+// follow them in each token's row. V is not touched.
+// A head row of D values is nch = D/CV chunks, one per lane, on LPR lanes
+// (a power of two >= nch); RoPE partners chunk c with chunk c ± D/(2·CV),
+// taken from the partner lane by a cross-lane read. The sum of squares
+// follows the order of rms_norm_kernel with the same CV and LPR.
+// ---------------------------------------------------------------------------
+template <int DT, int CT, int CV>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(void *__restrict__ qkv,
+                                                           int64_t row_stride, int S, int HQ,
+                                                           int HK, int D, int lpr,
+                                                           const void *__restrict__ wq,
+                                                           const void *__restrict__ wk, float eps,
+                                                           const void *__restrict__ cs,
+                                                           const void *__restrict__ sn) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int li = lane & (lpr - 1), grp0 = lane - li;
+  const int rpw = 64 / lpr;
+  const int nch = D / CV, hc = nch / 2, half = D / 2;
+  const int heads = HQ + HK;
+  const int64_t rows = (int64_t)S * heads;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const float fd = (float)D;
+  const int partner = grp0 + (li < hc ? li + hc : li - hc);
+  for (int64_t r0 = wave * rpw; r0 < rows; r0 += n_waves * rpw) {
+    const int64_t row = r0 + lane / lpr;
+    const bool live = row < rows && li < nch;
+    // rows < 2^31 (checked by the caller): 32-bit division
+    const int t = (int)((uint32_t)row / (uint32_t)heads);
+    const int hh = (int)row - t * heads;
+    const int64_t base = (int64_t)t * row_stride + (int64_t)hh * D + (int64_t)li * CV;
+    float f[CV];
+#pragma unroll
+    for (int e = 0; e < CV; ++e) f[e] = 0.f;
+    if (live) dt_load_vec<DT, CV>(qkv, base, f);
+    const void *w = hh < HQ ? wq : wk;
+    if (w) {
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < CV; ++e) acc += f[e] * f[e];
+      for (int off = lpr / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      const float inv = 1.0f / sqrtf(acc / fd + eps);
+      if (live) {
+        float wv[CV];
+        dt_load_vec<DT, CV>(w, (int64_t)li * CV, wv);
+#pragma unroll
+        for (int e = 0; e < CV; ++e) f[e] = dt_decode<DT>(dt_encode<DT>(f[e] * inv * wv[e]));
+      }
+    }
+    float p[CV];
+#pragma unroll
+    for (int e = 0; e < CV; ++e) p[e] = __shfl(f[e], partner, 64);
+    if (live) {
+      const bool lo = li < hc;
+      const int j = (lo ? li : li - hc) * CV;
+      float c[CV], s[CV], o[CV];
+      dt_load_vec<CT, CV>(cs, (int64_t)t * half + j, c);
+      dt_load_vec<CT, CV>(sn, (int64_t)t * half + j, s);
+#pragma unroll
+      for (int e = 0; e < CV; ++e)
+        o[e] = lo ? f[e] * c[e] - p[e] * s[e] : f[e] * c[e] + p[e] * s[e];
+      dt_store_vec<DT, CV>(qkv, base, o);
+    }
+  }
+}
+
+namespace {
+template <int DT, int CT, int CV>
+hipError_t launch_qknr_cfg(void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
+                           const void *wq, const void *wk, float eps, const void *cs,
+                           const void *sn, hipStream_t st) {
+  const int nch = D / CV;
+  int lpr = 1;
+  while (lpr < nch) lpr <<= 1;
+  const int64_t rows = (int64_t)S * (HQ + HK), rows_per_block = 4 * (64 / lpr);
+  const unsigned blocks =
+      (unsigned)std::min<int64_t>((rows + rows_per_block - 1) / rows_per_block, 16384);
+  hipLaunchKernelGGL((qk_norm_rope_kernel<DT, CT, CV>), dim3(blocks), dim3(256), 0, st, qkv,
+                     row_stride, S, HQ, HK, D, lpr, wq, wk, eps, cs, sn);
+  return hipGetLastError();
+}
+
+template <int DT, int CT>
+hipError_t launch_qknr_t(int cv, void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
+                         const void *wq, const void *wk, float eps, const void *cs,
+                         const void *sn, hipStream_t st) {
+  switch (cv) {
+    case 8:
+      if constexpr (DT != RK_DTYPE_F32)
+        return launch_qknr_cfg<DT, CT, 8>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+      break;
+    case 4: return launch_qknr_cfg<DT, CT, 4>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+    case 2: return launch_qknr_cfg<DT, CT, 2>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+    case 1: return launch_qknr_cfg<DT, CT, 1>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+  }
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+int rk_qk_norm_rope_cv(const void *qkv, int64_t row_stride, int D, int dtype, const void *wq,
+                       const void *wk, const void *cs, const void *sn, int cs_dtype) {
+  const int es = es_of(dtype), ces = es_of(cs_dtype);
+  for (int cv = 16 / es; cv >= 1; cv >>= 1) {
+    const bool ok = (D / 2) % cv == 0 && row_stride % cv == 0 && D / cv <= 64 &&
+                    (uintptr_t)qkv % (cv * es) == 0 && (uintptr_t)wq % (cv * es) == 0 &&
+                    (uintptr_t)wk % (cv * es) == 0 &&
+                    (((uintptr_t)cs | (uintptr_t)sn) % (cv * ces)) == 0;
+    if (ok) return cv;
+  }
+  return 0;
+}
+
+hipError_t rk_launch_qk_norm_rope(void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
+                                  const void *wq, const void *wk, float eps, const void *cs,
+                                  const void *sn, int cs_dtype, int dtype, hipStream_t st) {
+  if (S <= 0 || HQ + HK <= 0) return hipSuccess;
+  const int cv = rk_qk_norm_rope_cv(qkv, row_stride, D, dtype, wq, wk, cs, sn, cs_dtype);
+  if (cv == 0) return hipErrorInvalidValue;
+  const bool cs_f32 = cs_dtype == RK_DTYPE_F32;
+  if (cs_dtype != dtype && !cs_f32) return hipErrorInvalidValue;
+  switch (dtype) {
+    case RK_DTYPE_F32:
+      return launch_qknr_t<RK_DTYPE_F32, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+    case RK_DTYPE_F16:
+      return cs_f32 ? launch_qknr_t<RK_DTYPE_F16, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st)
+                    : launch_qknr_t<RK_DTYPE_F16, RK_DTYPE_F16>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+    case RK_DTYPE_BF16:
+      return cs_f32 ? launch_qknr_t<RK_DTYPE_BF16, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st)
+                    : launch_qknr_t<RK_DTYPE_BF16, RK_DTYPE_BF16>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+  }
+  return hipErrorInvalidValue;
+}

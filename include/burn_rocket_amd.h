@@ -236,6 +236,16 @@ int rk_attention_dev(const void *q, const void *k, const void *v, int64_t n_q,
                      int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
                      float scale, float softcap, int mask_mode, int64_t window,
                      int64_t q0, int64_t k0, void *out, rk_stream stream);
+/* rk_attention_dev with token strides (in values; multiples of 8, buffers
+ * 16-byte aligned): q, k, v and out may be column ranges of wider rows, e.g.
+ * the q, k and v parts of one fused q|k|v projection output, read where they
+ * lie (the reference slices them into separate tensors first,
+ * src/qwen3_embedding/model.rs:355-368). */
+int rk_attention_strided_dev(const void *q, int64_t q_stride, const void *k, int64_t k_stride,
+                             const void *v, int64_t v_stride, int64_t n_q, int64_t n_kv,
+                             int n_head, int n_kv_heads, int head_dim, float scale,
+                             float softcap, int mask_mode, int64_t window, int64_t q0,
+                             int64_t k0, void *out, int64_t out_stride, rk_stream stream);
 
 /* Head-major fp16 host buffers, the `RocketFaCtx::flash_attn` layout
  * (lib.rs:294-323; attn/mod.rs:1541-1600): q [n_head][n_q][head_dim],
@@ -359,6 +369,23 @@ int rk_rms_norm_noscale_dev(const void *x, void *out, int64_t rows, int64_t d, d
  * be x. */
 int rk_rope_dev(const void *x, const void *cos, const void *sin, int cs_dtype, void *out,
                 int64_t b, int64_t s, int64_t h, int64_t d, int dtype, rk_stream stream);
+/* The attention prologue of a fused q|k|v projection, in place: for each of
+ * s tokens (rows `row_stride` values apart) the n_q_heads q heads and the
+ * n_kv_heads k heads at the start of the row get RMSNorm over head_dim with
+ * q_norm_w / k_norm_w [head_dim] (eps as in rk_rms_norm_dev; the result
+ * rounded to dtype), then rotate-half RoPE with cos/sin row t for token t.
+ * The values after the k heads (V) are not touched. It is the composite the
+ * Qwen3 layer runs on the fused projection (src/qwen3_embedding/model.rs:
+ * 355-376: `q_norm`/`k_norm` through `burn_rocket::rms_norm` ext.rs:2112-2119,
+ * then `burn_rocket::rope_apply` ext.rs:2130-2137 with `cos_rows(0, s)`), in
+ * one pass. The norm weights have type dtype, or are both NULL (RoPE only);
+ * cos/sin [s, head_dim/2] have type dtype or f32. RK_E_UNSUPPORTED when
+ * head_dim / row_stride / alignment leave no vector width of at most 64
+ * values per lane (fp16: head_dim <= 512 with head_dim/2 % 8 == 0). */
+int rk_qk_norm_rope_dev(void *qkv, int64_t s, int64_t row_stride, int n_q_heads, int n_kv_heads,
+                        int64_t head_dim, const void *q_norm_w, const void *k_norm_w, double eps,
+                        const void *cos, const void *sin, int cs_dtype, int dtype,
+                        rk_stream stream);
 /* Host-buffer forms on f32 arrays (synchronous). */
 int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d, double eps);
 int rk_rms_norm_noscale(const float *x, float *out, int64_t rows, int64_t d, double eps);

@@ -261,3 +261,179 @@ def test_rope_errors_python_mirror_and_host_form(rk, orc):
     p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
     assert lib.rk_rope(p(x), p(c), p(s), p(out), 1, 6, 2, 16) == 0
     assert (out == want).all()
+
+
+# ---- fused attention prologue on a q|k|v buffer, strided attention ----------
+def _qkv_case(r, s, hq, hk, d, pad):
+    stride = (hq + 2 * hk) * d + pad
+    qkv = r.standard_normal((s, stride)).astype(np.float32)
+    wq = (1 + 0.3 * r.standard_normal(d)).astype(np.float32)
+    wk = (1 + 0.3 * r.standard_normal(d)).astype(np.float32)
+    c, sn = _tables(r, s, d // 2)
+    return qkv, stride, wq, wk, c, sn
+
+
+def qknr_dev(rk, orc, qkv32, stride, hq, hk, d, wq, wk, c32, s32, dt, cdt=None, eps=1e-6):
+    cdt = cdt or dt
+    x = _encode(orc, qkv32, dt)
+    dev = Dev(rk)
+    try:
+        px = dev.put(x)
+        pq = dev.put(_encode(orc, wq, dt)) if wq is not None else None
+        pk = dev.put(_encode(orc, wk, dt)) if wk is not None else None
+        pc, ps = dev.put(_encode(orc, c32, cdt)), dev.put(_encode(orc, s32, cdt))
+        rc = rk.lib().rk_qk_norm_rope_dev(px, x.shape[0], stride, hq, hk, d, pq, pk, eps, pc, ps,
+                                          _code(rk, cdt), _code(rk, dt), None)
+        assert rc == 0, rk.lib().rk_last_error()
+        return _decode(orc, dev.get(px, x), dt), x
+    finally:
+        dev.free()
+
+
+def qknr_ref(orc, x, hq, hk, d, wq, wk, c32, s32, dt, cdt=None, eps=1e-6):
+    """The reference's composite on the decoded inputs: rms_norm (rounded to the
+    element type, as the separate op returns it), then rope, per q and k part."""
+    cdt = cdt or dt
+    xs = _decode(orc, x, dt)
+    s = xs.shape[0]
+    cs = _decode(orc, _encode(orc, c32, cdt), cdt)
+    sn = _decode(orc, _encode(orc, s32, cdt), cdt)
+    out = xs.copy()
+    for c0, nh, w in ((0, hq, wq), (hq * d, hk, wk)):
+        part = xs[:, c0:c0 + nh * d].reshape(1, s, nh, d)
+        if w is not None:
+            wv = _decode(orc, _encode(orc, w, dt), dt)
+            part = _decode(orc, _encode(orc, orc.rms_norm(part, wv, eps), dt), dt)
+        rot = _decode(orc, _encode(orc, orc.rope(part, cs, sn), dt), dt)
+        out[:, c0:c0 + nh * d] = rot.reshape(s, nh * d)
+    return out
+
+
+@pytest.mark.parametrize("dt,d", [("f16", 128), ("bf16", 128), ("f32", 128), ("f16", 72),
+                                  ("f16", 256), ("f32", 64), ("bf16", 8)])
+def test_qk_norm_rope_matches_composite(rk, orc, dt, d):
+    hq, hk, s = 4, 2, 77
+    note(f"qk_norm_rope {dt} d={d} S={s} {hq}/{hk}")
+    r = np.random.default_rng(d * 3 + len(dt))
+    qkv, stride, wq, wk, c, sn = _qkv_case(r, s, hq, hk, d, 8)
+    got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, wq, wk, c, sn, dt)
+    want = qknr_ref(orc, x, hq, hk, d, wq, wk, c, sn, dt)
+    qk = (hq + hk) * d
+    xs = _decode(orc, x, dt)
+    assert (got[:, qk:] == xs[:, qk:]).all(), "V columns and row padding must not change"
+    g, w = got[:, :qk].reshape(-1, d), want[:, :qk].reshape(-1, d)
+    # the norm's f32 result may round to a neighbouring 16-bit value (sum order);
+    # RoPE then moves it by at most (|cos| + |sin|) <= 1.5 of that unit
+    # (a pair's length is kept, so the row's largest input is at most √2 times
+    # its largest output); f32 carries the norm's summation-order bound instead
+    wmax = np.abs(w).max(axis=1, keepdims=True)
+    if dt == "f32":
+        unit = (0.5 * (1.125 * d + 6) + 4) * 2.0 ** -24 * wmax
+    else:
+        unit = _ulp16(wmax, dt)
+        assert (g == w).mean() >= 0.99, (g == w).mean()
+    assert (np.abs(g - w) <= 4 * unit).all(), np.abs(g - w).max()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_qk_norm_rope_bit_exact_cases(rk, orc, dt):
+    hq, hk, s, d = 3, 1, 40, 128
+    r = np.random.default_rng(41)
+    qkv, stride, wq, wk, c, sn = _qkv_case(r, s, hq, hk, d, 0)
+    # integer rows: the sum of squares is exact in any order
+    qkv = r.integers(-8, 9, qkv.shape).astype(np.float32)
+    wq, wk = (r.integers(-32, 33, d) / 16).astype(np.float32), (r.integers(-32, 33, d) / 16).astype(np.float32)
+    note(f"qk_norm_rope exact {dt}")
+    got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, wq, wk, c, sn, dt)
+    assert (got == qknr_ref(orc, x, hq, hk, d, wq, wk, c, sn, dt)).all()
+    # no norm weights: RoPE alone, bit-exact; f32 tables with 16-bit values
+    note(f"qk_norm_rope rope-only {dt}, f32 tables")
+    qkv = r.standard_normal(qkv.shape).astype(np.float32)
+    got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, None, None, c, sn, dt, cdt="f32")
+    assert (got == qknr_ref(orc, x, hq, hk, d, None, None, c, sn, dt, cdt="f32")).all()
+    # against the separate device ops (same vector width, so the same sum order)
+    note(f"qk_norm_rope vs rk_rms_norm_dev + rk_rope_dev {dt}")
+    got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, wq, wk, c, sn, dt)
+    xs = _decode(orc, x, dt)
+    for c0, nh, w in ((0, hq, wq), (hq * d, hk, wk)):
+        part = xs[:, c0:c0 + nh * d].reshape(1, s, nh, d)
+        normed, _ = rms_dev(rk, orc, part, w, 1e-6, dt)
+        rot, _ = rope_dev(rk, orc, normed, c, sn, dt)
+        assert (got[:, c0:c0 + nh * d] == rot.reshape(s, nh * d)).all()
+
+
+def test_qk_norm_rope_errors(rk):
+    note("qk_norm_rope errors")
+    lib = rk.lib()
+    f16 = rk.DTYPE_F16
+    buf = rk.DeviceBuffer(4096)
+    p = buf.ptr
+    assert lib.rk_qk_norm_rope_dev(p, 1, 64, 1, 1, 6, None, None, 1e-6, p, p, f16, f16, None) == 0
+    assert lib.rk_qk_norm_rope_dev(p, 1, 64, 1, 1, 7, None, None, 1e-6, p, p, f16, f16, None) == rk.RK_E_SHAPE
+    assert lib.rk_qk_norm_rope_dev(p, 1, 8, 1, 1, 8, None, None, 1e-6, p, p, f16, f16, None) == rk.RK_E_SHAPE
+    assert lib.rk_qk_norm_rope_dev(p, 1, 64, 1, 1, 8, p, None, 1e-6, p, p, f16, f16, None) == rk.RK_E_SHAPE
+    assert lib.rk_qk_norm_rope_dev(p, 1, 64, 1, 1, 8, None, None, 1e-6, p, p, rk.DTYPE_BF16, f16, None) == rk.RK_E_UNSUPPORTED
+    # 1024 fp16 values per head: more than 64 lanes × 8 values
+    assert lib.rk_qk_norm_rope_dev(p, 0, 2048, 1, 1, 1024, None, None, 1e-6, p, p, f16, f16, None) == 0
+    rk.synchronize()
+    buf.free()
+
+
+def _attn_strided(rk, qkv, hq, hk, d, mode, out_stride, n):
+    """Attention on one fp16 [n, stride] q|k|v buffer, read in place."""
+    lib = rk.lib()
+    stride = qkv.shape[1]
+    dev = Dev(rk)
+    try:
+        p = dev.put(qkv)
+        out = np.zeros((n, out_stride), np.float16)
+        po = dev.put(out)
+        rc = lib.rk_attention_strided_dev(p, stride, p + hq * d * 2, stride, p + (hq + hk) * d * 2,
+                                          stride, n, n, hq, hk, d, d ** -0.5, 0.0, mode, -1, 0, 0,
+                                          po, out_stride, None)
+        assert rc == 0, lib.rk_last_error()
+        return dev.get(po, out)
+    finally:
+        dev.free()
+
+
+def _attn_packed(rk, q, k, v, hq, hk, d, mode, n):
+    lib = rk.lib()
+    dev = Dev(rk)
+    try:
+        pq, pk, pv = dev.put(q), dev.put(k), dev.put(v)
+        out = np.zeros((n, hq * d), np.float16)
+        po = dev.put(out)
+        rc = lib.rk_attention_dev(pq, pk, pv, n, n, hq, hk, d, d ** -0.5, 0.0, mode, -1, 0, 0, po, None)
+        assert rc == 0, lib.rk_last_error()
+        return dev.get(po, out)
+    finally:
+        dev.free()
+
+
+@pytest.mark.parametrize("d,hq,hk,mode", [(128, 4, 2, 1), (72, 3, 3, 0), (64, 8, 1, 1)])
+def test_attention_strided_on_a_qkv_buffer(rk, d, hq, hk, mode):
+    n = 301
+    note(f"strided attention d={d} {hq}/{hk} mode={mode} n={n}")
+    r = np.random.default_rng(d + hq)
+    stride = (hq + 2 * hk) * d + 16
+    qkv = r.standard_normal((n, stride)).astype(np.float16)
+    q = np.ascontiguousarray(qkv[:, :hq * d])
+    k = np.ascontiguousarray(qkv[:, hq * d:(hq + hk) * d])
+    v = np.ascontiguousarray(qkv[:, (hq + hk) * d:(hq + 2 * hk) * d])
+    want = _attn_packed(rk, q, k, v, hq, hk, d, mode, n)
+    out_stride = hq * d + 24
+    got = _attn_strided(rk, qkv, hq, hk, d, mode, out_stride, n)
+    assert (got[:, :hq * d].view(np.uint16) == want.view(np.uint16)).all()
+    assert (got[:, hq * d:] == 0).all()
+
+
+def test_attention_strided_errors(rk):
+    note("strided attention errors")
+    lib = rk.lib()
+    buf = rk.DeviceBuffer(1 << 16)
+    p = buf.ptr
+    # stride shorter than the heads; stride not a multiple of 8
+    assert lib.rk_attention_strided_dev(p, 64, p, 64, p, 64, 4, 4, 2, 1, 64, 0.1, 0.0, 0, -1, 0, 0, p, 128, None) == rk.RK_E_SHAPE
+    assert lib.rk_attention_strided_dev(p, 132, p, 68, p, 68, 4, 4, 2, 1, 64, 0.1, 0.0, 0, -1, 0, 0, p, 128, None) == rk.RK_E_SHAPE
+    buf.free()
