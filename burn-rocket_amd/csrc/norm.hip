@@ -58,12 +58,23 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void *__restrict__ 
     const int64_t base = row * (int64_t)d;
     float acc = 0.f;
     float v[NC > 0 ? NC : 1][CV];
+    // rows of at most two chunks per lane load their weight chunks with x,
+    // so the wave waits for memory once
+    constexpr bool PRE = WT >= 0 && NC > 0 && NC <= 2;
+    float wpre[PRE ? NC : 1][CV];
     if constexpr (NC > 0) {
 #pragma unroll
       for (int i = 0; i < NC; ++i) {
         const int ch = li + LPR * i;
         if (live && ch < nch) {
           dt_load_vec<DT, CV>(x, base + (int64_t)ch * CV, v[i]);
+          if constexpr (PRE) dt_load_vec<WT, CV>(w, (int64_t)ch * CV, wpre[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int ch = li + LPR * i;
+        if (live && ch < nch) {
 #pragma unroll
           for (int e = 0; e < CV; ++e) acc += v[i][e] * v[i][e];
         }
@@ -79,11 +90,16 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void *__restrict__ 
 #pragma unroll
     for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
     const float inv = 1.0f / sqrtf(acc / fd + eps);
-    auto emit = [&](int ch, float *f) {
+    auto emit = [&](int ch, float *f, const float *wp) {
       float o[CV];
       if constexpr (WT >= 0) {
         float wv[CV];
-        dt_load_vec<WT, CV>(w, (int64_t)ch * CV, wv);
+        if (wp) {
+#pragma unroll
+          for (int e = 0; e < CV; ++e) wv[e] = wp[e];
+        } else {
+          dt_load_vec<WT, CV>(w, (int64_t)ch * CV, wv);
+        }
 #pragma unroll
         for (int e = 0; e < CV; ++e) o[e] = f[e] * inv * wv[e];
       } else {
@@ -96,13 +112,13 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void *__restrict__ 
 #pragma unroll
       for (int i = 0; i < NC; ++i) {
         const int ch = li + LPR * i;
-        if (live && ch < nch) emit(ch, v[i]);
+        if (live && ch < nch) emit(ch, v[i], PRE ? wpre[PRE ? i : 0] : nullptr);
       }
     } else {
       if (live)
         for (int ch = li; ch < nch; ch += LPR) {
           dt_load_vec<DT, CV>(x, base + (int64_t)ch * CV, v[0]);
-          emit(ch, v[0]);
+          emit(ch, v[0], nullptr);
         }
     }
   }
@@ -318,33 +334,34 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(void *__restrict__ qk
     const int t = (int)((uint32_t)row / (uint32_t)heads);
     const int hh = (int)row - t * heads;
     const int64_t base = (int64_t)t * row_stride + (int64_t)hh * D + (int64_t)li * CV;
-    float f[CV];
-#pragma unroll
-    for (int e = 0; e < CV; ++e) f[e] = 0.f;
-    if (live) dt_load_vec<DT, CV>(qkv, base, f);
+    // every load of the row is issued up front: x, the norm weight and the
+    // table entries, so a wave waits for memory once
     const void *w = hh < HQ ? wq : wk;
+    const bool lo = li < hc;
+    const int j = (lo ? li : li - hc) * CV;
+    float f[CV], wv[CV], c[CV], s[CV];
+#pragma unroll
+    for (int e = 0; e < CV; ++e) f[e] = wv[e] = c[e] = s[e] = 0.f;
+    if (live) {
+      dt_load_vec<DT, CV>(qkv, base, f);
+      if (w) dt_load_vec<DT, CV>(w, (int64_t)li * CV, wv);
+      dt_load_vec<CT, CV>(cs, (int64_t)t * half + j, c);
+      dt_load_vec<CT, CV>(sn, (int64_t)t * half + j, s);
+    }
     if (w) {
       float acc = 0.f;
 #pragma unroll
       for (int e = 0; e < CV; ++e) acc += f[e] * f[e];
       for (int off = lpr / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
       const float inv = 1.0f / sqrtf(acc / fd + eps);
-      if (live) {
-        float wv[CV];
-        dt_load_vec<DT, CV>(w, (int64_t)li * CV, wv);
 #pragma unroll
-        for (int e = 0; e < CV; ++e) f[e] = dt_decode<DT>(dt_encode<DT>(f[e] * inv * wv[e]));
-      }
+      for (int e = 0; e < CV; ++e) f[e] = dt_decode<DT>(dt_encode<DT>(f[e] * inv * wv[e]));
     }
     float p[CV];
 #pragma unroll
     for (int e = 0; e < CV; ++e) p[e] = __shfl(f[e], partner, 64);
     if (live) {
-      const bool lo = li < hc;
-      const int j = (lo ? li : li - hc) * CV;
-      float c[CV], s[CV], o[CV];
-      dt_load_vec<CT, CV>(cs, (int64_t)t * half + j, c);
-      dt_load_vec<CT, CV>(sn, (int64_t)t * half + j, s);
+      float o[CV];
 #pragma unroll
       for (int e = 0; e < CV; ++e)
         o[e] = lo ? f[e] * c[e] - p[e] * s[e] : f[e] * c[e] + p[e] * s[e];
