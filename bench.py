@@ -327,6 +327,56 @@ def extra_moe(iters):
             "attention": att}
 
 
+def extra_glue(iters):
+    """The HBM-bound ops around the GEMMs at the Qwen3-0.6B layer shape (S=3633, hidden 1024,
+    MLP 3072, 16 q / 8 kv heads of 128): bytes are one read of each input and one write of
+    each output."""
+    c, g = synth.W8A8, synth.GQA_CAUSAL
+    m, hid, inter = c["m"], c["hidden"], c["inter"]
+    hq, hk, d = g["n_head"], g["n_kv"], g["d"]
+    lib = rk.lib()
+    r = np.random.default_rng(7)
+    out = {}
+
+    def rec(name, fn, nbytes):
+        ms = time_launches(fn, iters)
+        out[name] = {"ms": ms, "gbps": nbytes / ms / 1e6, "frac_hbm": nbytes / ms / 1e6 / PEAK_HBM}
+
+    x16 = dev(r.standard_normal((m, hid)).astype(np.float16).view(np.uint16))
+    w16 = dev((1 + 0.1 * r.standard_normal(hid)).astype(np.float16).view(np.uint16))
+    y16 = rk.DeviceBuffer(m * hid * 2)
+    rec("rms_norm_f16_3633x1024", lambda: call(lib.rk_rms_norm_dev(
+        x16.ptr, w16.ptr, rk.DTYPE_F16, y16.ptr, m, hid, 1e-6, rk.DTYPE_F16, None), "rms"), 2 * m * hid * 2)
+    width = (hq + 2 * hk) * d
+    qkv = dev(r.standard_normal((m, width)).astype(np.float16).view(np.uint16))
+    wq = dev((1 + 0.1 * r.standard_normal(d)).astype(np.float16).view(np.uint16))
+    wk = dev((1 + 0.1 * r.standard_normal(d)).astype(np.float16).view(np.uint16))
+    ang = np.arange(m)[:, None] * (10000.0 ** (-np.arange(d // 2) / (d // 2)))[None, :]
+    cs = dev(np.cos(ang).astype(np.float16).view(np.uint16))
+    sn = dev(np.sin(ang).astype(np.float16).view(np.uint16))
+    rec("qk_norm_rope_f16_3633x4096", lambda: call(lib.rk_qk_norm_rope_dev(
+        qkv.ptr, m, width, hq, hk, d, wq.ptr, wk.ptr, 1e-6, cs.ptr, sn.ptr, rk.DTYPE_F16, rk.DTYPE_F16, None),
+        "qknr"), 2 * m * (hq + hk) * d * 2)
+    n = m * inter
+    a32, b32 = dev(r.standard_normal(n).astype(np.float32)), dev(r.standard_normal(n).astype(np.float32))
+    o32 = rk.DeviceBuffer(n * 4)
+    rec("silu_mul_f32_3633x3072", lambda: call(lib.rk_silu_mul_dev(
+        a32.ptr, b32.ptr, o32.ptr, n, rk.DTYPE_F32, None), "silu"), 3 * n * 4)
+    # per-token int8 activations of normal data, as in the headline workload
+    xf = dev(synth.normal_f32(13, (m, hid)))
+    xq, xs = rk.DeviceBuffer(m * hid), rk.DeviceBuffer(m * 4)
+    call(lib.rk_quantize_rows_dev(xf.ptr, m, hid, hid, xq.ptr, xs.ptr, None), "quantize")
+    gate = synth.normal_f32(11, (inter, hid), 0.02)
+    up = synth.normal_f32(12, (inter, hid), 0.02)
+    wid = rk.pack_q8_0_glu_f32(gate, up)
+    ms = time_launches(lambda: call(lib.rk_matmul_w8a8_glu_dev(
+        int(wid), xq.ptr, xs.ptr, m, hid, 1, o32.ptr, 0, None), "glu"), iters)
+    ops = 2.0 * m * hid * 2 * inter
+    out["w8a8_gate_up_silu_3633x1024x2x3072"] = {"ms": ms, "tops": ops / ms / 1e9,
+                                                 "frac_int8_peak": ops / ms / 1e9 / PEAK_INT8}
+    return out
+
+
 # --------------------------------------------------------- CPU baseline ----
 def cpu_baseline(layers, budget_s):
     """The reference's W8A8 formula (emu_matmul_gw) on the host cores."""
@@ -426,7 +476,8 @@ def main():
                             synth.GQA_CAUSAL["s"], synth.GQA_CAUSAL["n_head"], synth.GQA_CAUSAL["n_kv"],
                             synth.GQA_CAUSAL["d"], True, synth.SEEDS["gqa"], 50)),
                         ("vision_layer_2394", lambda: extra_vision(50)),
-                        ("moe_30b_a3b_1024", lambda: extra_moe(20))):
+                        ("moe_30b_a3b_1024", lambda: extra_moe(20)),
+                        ("glue_qwen3_3633", lambda: extra_glue(50))):
             log(f"extra {key}")
             extras[key] = fn()
 
