@@ -198,3 +198,42 @@ __device__ __forceinline__ void dt_store_vec(void *p, int64_t i, const float *f)
     *(SV *)((S *)p + i) = v;
   }
 }
+
+// N elements kept as their storage bits, packed in dwords (loaded now, decoded
+// later): lets a kernel issue the loads of several rows before it computes on
+// any of them without one register per 16-bit value.
+template <int DT, int N>
+struct dt_raw {
+  static constexpr int BYTES = N * (DT == RK_DTYPE_F32 ? 4 : 2);
+  static constexpr int WORDS = BYTES < 4 ? 1 : BYTES / 4;
+  uint32_t w[WORDS];
+};
+template <int DT, int N>
+__device__ __forceinline__ void dt_load_raw(const void *p, int64_t i, dt_raw<DT, N> &r) {
+  constexpr int ES = DT == RK_DTYPE_F32 ? 4 : 2;
+  constexpr int W = dt_raw<DT, N>::WORDS;
+  const uint8_t *a = (const uint8_t *)p + i * ES;
+  if constexpr (dt_raw<DT, N>::BYTES < 4) {
+    r.w[0] = *(const uint16_t *)a;
+  } else if constexpr (W == 1) {
+    r.w[0] = *(const uint32_t *)a;
+  } else {
+    typedef uint32_t UV __attribute__((ext_vector_type(W)));
+    const UV x = *(const UV *)a;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const uint32_t u = x[k];
+      r.w[k] = u;
+    }
+  }
+}
+template <int DT, int N>
+__device__ __forceinline__ void dt_decode_raw(const dt_raw<DT, N> &r, float *f) {
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    if constexpr (DT == RK_DTYPE_F32)
+      f[e] = __uint_as_float(r.w[e]);
+    else
+      f[e] = dt_decode<DT>((uint16_t)(r.w[e / 2] >> (16 * (e & 1))));
+  }
+}

@@ -437,3 +437,15 @@ def test_attention_strided_errors(rk):
     assert lib.rk_attention_strided_dev(p, 64, p, 64, p, 64, 4, 4, 2, 1, 64, 0.1, 0.0, 0, -1, 0, 0, p, 128, None) == rk.RK_E_SHAPE
     assert lib.rk_attention_strided_dev(p, 132, p, 68, p, 68, 4, 4, 2, 1, 64, 0.1, 0.0, 0, -1, 0, 0, p, 128, None) == rk.RK_E_SHAPE
     buf.free()
+
+
+@pytest.mark.parametrize("groups", ["1", "2", "4"])
+def test_qk_norm_rope_row_groups(rk, orc, groups, monkeypatch):
+    monkeypatch.setenv("RK_QKNR_GROUPS", groups)
+    hq, hk, s, d = 5, 3, 61, 128
+    note(f"qk_norm_rope RK_QKNR_GROUPS={groups} S={s} {hq}/{hk}")
+    r = np.random.default_rng(43)
+    qkv, stride, wq, wk, c, sn = _qkv_case(r, s, hq, hk, d, 8)
+    qkv = r.integers(-8, 9, qkv.shape).astype(np.float32)
+    got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, wq, wk, c, sn, "f16")
+    assert (got == qknr_ref(orc, x, hq, hk, d, wq, wk, c, sn, "f16")).all()
