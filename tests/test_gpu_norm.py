@@ -449,3 +449,56 @@ def test_qk_norm_rope_row_groups(rk, orc, groups, monkeypatch):
     qkv = r.integers(-8, 9, qkv.shape).astype(np.float32)
     got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, wq, wk, c, sn, "f16")
     assert (got == qknr_ref(orc, x, hq, hk, d, wq, wk, c, sn, "f16")).all()
+
+
+def test_qwen3_attention_chain_in_place(rk, orc):
+    """qkv GEMM into one buffer → q/k norm + RoPE in place → attention reading q, k, v where
+    they lie; against the same ops on separate tensors (bit for bit) and the oracle."""
+    s, hid, hq, hk, d = 203, 256, 4, 2, 128
+    width = (hq + 2 * hk) * d
+    note(f"Qwen3 attention chain S={s} hidden={hid} {hq}/{hk} d={d}")
+    r = np.random.default_rng(44)
+    x = r.standard_normal((s, hid)).astype(np.float16)
+    w = (r.standard_normal((width, hid)) * 0.06).astype(np.float16)
+    wq = (1 + 0.2 * r.standard_normal(d)).astype(np.float16)
+    wk = (1 + 0.2 * r.standard_normal(d)).astype(np.float16)
+    ang = np.arange(s)[:, None] * (10000.0 ** (-np.arange(d // 2) / (d // 2)))[None, :]
+    cs, sn = np.cos(ang).astype(np.float16), np.sin(ang).astype(np.float16)
+    lib = rk.lib()
+    wid = rk.pack(w)
+    dev = Dev(rk)
+    try:
+        px = dev.put(x)
+        pqkv = dev.put(np.zeros((s, width), np.float16))
+        rc = lib.rk_matmul_f16_dev(int(wid), px, s, hid, pqkv, None)
+        assert rc == 0, lib.rk_last_error()
+        qkv0 = dev.get(pqkv, np.zeros((s, width), np.float16))  # the projection, before the prologue
+        pw, pk, pc, ps = dev.put(wq), dev.put(wk), dev.put(cs), dev.put(sn)
+        assert lib.rk_qk_norm_rope_dev(pqkv, s, width, hq, hk, d, pw, pk, 1e-6, pc, ps,
+                                       rk.DTYPE_F16, rk.DTYPE_F16, None) == 0, lib.rk_last_error()
+        po = dev.put(np.zeros((s, hq * d), np.float16))
+        assert lib.rk_attention_strided_dev(pqkv, width, pqkv + hq * d * 2, width, pqkv + (hq + hk) * d * 2,
+                                            width, s, s, hq, hk, d, d ** -0.5, 0.0, 1, -1, 0, 0, po,
+                                            hq * d, None) == 0, lib.rk_last_error()
+        got = dev.get(po, np.zeros((s, hq * d), np.float16))
+    finally:
+        dev.free()
+    # the same steps on separate tensors: sliced q, k, v, the separate norm and RoPE ops,
+    # then rk_attention_dev
+    q = qkv0[:, :hq * d].astype(np.float32).reshape(1, s, hq, d)
+    k = qkv0[:, hq * d:(hq + hk) * d].astype(np.float32).reshape(1, s, hk, d)
+    v = qkv0[:, (hq + hk) * d:].copy()
+    c32, s32 = cs.astype(np.float32), sn.astype(np.float32)
+    qn, _ = rms_dev(rk, orc, q, wq.astype(np.float32), 1e-6, "f16")
+    kn, _ = rms_dev(rk, orc, k, wk.astype(np.float32), 1e-6, "f16")
+    qr, _ = rope_dev(rk, orc, qn, c32, s32, "f16")
+    kr, _ = rope_dev(rk, orc, kn, c32, s32, "f16")
+    q16 = qr.reshape(s, hq * d).astype(np.float16)
+    k16 = kr.reshape(s, hk * d).astype(np.float16)
+    want = _attn_packed(rk, q16, k16, v, hq, hk, d, 1, s)
+    assert (got.view(np.uint16) == want.view(np.uint16)).all()
+    # and the oracle's f64 attention on those q, k, v (fp16 output gate)
+    ref = orc.attention_ref(q16, k16, v, hq, hk, d, d ** -0.5, 0.0, 1)
+    g = got.astype(np.float64)
+    cos = (g * ref).sum() / np.sqrt((g * g).sum() * (ref * ref).sum())
+    assert cos >= 0.9999 and orc.max_rel(g, ref) <= 1e-2
