@@ -2,7 +2,7 @@
  * oracle.c — CPU restatement of the royalcat/burn-rocket accelerator op surface.
  *
  * TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg may load this library, and only as the checker or as the
+ * cpu_baseline leg may load this library, and only as the parity reference or as the
  * timed CPU baseline. The product path (burn-rocket_amd/) never calls it.
  *
  * Each function names the reference file:line it restates. The reference is

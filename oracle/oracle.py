@@ -1,7 +1,7 @@
 """ctypes wrapper of the CPU oracle (oracle/liboracle.so) and parity metrics.
 
 TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker or the timed CPU baseline. The
+cpu_baseline leg of bench.py, as the parity reference or the timed CPU baseline. The
 functions restate the reference (see oracle.c for file:line citations).
 """
 import ctypes
