@@ -502,3 +502,15 @@ def test_qwen3_attention_chain_in_place(rk, orc):
     g = got.astype(np.float64)
     cos = (g * ref).sum() / np.sqrt((g * g).sum() * (ref * ref).sum())
     assert cos >= 0.9999 and orc.max_rel(g, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("hq,hk,s", [(2, 0, 9), (0, 3, 9), (1, 1, 1), (7, 1, 2)])
+def test_qk_norm_rope_head_counts(rk, orc, hq, hk, s):
+    d = 64
+    note(f"qk_norm_rope heads {hq}/{hk} S={s}")
+    r = np.random.default_rng(hq * 10 + hk + s)
+    qkv, stride, wq, wk, c, sn = _qkv_case(r, s, hq, hk, d, 8)
+    qkv = r.integers(-8, 9, qkv.shape).astype(np.float32)
+    for dt in ("f16", "f32"):
+        got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, wq, wk, c, sn, dt)
+        assert (got == qknr_ref(orc, x, hq, hk, d, wq, wk, c, sn, dt)).all()
