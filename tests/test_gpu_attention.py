@@ -200,3 +200,28 @@ def test_attention_is_deterministic(rk, orc):
     b = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=1)
     assert (a == b).all()
     check(orc, a, orc.attention_flex(q, k, v, h, kv, d, d ** -0.5, 0.0, 1))
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_head_padding_invariance(rk, orc, mode):
+    """Zero-padding the head dim 72 → 80 / 96 (the reference's padded-layout test,
+    src/clef/vision/tests.rs:411-473): the padded output columns are exactly zero and the
+    rest is the plain attention within the reference's max-abs bound 2e-3 of the f64 model.
+    The scale stays 72^-0.5."""
+    s, h, d = 157, 4, 72
+    r = np.random.default_rng(72 + mode)
+    q = r.standard_normal((s, h * d)).astype(np.float16)
+    k = r.standard_normal((s, h * d)).astype(np.float16)
+    v = r.standard_normal((s, h * d)).astype(np.float16)
+    want = orc.attention_ref(q, k, v, h, h, d, d ** -0.5, 0.0, mode)
+    for dp in (80, 96):
+        note(f"head padding 72 -> {dp}, mode {mode}")
+
+        def pad(x):
+            out = np.zeros((s, h, dp), np.float16)
+            out[:, :, :d] = x.reshape(s, h, d)
+            return out.reshape(s, h * dp)
+
+        got = attn_dev(rk, pad(q), pad(k), pad(v), h, h, dp, d ** -0.5, mode=mode).reshape(s, h, dp)
+        assert (got[:, :, d:] == 0).all()
+        assert np.abs(got[:, :, :d].reshape(s, h * d) - want).max() < 2e-3
