@@ -49,6 +49,7 @@
 // (flash_attn_ref, attn/oneshot.rs:118-127).
 #include "common.hpp"
 #include "kernels.hpp"
+#include "vt_tile.hpp"
 
 namespace {
 
@@ -550,62 +551,15 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   }
 }
 
-// V [n_kv] × (head g, d) → Vt[g][d][p] for p in [0, n_kv_pad): slot p of each
-// 32-key chunk holds key 4·(p/8 % 4) + p%4 + 16·((p%8)/4) of the chunk (the
-// order in which the PV operand lanes consume keys). Rows d ≥ D and keys ≥
-// n_kv are zero. A block moves a 64-key × 64-d tile: 16-byte loads along d
-// into LDS, 16-byte stores of 8 consecutive slots along the keys.
-// The LDS tile holds key row kk as 8 chunks of 8 d, chunk c at position
-// c ^ vt_swz(kk): the 8 key rows that one lane group reads for a slot are
-// kk0 + {0, 4, 8, 12, 32, 36, 40, 44} (+ a common offset below 4 or 16..19),
-// which vt_swz maps to 8 different positions, so the 2-byte reads that
-// gather a slot vector hit 8 different bank groups.
-__device__ __forceinline__ int vt_swz(int kk) { return ((kk >> 2) & 3) | ((kk >> 3) & 4); }
-
+// V [n_kv] × (head g, d) → Vt (layout and tile order: vt_tile.hpp); one
+// 64-key × 64-d tile per block.
 __global__ __launch_bounds__(256) void v_transpose_kernel(const f16 *__restrict__ v,
                                                           int64_t tok_stride, int64_t head_stride,
                                                           int64_t d_stride, int n_kv, int n_kv_pad,
                                                           int D, int DVp, f16 *__restrict__ vt) {
-  __shared__ half8 tile[64][8];
-  const int g = blockIdx.z;
-  const int key0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
-  const f16 *vg = v + (int64_t)g * head_stride;
-  if (d_stride == 1) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int idx = r * 256 + threadIdx.x;  // 64 keys × 8 chunks of 8 d
-      const int kk = idx >> 3, ch = idx & 7;
-      const int key = key0 + kk, d = d0 + ch * 8;
-      half8 x = half8{};
-      if (key < n_kv && d < D) x = *(const half8 *)(vg + (int64_t)key * tok_stride + d);
-      tile[kk][ch ^ vt_swz(kk)] = x;
-    }
-  } else {
-    f16 *t16 = (f16 *)tile;
-    for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
-      const int kk = idx / 64, dd = idx % 64;
-      const int key = key0 + kk, d = d0 + dd;
-      t16[kk * 64 + ((dd >> 3) ^ vt_swz(kk)) * 8 + (dd & 7)] =
-          (key < n_kv && d < D) ? vg[(int64_t)key * tok_stride + (int64_t)d * d_stride] : (f16)0.f;
-    }
-  }
-  __syncthreads();
-  const f16 *t16 = (const f16 *)tile;
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int idx = r * 256 + threadIdx.x;  // 64 d rows × 8 chunks of 8 slots
-    const int dd = idx >> 3, ch = idx & 7;
-    const int d = d0 + dd;
-    if (d >= DVp) continue;
-    half8 y;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int p = ch * 8 + i, pc = p & 31;
-      const int kk = (p & ~31) + 4 * ((pc >> 3) & 3) + (pc & 3) + 16 * ((pc & 7) >> 2);
-      y[i] = t16[kk * 64 + ((dd >> 3) ^ vt_swz(kk)) * 8 + (dd & 7)];
-    }
-    *(half8 *)(vt + ((int64_t)g * DVp + d) * n_kv_pad + key0 + ch * 8) = y;
-  }
+  __shared__ vt_half8 tile[64][8];
+  vt_tile(v, tok_stride, head_stride, d_stride, n_kv, n_kv_pad, D, DVp, vt, blockIdx.x, blockIdx.y,
+          blockIdx.z, tile, threadIdx.x);
 }
 
 int rk_attn_dv_pad(int head_dim) { return (head_dim + 15) / 16 * 16; }

@@ -1547,6 +1547,48 @@ extern "C" int rk_qk_norm_rope_dev(void *qkv, int64_t s, int64_t row_stride, int
                                  pick(stream)), name);
   return RK_OK;
 }
+extern "C" int rk_attention_qkv_dev(void *qkv, int64_t s, int64_t row_stride, int n_head,
+                                    int n_kv_heads, int head_dim, const void *q_norm_w,
+                                    const void *k_norm_w, double eps, const void *cos,
+                                    const void *sin, int cs_dtype, float scale, float softcap,
+                                    int mask_mode, int64_t window, int64_t q0, int64_t k0,
+                                    void *out, int64_t out_stride, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_attention_qkv_dev";
+  RK_TRY(ensure(name));
+  int mode = mask_mode;
+  RK_TRY(attn_check(s, s, n_head, n_kv_heads, head_dim, &mode, window, name));
+  if (s * (n_head + n_kv_heads) > INT32_MAX)
+    return fail(RK_E_SHAPE, name, "s·(q + k heads) of 2^31 or more");
+  const int64_t width = (int64_t)(n_head + 2 * n_kv_heads) * head_dim;
+  if (row_stride < width || out_stride < (int64_t)n_head * head_dim)
+    return fail(RK_E_SHAPE, name, "a row stride is shorter than its heads");
+  if ((row_stride | out_stride) % 8 != 0 || (((uintptr_t)qkv | (uintptr_t)out) & 15) != 0)
+    return fail(RK_E_SHAPE, name, "row strides must be multiples of 8 values, buffers 16-byte aligned");
+  if (cs_dtype != RK_DTYPE_F16 && cs_dtype != RK_DTYPE_F32)
+    return fail(RK_E_UNSUPPORTED, name, "cos/sin must be fp16 or f32");
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(RK_E_SHAPE, name, "give both norm weights or neither");
+  if (head_dim % 2 != 0) return fail(RK_E_SHAPE, name, "the head dim must be even");
+  if (s == 0) return RK_OK;
+  if (!qkv || !cos || !sin || !out) return fail(RK_E_SHAPE, name, "null buffer");
+  if (rk_qk_norm_rope_cv(qkv, row_stride, head_dim, RK_DTYPE_F16, q_norm_w, k_norm_w, cos, sin,
+                         cs_dtype) == 0)
+    return fail(RK_E_UNSUPPORTED, name, "head_dim / row_stride / buffer alignment allow no vector width");
+  hipStream_t st = pick(stream);
+  const int dvp = rk_attn_dv_pad(head_dim);
+  const int64_t n_kv_pad = round_up_i(s, rk_attn_kv_tile());
+  void *vt;
+  RK_TRY(scratch("attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
+  HIP_TRY(rk_launch_qk_norm_rope(qkv, row_stride, (int)s, n_head, n_kv_heads, head_dim, q_norm_w,
+                                 k_norm_w, (float)eps, cos, sin, cs_dtype, RK_DTYPE_F16, st, vt,
+                                 (int)n_kv_pad, dvp), name);
+  RK_TRY(attn_run(qkv, (const uint16_t *)qkv + (int64_t)n_head * head_dim, vt, out, s, s, n_kv_pad,
+                  n_head, n_kv_heads, head_dim, scale, softcap, mode, window, q0, k0, false, st,
+                  name, row_stride, row_stride, out_stride));
+  g_eng->calls++;
+  return RK_OK;
+}
 extern "C" int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d,
                            double eps) {
   std::lock_guard<std::mutex> lk(g_mu);

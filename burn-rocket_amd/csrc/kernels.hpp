@@ -64,9 +64,18 @@ hipError_t rk_launch_rope(const void *x, const void *cs, const void *sn, int cs_
 // will use, 0 when none fits (then the launch fails).
 int rk_qk_norm_rope_cv(const void *qkv, int64_t row_stride, int D, int dtype, const void *wq,
                        const void *wk, const void *cs, const void *sn, int cs_dtype);
+// With vt non-null (fp16 only) the same launch also writes V — the HK heads
+// after the k heads — as the attention kernel's Vᵀ [HK][dv_pad][n_kv_pad].
+struct QknrVt {
+  void *vt;        // null: no Vᵀ tiles
+  int n_kv_pad, dv_pad;
+  int tiles_k, tiles_d;
+  int nb_norm;     // blocks of the norm part (set by the launcher)
+};
 hipError_t rk_launch_qk_norm_rope(void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
                                   const void *wq, const void *wk, float eps, const void *cs,
-                                  const void *sn, int cs_dtype, int dtype, hipStream_t st);
+                                  const void *sn, int cs_dtype, int dtype, hipStream_t st,
+                                  void *vt = nullptr, int n_kv_pad = 0, int dv_pad = 0);
 
 // Per-row symmetric quantizer (scale = max(amax/127, 1e-12), codes
 // round-half-away(x·(1/scale)) clamped to ±127), `group` values per scale.

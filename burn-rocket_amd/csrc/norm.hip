@@ -19,6 +19,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "vt_tile.hpp"
 
 namespace {
 constexpr int es_of(int dt) { return dt == RK_DTYPE_F32 ? 4 : 2; }
@@ -318,8 +319,21 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(void *__restrict__ qk
                                                            const void *__restrict__ wq,
                                                            const void *__restrict__ wk, float eps,
                                                            const void *__restrict__ cs,
-                                                           const void *__restrict__ sn) {
+                                                           const void *__restrict__ sn,
+                                                           QknrVt vtj) {
 #pragma clang fp contract(off)
+  // Blocks from vtj.nb_norm on rewrite V (the HK heads after the k heads) as
+  // the attention kernel's Vᵀ, one 64-key × 64-d tile each.
+  if ((int)blockIdx.x >= vtj.nb_norm) {
+    __shared__ vt_half8 tile[64][8];
+    const int t = (int)blockIdx.x - vtj.nb_norm;
+    const int kb = t % vtj.tiles_k, rest = t / vtj.tiles_k;
+    const int db = rest % vtj.tiles_d, g = rest / vtj.tiles_d;
+    const f16 *v = (const f16 *)qkv + (int64_t)(HQ + HK) * D;
+    vt_tile(v, row_stride, D, 1, S, vtj.n_kv_pad, D, vtj.dv_pad, (f16 *)vtj.vt, kb, db, g, tile,
+            threadIdx.x);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int li = lane & (lpr - 1), grp0 = lane - li;
   const int rpw = 64 / lpr;
@@ -327,7 +341,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(void *__restrict__ qk
   const int heads = HQ + HK;
   const int64_t rows = (int64_t)S * heads;
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int64_t n_waves = ((int64_t)vtj.nb_norm * blockDim.x) >> 6;
   const float fd = (float)D;
   const bool has_w = wq != nullptr;
   const int partner = grp0 + (li < hc ? li + hc : li - hc);
@@ -394,7 +408,7 @@ namespace {
 template <int DT, int CT, int CV>
 hipError_t launch_qknr_cfg(void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
                            const void *wq, const void *wk, float eps, const void *cs,
-                           const void *sn, hipStream_t st) {
+                           const void *sn, QknrVt vtj, hipStream_t st) {
   const int nch = D / CV;
   int lpr = 1;
   while (lpr < nch) lpr <<= 1;
@@ -403,32 +417,33 @@ hipError_t launch_qknr_cfg(void *qkv, int64_t row_stride, int S, int HQ, int HK,
   const int knob = rk_knob("RK_QKNR_GROUPS", 2);
   const int g = knob == 1 || knob == 4 ? knob : 2;
   const int64_t rows = (int64_t)S * (HQ + HK), rows_per_block = 4 * (64 / lpr) * g;
-  const unsigned blocks =
-      (unsigned)std::min<int64_t>((rows + rows_per_block - 1) / rows_per_block, 16384);
+  const int nb = (int)std::min<int64_t>((rows + rows_per_block - 1) / rows_per_block, 16384);
+  vtj.nb_norm = nb;
+  const unsigned blocks = (unsigned)nb + (vtj.vt ? (unsigned)(vtj.tiles_k * vtj.tiles_d * HK) : 0u);
   if (g == 1)
     hipLaunchKernelGGL((qk_norm_rope_kernel<DT, CT, CV, 1>), dim3(blocks), dim3(256), 0, st, qkv,
-                       row_stride, S, HQ, HK, D, lpr, wq, wk, eps, cs, sn);
+                       row_stride, S, HQ, HK, D, lpr, wq, wk, eps, cs, sn, vtj);
   else if (g == 2)
     hipLaunchKernelGGL((qk_norm_rope_kernel<DT, CT, CV, 2>), dim3(blocks), dim3(256), 0, st, qkv,
-                       row_stride, S, HQ, HK, D, lpr, wq, wk, eps, cs, sn);
+                       row_stride, S, HQ, HK, D, lpr, wq, wk, eps, cs, sn, vtj);
   else
     hipLaunchKernelGGL((qk_norm_rope_kernel<DT, CT, CV, 4>), dim3(blocks), dim3(256), 0, st, qkv,
-                       row_stride, S, HQ, HK, D, lpr, wq, wk, eps, cs, sn);
+                       row_stride, S, HQ, HK, D, lpr, wq, wk, eps, cs, sn, vtj);
   return hipGetLastError();
 }
 
 template <int DT, int CT>
 hipError_t launch_qknr_t(int cv, void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
                          const void *wq, const void *wk, float eps, const void *cs,
-                         const void *sn, hipStream_t st) {
+                         const void *sn, QknrVt vtj, hipStream_t st) {
   switch (cv) {
     case 8:
       if constexpr (DT != RK_DTYPE_F32)
-        return launch_qknr_cfg<DT, CT, 8>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+        return launch_qknr_cfg<DT, CT, 8>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st);
       break;
-    case 4: return launch_qknr_cfg<DT, CT, 4>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
-    case 2: return launch_qknr_cfg<DT, CT, 2>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
-    case 1: return launch_qknr_cfg<DT, CT, 1>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+    case 4: return launch_qknr_cfg<DT, CT, 4>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st);
+    case 2: return launch_qknr_cfg<DT, CT, 2>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st);
+    case 1: return launch_qknr_cfg<DT, CT, 1>(qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st);
   }
   return hipErrorInvalidValue;
 }
@@ -449,21 +464,32 @@ int rk_qk_norm_rope_cv(const void *qkv, int64_t row_stride, int D, int dtype, co
 
 hipError_t rk_launch_qk_norm_rope(void *qkv, int64_t row_stride, int S, int HQ, int HK, int D,
                                   const void *wq, const void *wk, float eps, const void *cs,
-                                  const void *sn, int cs_dtype, int dtype, hipStream_t st) {
+                                  const void *sn, int cs_dtype, int dtype, hipStream_t st,
+                                  void *vt, int n_kv_pad, int dv_pad) {
   if (S <= 0 || HQ + HK <= 0) return hipSuccess;
+  QknrVt vtj{};
+  if (vt) {
+    // Vᵀ tiles only for fp16 V (the attention kernel's operand type)
+    if (dtype != RK_DTYPE_F16 || n_kv_pad % 64 != 0 || D % 8 != 0) return hipErrorInvalidValue;
+    vtj.vt = vt;
+    vtj.n_kv_pad = n_kv_pad;
+    vtj.dv_pad = dv_pad;
+    vtj.tiles_k = n_kv_pad / 64;
+    vtj.tiles_d = (dv_pad + 63) / 64;
+  }
   const int cv = rk_qk_norm_rope_cv(qkv, row_stride, D, dtype, wq, wk, cs, sn, cs_dtype);
   if (cv == 0) return hipErrorInvalidValue;
   const bool cs_f32 = cs_dtype == RK_DTYPE_F32;
   if (cs_dtype != dtype && !cs_f32) return hipErrorInvalidValue;
   switch (dtype) {
     case RK_DTYPE_F32:
-      return launch_qknr_t<RK_DTYPE_F32, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+      return launch_qknr_t<RK_DTYPE_F32, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st);
     case RK_DTYPE_F16:
-      return cs_f32 ? launch_qknr_t<RK_DTYPE_F16, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st)
-                    : launch_qknr_t<RK_DTYPE_F16, RK_DTYPE_F16>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+      return cs_f32 ? launch_qknr_t<RK_DTYPE_F16, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st)
+                    : launch_qknr_t<RK_DTYPE_F16, RK_DTYPE_F16>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st);
     case RK_DTYPE_BF16:
-      return cs_f32 ? launch_qknr_t<RK_DTYPE_BF16, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st)
-                    : launch_qknr_t<RK_DTYPE_BF16, RK_DTYPE_BF16>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, st);
+      return cs_f32 ? launch_qknr_t<RK_DTYPE_BF16, RK_DTYPE_F32>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st)
+                    : launch_qknr_t<RK_DTYPE_BF16, RK_DTYPE_BF16>(cv, qkv, row_stride, S, HQ, HK, D, wq, wk, eps, cs, sn, vtj, st);
   }
   return hipErrorInvalidValue;
 }

@@ -386,6 +386,20 @@ int rk_qk_norm_rope_dev(void *qkv, int64_t s, int64_t row_stride, int n_q_heads,
                         int64_t head_dim, const void *q_norm_w, const void *k_norm_w, double eps,
                         const void *cos, const void *sin, int cs_dtype, int dtype,
                         rk_stream stream);
+/* A whole self-attention block on an fp16 q|k|v projection output, in two
+ * launches: rk_qk_norm_rope_dev's in-place prologue (its conventions; the
+ * same launch also rewrites V into the attention kernel's operand layout),
+ * then attention over the s tokens as rk_attention_strided_dev with q, k and
+ * v read from the buffer (n_head q heads at column 0, n_kv_heads k heads at
+ * n_head·head_dim, V after them) and out [s, out_stride]. The qkv buffer
+ * holds the normalised, rotated q and k afterwards. It is the Qwen3 layer's
+ * fused-projection path, src/qwen3_embedding/model.rs:355-376 followed by its
+ * attention call (model.rs:449-463), with no intermediate tensors. */
+int rk_attention_qkv_dev(void *qkv, int64_t s, int64_t row_stride, int n_head, int n_kv_heads,
+                         int head_dim, const void *q_norm_w, const void *k_norm_w, double eps,
+                         const void *cos, const void *sin, int cs_dtype, float scale,
+                         float softcap, int mask_mode, int64_t window, int64_t q0, int64_t k0,
+                         void *out, int64_t out_stride, rk_stream stream);
 /* Host-buffer forms on f32 arrays (synchronous). */
 int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d, double eps);
 int rk_rms_norm_noscale(const float *x, float *out, int64_t rows, int64_t d, double eps);

@@ -514,3 +514,40 @@ def test_qk_norm_rope_head_counts(rk, orc, hq, hk, s):
     for dt in ("f16", "f32"):
         got, x = qknr_dev(rk, orc, qkv, stride, hq, hk, d, wq, wk, c, sn, dt)
         assert (got == qknr_ref(orc, x, hq, hk, d, wq, wk, c, sn, dt)).all()
+
+
+@pytest.mark.parametrize("s,hq,hk,d,mode", [(203, 4, 2, 128, 1), (150, 3, 3, 72, 0), (64, 8, 1, 64, 1),
+                                            (1, 2, 1, 128, 1)])
+def test_attention_qkv_equals_prologue_then_strided_attention(rk, orc, s, hq, hk, d, mode):
+    note(f"rk_attention_qkv_dev S={s} {hq}/{hk} d={d} mode={mode}")
+    width = (hq + 2 * hk) * d + 8
+    r = np.random.default_rng(s + d)
+    qkv = (r.standard_normal((s, width)) * 2).astype(np.float16)
+    wq = (1 + 0.2 * r.standard_normal(d)).astype(np.float16)
+    wk = (1 + 0.2 * r.standard_normal(d)).astype(np.float16)
+    ang = np.arange(s)[:, None] * (10000.0 ** (-np.arange(d // 2) / (d // 2)))[None, :]
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    lib = rk.lib()
+    outs = []
+    for fused in (False, True):
+        dev = Dev(rk)
+        try:
+            p = dev.put(qkv)
+            pw, pk, pc, ps = dev.put(wq), dev.put(wk), dev.put(cs), dev.put(sn)
+            po = dev.put(np.zeros((s, hq * d), np.float16))
+            if fused:
+                rc = lib.rk_attention_qkv_dev(p, s, width, hq, hk, d, pw, pk, 1e-6, pc, ps, rk.DTYPE_F32,
+                                              d ** -0.5, 0.0, mode, -1, 0, 0, po, hq * d, None)
+                assert rc == 0, lib.rk_last_error()
+            else:
+                assert lib.rk_qk_norm_rope_dev(p, s, width, hq, hk, d, pw, pk, 1e-6, pc, ps, rk.DTYPE_F32,
+                                               rk.DTYPE_F16, None) == 0, lib.rk_last_error()
+                assert lib.rk_attention_strided_dev(p, width, p + hq * d * 2, width, p + (hq + hk) * d * 2, width,
+                                                    s, s, hq, hk, d, d ** -0.5, 0.0, mode, -1, 0, 0, po, hq * d,
+                                                    None) == 0, lib.rk_last_error()
+            outs.append((dev.get(po, np.zeros((s, hq * d), np.float16)), dev.get(p, qkv)))
+        finally:
+            dev.free()
+    (o0, b0), (o1, b1) = outs
+    assert (b0.view(np.uint16) == b1.view(np.uint16)).all(), "the buffer after the prologue"
+    assert (o0.view(np.uint16) == o1.view(np.uint16)).all(), "the attention output"
