@@ -90,6 +90,7 @@ SIGNATURES = {
                                       _p]),
     "rk_attention_qkv_dev": (_i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _c.c_double, _p, _p, _i,
                                   _c.c_float, _c.c_float, _i, _i64, _i64, _i64, _p, _i64, _p]),
+    "rk_rms_norm_quantize_dev": (_i, [_p, _p, _i, _i64, _i64, _c.c_double, _i, _p, _p, _p]),
     "rk_rms_norm": (_i, [_p, _p, _p, _i64, _i64, _c.c_double]),
     "rk_rms_norm_noscale": (_i, [_p, _p, _i64, _i64, _c.c_double]),
     "rk_rope": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64]),

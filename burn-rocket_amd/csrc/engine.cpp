@@ -1589,6 +1589,23 @@ extern "C" int rk_attention_qkv_dev(void *qkv, int64_t s, int64_t row_stride, in
   g_eng->calls++;
   return RK_OK;
 }
+extern "C" int rk_rms_norm_quantize_dev(const void *x, const void *w, int w_dtype, int64_t rows,
+                                        int64_t d, double eps, int dtype, int8_t *q,
+                                        float *q_scale, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *name = "rk_rms_norm_quantize_dev";
+  RK_TRY(ensure(name));
+  RK_TRY(rms_check(x, q, rows, d, dtype, name));
+  if (w && !float_dtype(w_dtype)) return fail(RK_E_SHAPE, name, "unknown weight dtype");
+  if (rows > 0 && !q_scale) return fail(RK_E_SHAPE, name, "null scale buffer");
+  if (!rk_rms_quant_fits(x, w, w_dtype, q, (int)d, dtype))
+    return fail(RK_E_UNSUPPORTED, name,
+                "needs d a multiple of 16 bytes of x and at most 8 KB per row, the weight in x's "
+                "type, 16-byte aligned x and w (use rk_rms_norm_dev + rk_quantize_rows_dev)");
+  HIP_TRY(rk_launch_rms_quant(x, w, q, q_scale, rows, (int)d, (float)eps, dtype, pick(stream)),
+          name);
+  return RK_OK;
+}
 extern "C" int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d,
                            double eps) {
   std::lock_guard<std::mutex> lk(g_mu);

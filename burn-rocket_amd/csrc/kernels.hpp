@@ -77,6 +77,13 @@ hipError_t rk_launch_qk_norm_rope(void *qkv, int64_t row_stride, int S, int HQ, 
                                   const void *sn, int cs_dtype, int dtype, hipStream_t st,
                                   void *vt = nullptr, int n_kv_pad = 0, int dv_pad = 0);
 
+// RMSNorm (w null: scale-free; else of x's type) rounded to x's type, then the
+// per-token int8 quantizer, in one pass; rk_rms_quant_fits: whether the
+// shape and alignment take this kernel (rows of at most 512 16-byte chunks).
+bool rk_rms_quant_fits(const void *x, const void *w, int w_dtype, const int8_t *q, int d, int dtype);
+hipError_t rk_launch_rms_quant(const void *x, const void *w, int8_t *q, float *qs, int64_t rows,
+                               int d, float eps, int dtype, hipStream_t st);
+
 // Per-row symmetric quantizer (scale = max(amax/127, 1e-12), codes
 // round-half-away(x·(1/scale)) clamped to ±127), `group` values per scale.
 hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,

@@ -493,3 +493,134 @@ hipError_t rk_launch_qk_norm_rope(void *qkv, int64_t row_stride, int S, int HQ, 
   }
   return hipErrorInvalidValue;
 }
+
+// ---------------------------------------------------------------------------
+// RMSNorm followed by the per-token int8 quantizer, one pass: y = RMSNorm(x)
+// rounded to x's type (what the separate op returns), then scale[row] =
+// max(amax(y)/127, 1e-12) and q = round-half-away(y·(1/scale)) clamped to
+// ±127 (quantize_row_groups with one group per row, host.rs:77-90) — the
+// activation side of a per-token W8A8 GEMM after a norm. Rows are held in
+// registers (NC chunks of 16 bytes per lane on LPR lanes); the row maximum
+// is a butterfly of fmaxf, exact in any order.
+// ---------------------------------------------------------------------------
+template <int DT, int WT, int LPR, int NC>
+__global__ __launch_bounds__(256) void rms_quant_kernel(const void *__restrict__ x,
+                                                        const void *__restrict__ w,
+                                                        int8_t *__restrict__ q,
+                                                        float *__restrict__ qscale, int64_t rows,
+                                                        int d, float eps) {
+#pragma clang fp contract(off)
+  constexpr int CV = 16 / es_of(DT);
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, li = lane % LPR;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t n_waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int nch = d / CV;
+  const float fd = (float)d;
+  for (int64_t r0 = wave * RPW; r0 < rows; r0 += n_waves * RPW) {
+    const int64_t row = r0 + lane / LPR;
+    const bool live = row < rows;
+    const int64_t base = row * (int64_t)d;
+    float v[NC][CV];
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int ch = li + LPR * i;
+#pragma unroll
+      for (int e = 0; e < CV; ++e) v[i][e] = 0.f;
+      if (live && ch < nch) dt_load_vec<DT, CV>(x, base + (int64_t)ch * CV, v[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+#pragma unroll
+      for (int e = 0; e < CV; ++e) acc += v[i][e] * v[i][e];
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    const float inv = 1.0f / sqrtf(acc / fd + eps);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int ch = li + LPR * i;
+      if (live && ch < nch) {
+        float wv[CV];
+        if constexpr (WT >= 0) dt_load_vec<WT, CV>(w, (int64_t)ch * CV, wv);
+#pragma unroll
+        for (int e = 0; e < CV; ++e) {
+          const float o = WT >= 0 ? v[i][e] * inv * wv[e] : v[i][e] * inv;
+          v[i][e] = dt_decode<DT>(dt_encode<DT>(o));
+          amax = fmaxf(amax, fabsf(v[i][e]));
+        }
+      }
+    }
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float s = fmaxf(amax / 127.0f, 1e-12f);
+    const float qinv = 1.0f / s;
+    if (live && li == 0) qscale[row] = s;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int ch = li + LPR * i;
+      if (live && ch < nch) {
+        uint32_t words[CV / 4];
+#pragma unroll
+        for (int k = 0; k < CV / 4; ++k) words[k] = 0;
+#pragma unroll
+        for (int e = 0; e < CV; ++e) {
+          const float c = fminf(fmaxf(roundf(v[i][e] * qinv), -127.0f), 127.0f);
+          words[e / 4] |= (uint32_t)(uint8_t)(int8_t)(int)c << (8 * (e % 4));
+        }
+        int8_t *qp = q + base + (int64_t)ch * CV;
+        if constexpr (CV == 8) *(uintx2 *)qp = uintx2{words[0], words[1]};
+        else *(uint32_t *)qp = words[0];
+      }
+    }
+  }
+}
+
+namespace {
+template <int DT, int WT, int LPR, int NC>
+hipError_t launch_rq_cfg(const void *x, const void *w, int8_t *q, float *qs, int64_t rows, int d,
+                         float eps, hipStream_t st) {
+  const int64_t rows_per_block = 4 * (64 / LPR);
+  const unsigned blocks =
+      (unsigned)std::min<int64_t>((rows + rows_per_block - 1) / rows_per_block, 16384);
+  hipLaunchKernelGGL((rms_quant_kernel<DT, WT, LPR, NC>), dim3(blocks), dim3(256), 0, st, x, w, q,
+                     qs, rows, d, eps);
+  return hipGetLastError();
+}
+template <int DT, int WT>
+hipError_t launch_rq_t(const void *x, const void *w, int8_t *q, float *qs, int64_t rows, int d,
+                       float eps, hipStream_t st) {
+  const int nch = d / (16 / es_of(DT));
+  if (nch <= 8) return launch_rq_cfg<DT, WT, 8, 1>(x, w, q, qs, rows, d, eps, st);
+  if (nch <= 16) return launch_rq_cfg<DT, WT, 16, 1>(x, w, q, qs, rows, d, eps, st);
+  if (nch <= 32) return launch_rq_cfg<DT, WT, 32, 1>(x, w, q, qs, rows, d, eps, st);
+  if (nch <= 64) return launch_rq_cfg<DT, WT, 64, 1>(x, w, q, qs, rows, d, eps, st);
+  if (nch <= 128) return launch_rq_cfg<DT, WT, 64, 2>(x, w, q, qs, rows, d, eps, st);
+  if (nch <= 256) return launch_rq_cfg<DT, WT, 64, 4>(x, w, q, qs, rows, d, eps, st);
+  return launch_rq_cfg<DT, WT, 64, 8>(x, w, q, qs, rows, d, eps, st);
+}
+}  // namespace
+
+bool rk_rms_quant_fits(const void *x, const void *w, int w_dtype, const int8_t *q, int d, int dtype) {
+  const int cv = 16 / es_of(dtype);
+  return d % cv == 0 && d / cv <= 512 && (w == nullptr || w_dtype == dtype) &&
+         (((uintptr_t)x | (uintptr_t)w) & 15) == 0 && ((uintptr_t)q % cv) == 0;
+}
+
+hipError_t rk_launch_rms_quant(const void *x, const void *w, int8_t *q, float *qs, int64_t rows,
+                               int d, float eps, int dtype, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  switch (dtype) {
+    case RK_DTYPE_F32:
+      return w ? launch_rq_t<RK_DTYPE_F32, RK_DTYPE_F32>(x, w, q, qs, rows, d, eps, st)
+               : launch_rq_t<RK_DTYPE_F32, -1>(x, w, q, qs, rows, d, eps, st);
+    case RK_DTYPE_F16:
+      return w ? launch_rq_t<RK_DTYPE_F16, RK_DTYPE_F16>(x, w, q, qs, rows, d, eps, st)
+               : launch_rq_t<RK_DTYPE_F16, -1>(x, w, q, qs, rows, d, eps, st);
+    case RK_DTYPE_BF16:
+      return w ? launch_rq_t<RK_DTYPE_BF16, RK_DTYPE_BF16>(x, w, q, qs, rows, d, eps, st)
+               : launch_rq_t<RK_DTYPE_BF16, -1>(x, w, q, qs, rows, d, eps, st);
+  }
+  return hipErrorInvalidValue;
+}

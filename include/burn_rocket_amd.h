@@ -400,6 +400,17 @@ int rk_attention_qkv_dev(void *qkv, int64_t s, int64_t row_stride, int n_head, i
                          const void *cos, const void *sin, int cs_dtype, float scale,
                          float softcap, int mask_mode, int64_t window, int64_t q0, int64_t k0,
                          void *out, int64_t out_stride, rk_stream stream);
+/* RMSNorm then per-token int8 quantization in one pass, the activation input
+ * of a per-token W8A8 GEMM after a norm (the Qwen3 MLP: `post_attention_layernorm`
+ * through `burn_rocket::rms_norm` ext.rs:2112-2119, then `matmul` on an I8
+ * weight, whose host side quantizes each row, ext.rs:1017-1029 with
+ * quantize_row_groups host.rs:77-90): y = rk_rms_norm_dev's result in dtype
+ * (w NULL: scale-free; else w_dtype must equal dtype), then q_scale[row] =
+ * max(amax(y)/127, 1e-12) and q = round-half-away(y·(1/q_scale)) clamped to
+ * ±127, q int8 [rows, d]. RK_E_UNSUPPORTED unless d·sizeof(dtype) is a
+ * multiple of 16 and at most 8 KB and x and w are 16-byte aligned. */
+int rk_rms_norm_quantize_dev(const void *x, const void *w, int w_dtype, int64_t rows, int64_t d,
+                             double eps, int dtype, int8_t *q, float *q_scale, rk_stream stream);
 /* Host-buffer forms on f32 arrays (synchronous). */
 int rk_rms_norm(const float *x, const float *w, float *out, int64_t rows, int64_t d, double eps);
 int rk_rms_norm_noscale(const float *x, float *out, int64_t rows, int64_t d, double eps);

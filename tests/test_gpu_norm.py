@@ -551,3 +551,69 @@ def test_attention_qkv_equals_prologue_then_strided_attention(rk, orc, s, hq, hk
     (o0, b0), (o1, b1) = outs
     assert (b0.view(np.uint16) == b1.view(np.uint16)).all(), "the buffer after the prologue"
     assert (o0.view(np.uint16) == o1.view(np.uint16)).all(), "the attention output"
+
+
+def rms_quant_dev(rk, orc, x32, w32, dt, eps=1e-6):
+    x = _encode(orc, x32, dt)
+    rows, d = x.shape
+    dev = Dev(rk)
+    try:
+        px = dev.put(x)
+        pw = dev.put(_encode(orc, w32, dt)) if w32 is not None else None
+        pq = dev.put(np.zeros((rows, d), np.int8))
+        ps = dev.put(np.zeros(rows, np.float32))
+        rc = rk.lib().rk_rms_norm_quantize_dev(px, pw, _code(rk, dt), rows, d, eps, _code(rk, dt), pq, ps, None)
+        assert rc == 0, rk.lib().rk_last_error()
+        return dev.get(pq, np.zeros((rows, d), np.int8)), dev.get(ps, np.zeros(rows, np.float32)), x
+    finally:
+        dev.free()
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("rows,d", [(1, 32), (37, 64), (300, 1024), (9, 2048), (5, 4096)])
+def test_rms_norm_quantize_equals_the_two_ops(rk, orc, dt, rows, d):
+    if dt == "f32" and d > 2048:
+        pytest.skip("f32 rows above 2048 values are outside the fused kernel (RK_E_UNSUPPORTED)")
+    note(f"rms_norm_quantize {dt} rows={rows} d={d}")
+    r = np.random.default_rng(rows + d)
+    x32 = (r.standard_normal((rows, d)) * 3).astype(np.float32)
+    w32 = (1 + 0.3 * r.standard_normal(d)).astype(np.float32)
+    for w in (w32, None):
+        q, sc, x = rms_quant_dev(rk, orc, x32, w, dt)
+        # the separate device ops: rk_rms_norm_dev in dt, then rk_quantize_rows_dev per token
+        y, _ = rms_dev(rk, orc, _decode(orc, x, dt), w, 1e-6, dt)
+        dev = Dev(rk)
+        try:
+            py = dev.put(y.astype(np.float32))
+            pq, ps = dev.put(np.zeros((rows, d), np.int8)), dev.put(np.zeros(rows, np.float32))
+            assert rk.lib().rk_quantize_rows_dev(py, rows, d, d, pq, ps, None) == 0
+            q2, s2 = dev.get(pq, q), dev.get(ps, sc)
+        finally:
+            dev.free()
+        assert (q == q2).all() and (sc.view(np.uint32) == s2.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_rms_norm_quantize_exact_rows_match_the_oracle(rk, orc, dt):
+    rows, d = 70, 512
+    note(f"rms_norm_quantize vs oracle, integer rows, {dt}")
+    r = np.random.default_rng(9)
+    x32 = r.integers(-8, 9, (rows, d)).astype(np.float32)
+    w32 = (r.integers(-32, 33, d) / 16).astype(np.float32)
+    q, sc, x = rms_quant_dev(rk, orc, x32, w32, dt)
+    y = _decode(orc, _encode(orc, orc.rms_norm(_decode(orc, x, dt), _decode(orc, _encode(orc, w32, dt), dt), 1e-6), dt), dt)
+    qo, so = orc.quantize_rows(y, d)
+    assert (q == qo).all() and (sc == so[:, 0]).all()
+
+
+def test_rms_norm_quantize_rejects_what_it_does_not_fuse(rk):
+    note("rms_norm_quantize errors")
+    lib = rk.lib()
+    buf = rk.DeviceBuffer(1 << 16)
+    p = buf.ptr
+    f16 = rk.DTYPE_F16
+    assert lib.rk_rms_norm_quantize_dev(p, None, f16, 4, 12, 1e-6, f16, p, p, None) == rk.RK_E_UNSUPPORTED
+    assert lib.rk_rms_norm_quantize_dev(p, p, rk.DTYPE_F32, 4, 64, 1e-6, f16, p, p, None) == rk.RK_E_UNSUPPORTED
+    assert lib.rk_rms_norm_quantize_dev(p, None, f16, 2, 8192, 1e-6, f16, p, p, None) == rk.RK_E_UNSUPPORTED
+    assert lib.rk_rms_norm_quantize_dev(p, None, f16, 0, 64, 1e-6, f16, p, p, None) == 0
+    buf.free()
