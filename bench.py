@@ -357,6 +357,16 @@ def extra_glue(iters):
     rec("qk_norm_rope_f16_3633x4096", lambda: call(lib.rk_qk_norm_rope_dev(
         qkv.ptr, m, width, hq, hk, d, wq.ptr, wk.ptr, 1e-6, cs.ptr, sn.ptr, rk.DTYPE_F16, rk.DTYPE_F16, None),
         "qknr"), 2 * m * (hq + hk) * d * 2)
+    o16 = rk.DeviceBuffer(m * hq * d * 2)
+    ms = time_launches(lambda: call(lib.rk_attention_qkv_dev(
+        qkv.ptr, m, width, hq, hk, d, wq.ptr, wk.ptr, 1e-6, cs.ptr, sn.ptr, rk.DTYPE_F16, d ** -0.5, 0.0, 1, -1,
+        0, 0, o16.ptr, hq * d, None), "attention block"), iters)
+    fl = attn_flops(m, m, hq, d, True)
+    out["attention_block_qkv_3633"] = {"ms": ms, "tflops": fl / ms / 1e9, "frac_fp16_peak": fl / ms / 1e9 / PEAK_FP16}
+    q8, qs8 = rk.DeviceBuffer(m * hid), rk.DeviceBuffer(m * 4)
+    rec("rms_norm_quantize_f16_3633x1024", lambda: call(lib.rk_rms_norm_quantize_dev(
+        x16.ptr, w16.ptr, rk.DTYPE_F16, m, hid, 1e-6, rk.DTYPE_F16, q8.ptr, qs8.ptr, None), "rmsq"),
+        m * hid * 2 + m * hid + m * 4)
     n = m * inter
     a32, b32 = dev(r.standard_normal(n).astype(np.float32)), dev(r.standard_normal(n).astype(np.float32))
     o32 = rk.DeviceBuffer(n * 4)
