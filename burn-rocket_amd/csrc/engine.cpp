@@ -1250,30 +1250,34 @@ int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const f
 
 int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipStream_t st,
             float *act_out = nullptr) {
-  const int64_t H = w.hidden, I = w.inter, S = plan.s, R = plan.rows;
+  const int64_t H = w.hidden, I = w.inter, S = plan.s, R = std::max<int64_t>(plan.rows, 1);
+  const int64_t KBh = H / 32, KBi = I / 32;  // 32-value activation groups per row
   void *xq, *xs, *act, *aq, *as, *yb;
   RK_TRY(scratch("moe_xq", (size_t)S * H, &xq));
-  RK_TRY(scratch("moe_xs", (size_t)S * 4, &xs));
+  RK_TRY(scratch("moe_xs", (size_t)S * KBh * 4, &xs));
   if (act_out)
     act = act_out;
   else
-    RK_TRY(scratch("moe_act", (size_t)std::max<int64_t>(R, 1) * I * 4, &act));
-  RK_TRY(scratch("moe_aq", (size_t)std::max<int64_t>(R, 1) * I, &aq));
-  RK_TRY(scratch("moe_as", (size_t)std::max<int64_t>(R, 1) * 4, &as));
-  RK_TRY(scratch("moe_yb", (size_t)std::max<int64_t>(R, 1) * H * 4, &yb));
+    RK_TRY(scratch("moe_act", (size_t)R * I * 4, &act));
+  RK_TRY(scratch("moe_aq", (size_t)R * I, &aq));
+  RK_TRY(scratch("moe_as", (size_t)R * KBi * 4, &as));
+  RK_TRY(scratch("moe_yb", (size_t)R * H * 4, &yb));
   const char *op = "rk_moe_experts_dev";
-  HIP_TRY(rk_launch_quantize_rows(x, S, H, H, (int8_t *)xq, (float *)xs, st), op);
-  HIP_TRY(rk_launch_moe_gemm_gu((const int8_t *)xq, (const float *)xs, plan.tok, S, plan.tiles,
-                                plan.n_tiles, w.gu_codes, w.gu_scales, moe_gu_code_stride(w),
-                                2 * I * w.gu_ws_stride, w.gu_ws_stride, (int)(2 * I), (int)H,
-                                (float *)act, g_eng->num_cus, st),
+  // x and the silu·up rows are quantized per row per 32-value group, as the
+  // reference's expert workers do (engine.rs:1005-1006, 1034-1035).
+  HIP_TRY(rk_launch_quantize_rows(x, S, H, 32, (int8_t *)xq, (float *)xs, st), op);
+  HIP_TRY(rk_launch_moe_gemm_gu((const int8_t *)xq, (const float *)xs, (int)KBh, plan.tok, S,
+                                plan.tiles, plan.n_tiles, w.gu_codes, w.gu_scales,
+                                moe_gu_code_stride(w), 2 * I * w.gu_ws_stride, w.gu_ws_stride,
+                                (int)(2 * I), (int)H, (float *)act, g_eng->num_cus, st),
           op);
   if (!y) return RK_OK;  // stage 1 only
-  HIP_TRY(rk_launch_quantize_rows((const float *)act, R, I, I, (int8_t *)aq, (float *)as, st), op);
-  HIP_TRY(rk_launch_moe_gemm_down((const int8_t *)aq, (const float *)as, R, plan.tiles, plan.n_tiles,
-                                  w.dn_codes, w.dn_scales, moe_dn_code_stride(w), H * w.dn_ws_stride,
-                                  w.dn_ws_stride, (int)H, (int)I, plan.roww, (float *)yb,
-                                  g_eng->num_cus, st),
+  HIP_TRY(rk_launch_quantize_rows((const float *)act, plan.rows, I, 32, (int8_t *)aq, (float *)as, st),
+          op);
+  HIP_TRY(rk_launch_moe_gemm_down((const int8_t *)aq, (const float *)as, (int)KBi, plan.rows,
+                                  plan.tiles, plan.n_tiles, w.dn_codes, w.dn_scales,
+                                  moe_dn_code_stride(w), H * w.dn_ws_stride, w.dn_ws_stride, (int)H,
+                                  (int)I, plan.roww, (float *)yb, g_eng->num_cus, st),
           op);
   HIP_TRY(rk_launch_moe_combine((const float *)yb, plan.slot, S, plan.top_k, H, y, st), op);
   return RK_OK;
@@ -1284,6 +1288,10 @@ int moe_check(uint64_t id, int64_t s, int top_k, Weight **w, const char *op) {
   if (!*w || !(*w)->moe) return fail(RK_E_RANGE, op, "id is not an expert stack");
   if (s <= 0 || top_k <= 0 || top_k > (*w)->n_experts)
     return fail(RK_E_SHAPE, op, "need s > 0 and 0 < top_k <= n_experts");
+  // The expert kernels address the int8 activations (x [s, hidden], the
+  // quantized silu·up rows [s·top_k, inter]) with 32-bit byte offsets.
+  if (s * (*w)->hidden >= ((int64_t)1 << 31) || s * top_k * (*w)->inter >= ((int64_t)1 << 31))
+    return fail(RK_E_SHAPE, op, "s·hidden and s·top_k·inter must stay below 2^31");
   return RK_OK;
 }
 }  // namespace

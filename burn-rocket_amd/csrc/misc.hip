@@ -124,9 +124,42 @@ __global__ __launch_bounds__(256) void quantize_tokens_kernel(const float *__res
   }
 }
 
+// 32-value groups (K % 32 == 0): each lane quantizes 8 consecutive values, so
+// four neighbouring lanes hold one group (groups never straddle a row) and
+// the group maximum is two lane swaps. Same arithmetic as above.
+__global__ __launch_bounds__(256) void quantize_g32_kernel(const float *__restrict__ x, int64_t n8,
+                                                           int8_t *__restrict__ q,
+                                                           float *__restrict__ scale) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n8) return;  // n8 % 4 == 0: a group's four lanes leave together
+  const floatx4 a = ((const floatx4 *)x)[2 * t], b = ((const floatx4 *)x)[2 * t + 1];
+  float amax = fmaxf(fmaxf(fmaxf(fabsf(a[0]), fabsf(a[1])), fmaxf(fabsf(a[2]), fabsf(a[3]))),
+                     fmaxf(fmaxf(fabsf(b[0]), fabsf(b[1])), fmaxf(fabsf(b[2]), fabsf(b[3]))));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 4));
+  const float s = fmaxf(amax / 127.0f, 1e-12f);
+  const float inv = 1.0f / s;
+  if ((t & 3) == 0) scale[t >> 2] = s;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float c = roundf((e < 4 ? a[e] : b[e - 4]) * inv);
+    c = fminf(fmaxf(c, -127.0f), 127.0f);
+    w[e >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)c << (8 * (e & 3));
+  }
+  ((uintx2 *)q)[t] = uintx2{w[0], w[1]};
+}
+
 hipError_t rk_launch_quantize_rows(const float *x, int64_t m, int64_t k, int64_t group,
                                    int8_t *q, float *scale, hipStream_t st) {
   if (m <= 0) return hipSuccess;
+  if (group == 32 && k % 32 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 8) == 0 &&
+      ((uintptr_t)scale % 4) == 0) {
+    const int64_t n8 = m * k / 8;
+    hipLaunchKernelGGL(quantize_g32_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, x,
+                       n8, q, scale);
+    return hipGetLastError();
+  }
   if (group == k && k % 4 == 0 && k <= 4 * 64 * QTOK_MAX_VEC &&
       ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 4) == 0) {
     hipLaunchKernelGGL(quantize_tokens_kernel, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, st, x,

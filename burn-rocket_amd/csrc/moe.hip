@@ -2,9 +2,16 @@
 //
 // Stands in for the reference's expert workers (src/clef/engine_npu.rs:75-207:
 // gate|up matmul_gw, silu·up on the host, down matmul_gw, one expert per NPU
-// core) and the per-token combine (src/clef/engine.rs:317-338). Tokens are
-// bucketed per expert on the host (engine.rs:284-313); a tile table lists
-// (expert, first bucket row, rows ≤ 128) entries.
+// core; the exact host twin EmuWorker, src/clef/engine.rs:990-1043) and the
+// per-token combine (src/clef/engine.rs:317-338). Tokens are bucketed per
+// expert on the host (engine.rs:284-313); a tile table lists (expert, first
+// bucket row, rows ≤ 128) entries.
+//
+// Arithmetic (the reference's matmul_gw, src/clef/int8.rs:101-158): the
+// activations are quantized per row per 32-value group, the Q8_0 weights
+// carry one scale per 32-value block, and
+//   C[m, n] = Σ_b a_s[m, b] · w_s[n, b] · P_b[m, n],  P_b exact int32,
+// accumulated in f32 in block order.
 //
 // The expert GEMMs are HBM-bound: 128 experts of Q8_0 weights are read once
 // per call while each expert sees ~64 token rows. One workgroup takes one
@@ -19,67 +26,82 @@
 // and stage that keeps the HBM pipe full. The token rows of the tile, which
 // every wave reads, are gathered into a (PD+1)-slot LDS ring by buffer→LDS
 // copies with per-lane row offsets (16-byte chunks, swizzled by
-// (row >> 1) & 7); rows past the tile read as zeros.
+// (row >> 1) & 7), and next to them the rows' activation scales of the
+// stage's 4 blocks, stored [block][row]; rows past the tile read as zeros.
 //
-// One v_mfma_i32_32x32x32_i8 covers one Q8_0 block (exact int32); each
-// result is folded into an f32 accumulator with the block's f32 scale
-// (convert + FMA), and the MFMA of row block u+1 is issued before the fold
-// of row block u so the two overlap.
+// One v_mfma_i32_32x32x32_i8 covers one Q8_0 block. It starts from the int32
+// bits of 1.5·2^23 (0x4B400000), so its result read as a float is exactly
+// F = 1.5·2^23 + P (|P| <= 32·127² < 2^22): no int→float conversion.
+//   gate|up: acc = acc + fl(fl(a_s·d)·(F - 1.5·2^23)), the reference's own
+//            rounding sequence (its results are quantized again, where any
+//            difference could move a code);
+//   down:    two FMAs, y = fma(F, d, -1.5·2^23·d) = P·d rounded once (d = the
+//            f16 weight scale widened to f32, so 1.5·2^23·d is exact), then
+//            acc = fma(y, a_s, acc).
+// The MFMA of row block u+1 is issued before the fold of row block u so the
+// two overlap.
 //
 //   gate|up: weight rows are interleaved per 16-row slice t as
 //            [gate 16t..16t+15 | up 16t..16t+15], so the lane holding gate
 //            column j and the lane 16 above it holding up column j swap
 //            through ds_bpermute and the epilogue writes
-//            act = silu(xs·g) · (xs·u) (silu(x) = x / (1 + e^-x),
-//            src/clef/model.rs:491; computed as x·rcp(1 + e^-x), within
-//            2 ulp of the division).
-//   down:    yb[row] = (as·acc) · router weight of the row.
+//            act = silu(g) · u, silu(v) = v / (1 + e^-v) (src/clef/model.rs:
+//            491-493) with e^-v rounded once from f64 (exp_rn).
+//   down:    yb[row] = acc · router weight of the row (engine.rs:649-650).
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace {
-constexpr int MOE_BM = 128;  // rows per tile (the host lists tiles of ≤128 rows)
-constexpr int MOE_ROWB = 128;
+constexpr int MOE_BM = 128;    // rows per tile (the host lists tiles of ≤128 rows)
+constexpr int MOE_ROWB = 128;  // K bytes of one stage row
+constexpr int MOE_A_STAGE = MOE_BM * MOE_ROWB;  // token-row codes of one stage
+constexpr int MOE_S_STAGE = 4 * MOE_BM * 4;     // their scales, [block 0..3][row]
+constexpr int MOE_SLOT = MOE_A_STAGE + MOE_S_STAGE;
+constexpr int MOE_BIAS_BITS = 0x4B400000;  // 1.5·2^23 as f32 bits
+constexpr float MOE_BIAS = 12582912.0f;
 
-// LDS: the (PD+1)-slot ring of token-row stages, then the activation scale
-// and the router weight of each tile row.
+// LDS: the (PD+1)-slot ring of token-row stages with their scales, then the
+// router weight of each tile row.
 template <int PD>
 constexpr int moe_smem() {
-  return (PD + 1) * MOE_BM * MOE_ROWB + MOE_BM * 8;
+  return (PD + 1) * MOE_SLOT + MOE_BM * 4;
 }
 }  // namespace
 
+// e^x rounded once to f32: the f64 exponential (error well below half an f32
+// ulp) rounded to nearest. libm's expf, which the reference's f32::exp calls,
+// is correctly rounded on all but ~0.06 % of arguments, so silu·up matches it
+// bit for bit almost everywhere.
+__device__ __forceinline__ float exp_rn(float x) { return (float)exp((double)x); }
+
+__device__ __forceinline__ void bdma4(rsrc_t r, void *lds_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds_base), 4, voff, soff, 0, 0);
+}
+
 template <bool GU, int NW, int PD, int NRB>
 __device__ __forceinline__ void moe_body(
-    const int8_t *__restrict__ A, const float *__restrict__ AS, const int32_t *__restrict__ tok,
-    int64_t a_rows, const MoeTile &tile, const int8_t *__restrict__ We,
-    const float *__restrict__ WSe, int ws_stride, int N, int K, int n0,
-    const float *__restrict__ row_w, float *__restrict__ out, int out_ld, uint8_t *smem) {
+    const int8_t *__restrict__ A, const float *__restrict__ AS, int as_stride,
+    const int32_t *__restrict__ tok, int64_t a_rows, const MoeTile &tile,
+    const int8_t *__restrict__ We, const float *__restrict__ WSe, int ws_stride, int N, int K,
+    int n0, const float *__restrict__ row_w, float *__restrict__ out, int out_ld, uint8_t *smem) {
   constexpr int BM = MOE_BM, ROWB = MOE_ROWB, NSLOT = PD + 1;
-  constexpr int A_STAGE = BM * ROWB;
   constexpr int QA = BM / 8;     // 8-row copies of token rows per stage
   constexpr int CPA = QA / NW;   // of them per wave
-  constexpr int VM = CPA + 4 + 1;  // memory ops per wave and stage: A copies, 4 weight loads, scales
-  static_assert(CPA * NW == QA, "token-row copies per wave");
+  constexpr int SC = 8;          // 4-byte scale copies per stage: 4 blocks × 2 halves of 64 rows
+  constexpr int SPW = SC / NW;   // of them per wave
+  constexpr int VM = CPA + 4 + 1 + SPW;  // memory ops per wave and stage
+  static_assert(CPA * NW == QA && SPW * NW == SC, "copies per wave");
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KT = (K + 127) / 128;
   const int KB = K / 32;
 
-  // Row scales (and router weights) for the epilogue, loaded now (visible
-  // after the first stage's barrier) so the epilogue reads them from LDS.
-  float *s_rf = (float *)(smem + NSLOT * A_STAGE);
-  float *s_rw = s_rf + BM;
-  for (int row = threadIdx.x; row < BM; row += NW * 64) {
-    float f = 0.f, rw_ = 0.f;
-    if (row < tile.rows) {
-      const int br = tile.row0 + row;
-      f = GU ? AS[tok[br]] : AS[br];
-      if constexpr (!GU) rw_ = row_w[br];
-    }
-    s_rf[row] = f;
-    s_rw[row] = rw_;
+  // Router weights for the epilogue (visible after the first stage's barrier).
+  float *s_rw = (float *)(smem + NSLOT * MOE_SLOT);
+  if constexpr (!GU) {
+    for (int row = threadIdx.x; row < BM; row += NW * 64)
+      s_rw[row] = row < tile.rows ? row_w[tile.row0 + row] : 0.f;
   }
 
   // Expert weights are stored fragment-major: per 32-column block cb and
@@ -89,38 +111,55 @@ __device__ __forceinline__ void moe_body(
   const int KS = ws_stride / 4;  // stages per row (blocks padded to a multiple of 4)
   const int cb0 = n0 / 32, ncb = (N + 31) / 32;
   const rsrc_t ra = make_rsrc(A, a_rows * K);
+  const rsrc_t ras = make_rsrc(AS, a_rows * as_stride * 4);
   const rsrc_t rw = make_rsrc(We + (size_t)cb0 * KS * 4096, (int64_t)(ncb - cb0) * KS * 4096);
   const rsrc_t rs = make_rsrc(WSe + (size_t)cb0 * KS * 128, (int64_t)(ncb - cb0) * KS * 512);
 
   // Token-row copy q covers stage rows 8q..8q+7: lane → row 8q + lane/8,
   // physical chunk lane%8 holding logical chunk (lane%8) ^ ((row >> 1) & 7).
+  // Scale copy c covers block c%4 of rows 64·(c/4) + lane.
   const int r8 = lane >> 3, p8 = lane & 7;
+  auto src_row = [&](int row) -> int64_t {
+    if (row >= tile.rows) return -1;
+    return GU ? (int64_t)tok[tile.row0 + row] : (int64_t)(tile.row0 + row);
+  };
   uint32_t voff_a[CPA];
 #pragma unroll
   for (int i = 0; i < CPA; ++i) {
     const int q = wave + i * NW;
     const int row = 8 * q + r8;
     const uint32_t ch = (uint32_t)((p8 ^ ((row >> 1) & 7)) << 4);
-    int64_t src = -1;
-    if (row < tile.rows) src = GU ? (int64_t)tok[tile.row0 + row] : (int64_t)(tile.row0 + row);
+    const int64_t src = src_row(row);
     voff_a[i] = src >= 0 ? (uint32_t)(src * K) + ch : OOB_OFFSET;
+  }
+  uint32_t voff_as[SPW];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const int c = wave + i * NW;
+    const int64_t src = src_row(64 * (c >> 2) + lane);
+    voff_as[i] = src >= 0 ? (uint32_t)((src * as_stride + (c & 3)) * 4) : OOB_OFFSET;
   }
   const int fcol = lane & 31, fh = lane >> 5;
   const uint32_t voff_w = (uint32_t)(wave * KS * 4096 + lane * 16);
-  const uint32_t voff_s = (uint32_t)(wave * KS * 512 + fcol * 16);
+  const uint32_t voff_ws = (uint32_t)(wave * KS * 512 + fcol * 16);
 
   intx4 bq[NSLOT][4];
   floatx4 sq[NSLOT];
   auto issue = [&](auto slot_c, int kt) {
     constexpr int slot = decltype(slot_c)::value;
-    uint8_t *sb = smem + slot * A_STAGE;
+    uint8_t *sb = smem + slot * MOE_SLOT;
     const uint32_t k0 = kt * 128;
 #pragma unroll
     for (int i = 0; i < CPA; ++i) bdma16(ra, sb + (wave + i * NW) * 1024, voff_a[i], k0);
 #pragma unroll
     for (int b = 0; b < 4; ++b)
       bq[slot][b] = __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + 1024 * b, kt * 4096, 0);
-    sq[slot] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff_s, kt * 512, 0));
+    sq[slot] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff_ws, kt * 512, 0));
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      const int c = wave + i * NW;
+      bdma4(ras, sb + MOE_A_STAGE + (c & 3) * 512 + (c >> 2) * 256, voff_as[i], kt * 16);
+    }
   };
 
   const int swz = (fcol >> 1) & 7;
@@ -132,11 +171,27 @@ __device__ __forceinline__ void moe_body(
   auto load_afrag = [&](auto buf_c, auto slot_c, auto b_c) {
     constexpr int buf = decltype(buf_c)::value, slot = decltype(slot_c)::value,
                   b = decltype(b_c)::value;
-    const uint8_t *base = smem + slot * A_STAGE;
+    const uint8_t *base = smem + slot * MOE_SLOT;
 #pragma unroll
     for (int i = 0; i < NRB; ++i) af[buf][i] = *(const intx4 *)(base + a_off[b] + i * 32 * ROWB);
   };
+  // Activation scales of the lane's 16 rows of row block u for block b:
+  // rows 32u + 8q + 4·fh + j for register 4q + j.
+  auto load_as = [&](float(&v)[16], auto slot_c, auto b_c, auto u_c) {
+    constexpr int slot = decltype(slot_c)::value, b = decltype(b_c)::value,
+                  u = decltype(u_c)::value;
+    const float *p = (const float *)(smem + slot * MOE_SLOT + MOE_A_STAGE + b * 512) + u * 32 + fh * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const floatx4 t = *(const floatx4 *)(p + q * 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[4 * q + j] = t[j];
+    }
+  };
 
+  intx16 bias;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) bias[r] = MOE_BIAS_BITS;
   floatx16 facc[NRB];
 #pragma unroll
   for (int i = 0; i < NRB; ++i)
@@ -145,11 +200,34 @@ __device__ __forceinline__ void moe_body(
   intx16 ires[2];
 #pragma unroll
   for (int r = 0; r < 16; ++r) ires[0][r] = ires[1][r] = 0;
-  float dpend = 0.f;
-  auto fold = [&](auto p_c, auto i_c, float d) {
-    constexpr int P = decltype(p_c)::value, I = decltype(i_c)::value;
+  // The pending fold (the last row block of the previous block): its weight
+  // scale, bias correction and activation scales. Zero at the start, so the
+  // first pending fold adds nothing.
+  float dpend = 0.f, cpend = 0.f, asp[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) facc[I][r] = __builtin_fmaf((float)ires[P][r], d, facc[I][r]);
+  for (int r = 0; r < 16; ++r) asp[r] = 0.f;
+  auto fold = [&](auto p_c, auto i_c, float d, float c, const float(&as)[16]) {
+    constexpr int P = decltype(p_c)::value, I = decltype(i_c)::value;
+    if constexpr (GU) {
+      // The reference's rounding sequence, acc + fl(fl(a_s·w_s)·P): gate|up
+      // results feed the next quantizer, where a one-ulp difference could move
+      // an int8 code, so they are computed exactly as the reference does.
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int bits = ires[P][r];  // element to a scalar before the bit cast
+        const float pf = __int_as_float(bits) - MOE_BIAS;  // P, exact
+        const float sc = as[r] * d;
+        facc[I][r] = facc[I][r] + sc * pf;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int bits = ires[P][r];
+        const float y = __builtin_fmaf(__int_as_float(bits), d, c);
+        facc[I][r] = __builtin_fmaf(y, as[r], facc[I][r]);
+      }
+    }
   };
 
   // Row block u of block b (b = block index within its stage) uses result set
@@ -159,20 +237,27 @@ __device__ __forceinline__ void moe_body(
     constexpr int CUR = B & 1, NXT = CUR ^ 1;
     constexpr int P0 = (B * NRB) & 1;
     const float d = sq[S][B];
-    ires[P0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bq[S][B], intx16{}, 0, 0, 0);
+    const float c = -MOE_BIAS * d;
+    ires[P0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bq[S][B], bias, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (B < 3) load_afrag(ic<NXT>{}, ic<S>{}, ic<B + 1>{});
     __builtin_amdgcn_sched_barrier(0);
-    fold(ic<P0 ^ 1>{}, ic<NRB - 1>{}, dpend);
+    fold(ic<P0 ^ 1>{}, ic<NRB - 1>{}, dpend, cpend, asp);
     __builtin_amdgcn_sched_barrier(0);
     static_for<NRB - 1>([&](auto uc) {
       constexpr int u = decltype(uc)::value + 1;
-      ires[(P0 + u) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][u], bq[S][B], intx16{}, 0, 0, 0);
+      float asv[16];
+      load_as(asv, ic<S>{}, ic<B>{}, ic<u - 1>{});
+      ires[(P0 + u) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][u], bq[S][B], bias, 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      fold(ic<(P0 + u - 1) & 1>{}, ic<u - 1>{}, d);
+      fold(ic<(P0 + u - 1) & 1>{}, ic<u - 1>{}, d, c, asv);
       __builtin_amdgcn_sched_barrier(0);
     });
+    // The slot may be refilled before the pending fold runs: its scales go to
+    // registers now (the next stage's lgkmcnt wait covers these reads).
+    load_as(asp, ic<S>{}, ic<B>{}, ic<NRB - 1>{});
     dpend = d;
+    cpend = c;
   };
 
   // Stage kt is ready once at most `later` stages' memory ops (those issued
@@ -228,9 +313,9 @@ __device__ __forceinline__ void moe_body(
     });
   }
   if (((KB * NRB - 1) & 1) != 0)
-    fold(ic<1>{}, ic<NRB - 1>{}, dpend);
+    fold(ic<1>{}, ic<NRB - 1>{}, dpend, cpend, asp);
   else
-    fold(ic<0>{}, ic<NRB - 1>{}, dpend);
+    fold(ic<0>{}, ic<NRB - 1>{}, dpend, cpend, asp);
   WAIT_VMCNT(0);  // no copy may still be writing LDS when the workgroup ends
 
   // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of each 32-row
@@ -243,22 +328,20 @@ __device__ __forceinline__ void moe_body(
       // wave). For the row pair (r, r+1) the lower lanes finish row r and the
       // upper lanes row r+1: one swap across the 16-lane halves gives each
       // lane the gate and up values of its row, so every lane computes one
-      // output. silu(g)·u = g·u / (1 + e^-g).
+      // output.
       const bool lo = (fcol & 16) == 0;
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const int rr = lo ? r : r + 1;
         const int row = i * 32 + (rr >> 2) * 8 + fh * 4 + (rr & 3);
-        const float v0 = s_rf[i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3)] * facc[i][r];
-        const float v1 = s_rf[i * 32 + ((r + 1) >> 2) * 8 + fh * 4 + ((r + 1) & 3)] * facc[i][r + 1];
+        const float v0 = facc[i][r], v1 = facc[i][r + 1];
         // lower lanes send the gate of row r+1, upper lanes the up of row r
         const float x = __int_as_float(
             __builtin_amdgcn_ds_bpermute((lane ^ 16) << 2, __float_as_int(lo ? v1 : v0)));
         const float g = lo ? v0 : x, u = lo ? x : v1;
         if (row < tile.rows && col < N) {
           const int c = (n0 + wave * 32) / 2 + (fcol & 15);
-          out[(int64_t)(tile.row0 + row) * out_ld + c] =
-              g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+          out[(int64_t)(tile.row0 + row) * out_ld + c] = g / (1.0f + exp_rn(-g)) * u;
         }
       }
     } else {
@@ -266,7 +349,7 @@ __device__ __forceinline__ void moe_body(
       for (int r = 0; r < 16; ++r) {
         const int row = i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
         if (row < tile.rows && col < N)
-          out[(int64_t)(tile.row0 + row) * out_ld + col] = s_rf[row] * facc[i][r] * s_rw[row];
+          out[(int64_t)(tile.row0 + row) * out_ld + col] = facc[i][r] * s_rw[row];
       }
     }
   }
@@ -274,8 +357,8 @@ __device__ __forceinline__ void moe_body(
 
 template <bool GU, int NW, int PD>
 __global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
-    const int8_t *__restrict__ A, const float *__restrict__ AS, const int32_t *__restrict__ tok,
-    int64_t a_rows, const MoeTile *__restrict__ tiles, int n_col_tiles,
+    const int8_t *__restrict__ A, const float *__restrict__ AS, int as_stride,
+    const int32_t *__restrict__ tok, int64_t a_rows, const MoeTile *__restrict__ tiles, int n_col_tiles,
     const int8_t *__restrict__ W, const float *__restrict__ WS, int64_t w_stride_e,
     int64_t ws_stride_e, int ws_stride, int N, int K, const float *__restrict__ row_w,
     float *__restrict__ out, int out_ld) {
@@ -289,32 +372,32 @@ __global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
   const float *WSe = WS + (int64_t)tile.expert * ws_stride_e;
   switch ((tile.rows + 31) >> 5) {
     case 1:
-      moe_body<GU, NW, PD, 1>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
-                              out_ld, smem);
+      moe_body<GU, NW, PD, 1>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
+                              row_w, out, out_ld, smem);
       break;
     case 2:
-      moe_body<GU, NW, PD, 2>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
-                              out_ld, smem);
+      moe_body<GU, NW, PD, 2>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
+                              row_w, out, out_ld, smem);
       break;
     case 3:
-      moe_body<GU, NW, PD, 3>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
-                              out_ld, smem);
+      moe_body<GU, NW, PD, 3>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
+                              row_w, out, out_ld, smem);
       break;
     default:
-      moe_body<GU, NW, PD, 4>(A, AS, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0, row_w, out,
-                              out_ld, smem);
+      moe_body<GU, NW, PD, 4>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
+                              row_w, out, out_ld, smem);
       break;
   }
 }
 
 template <bool GU, int NW, int PD>
-static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, const int32_t *tok,
+static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, int as_stride, const int32_t *tok,
                                  int64_t a_rows, const MoeTile *tiles, int n_tiles,
                                  const int8_t *w, const float *ws, int64_t w_stride_e,
                                  int64_t ws_stride_e, int ws_stride, int N, int K,
                                  const float *row_w, float *out, int out_ld, hipStream_t st) {
   constexpr int smem = moe_smem<PD>();
-  static_assert(smem <= 80 * 1024 + MOE_BM * 8, "LDS per workgroup");
+  static_assert(smem <= 160 * 1024, "LDS per workgroup");
   auto kern = moe_q8_kernel<GU, NW, PD>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -324,54 +407,55 @@ static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, const int32_t
     attr_set = true;
   }
   const int n_col = (N + 32 * NW - 1) / (32 * NW);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(n_tiles * n_col)), dim3(NW * 64), smem, st, A, AS, tok,
-                     a_rows, tiles, n_col, w, ws, w_stride_e, ws_stride_e, ws_stride, N, K,
+  hipLaunchKernelGGL(kern, dim3((unsigned)(n_tiles * n_col)), dim3(NW * 64), smem, st, A, AS, as_stride,
+                     tok, a_rows, tiles, n_col, w, ws, w_stride_e, ws_stride_e, ws_stride, N, K,
                      row_w, out, out_ld);
   return hipGetLastError();
 }
 
 // Workgroup shapes (RK_MOE_TILE): 0 = 4 waves × 128 columns, weights 2
 // stages ahead (two workgroups per CU); 1 = 8 waves × 256 columns, 3 ahead;
-// 2 = 4 waves, 3 ahead; 3 = 4 waves, 4 ahead.
+// 2 = 4 waves, 3 ahead; 3 = 4 waves, 4 ahead (one workgroup per CU by LDS).
 template <bool GU>
-static hipError_t launch_moe(const int8_t *A, const float *AS, const int32_t *tok, int64_t a_rows,
+static hipError_t launch_moe(const int8_t *A, const float *AS, int as_stride, const int32_t *tok,
+                             int64_t a_rows,
                              const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
                              int64_t w_stride_e, int64_t ws_stride_e, int ws_stride, int N,
                              int K, const float *row_w, float *out, int out_ld, hipStream_t st) {
   if (n_tiles == 0) return hipSuccess;
   switch (rk_knob("RK_MOE_TILE", 0)) {
     case 1:
-      return launch_moe_cfg<GU, 8, 3>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+      return launch_moe_cfg<GU, 8, 3>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
                                       ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
     case 2:
-      return launch_moe_cfg<GU, 4, 3>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+      return launch_moe_cfg<GU, 4, 3>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
                                       ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
     case 3:
-      return launch_moe_cfg<GU, 4, 4>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+      return launch_moe_cfg<GU, 4, 4>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
                                       ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
     default:
-      return launch_moe_cfg<GU, 4, 2>(A, AS, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
+      return launch_moe_cfg<GU, 4, 2>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
                                       ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
   }
 }
 
-hipError_t rk_launch_moe_gemm_gu(const int8_t *xq, const float *xs, const int32_t *tok,
-                                 int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
+hipError_t rk_launch_moe_gemm_gu(const int8_t *xq, const float *xs, int xs_stride,
+                                 const int32_t *tok, int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
                                  const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                  int ws_stride, int N, int K, float *act, int num_cus,
                                  hipStream_t st) {
   (void)num_cus;
-  return launch_moe<true>(xq, xs, tok, s, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
+  return launch_moe<true>(xq, xs, xs_stride, tok, s, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
                           ws_stride, N, K, nullptr, act, N / 2, st);
 }
 
-hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, int64_t rows,
+hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, int as_stride, int64_t rows,
                                    const MoeTile *tiles, int n_tiles, const int8_t *w,
                                    const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                    int ws_stride, int N, int K, const float *row_w, float *yb,
                                    int num_cus, hipStream_t st) {
   (void)num_cus;
-  return launch_moe<false>(aq, as, nullptr, rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
+  return launch_moe<false>(aq, as, as_stride, nullptr, rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
                            ws_stride, N, K, row_w, yb, N, st);
 }
 

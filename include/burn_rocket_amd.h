@@ -283,10 +283,16 @@ int rk_pack_moe_f32(const float *gate, const float *up, const float *down,
 /* Expert FFN over routed tokens on device buffers: per token t and slot j,
  * y[t] += wts[t,j] · down(silu(gate(x_t)) ⊙ up(x_t)) of expert ids[t,j], the
  * slots summed in ascending expert id (combine, src/clef/engine.rs:317-338;
- * layer_forward_multi, src/clef/model.rs:526-620). x f32 [s, hidden] is
- * quantized per token; the gate|up product is quantized per row before down.
- * ids/wts are host arrays (bucketing runs on the host, engine.rs:284-313);
- * y f32 [s, hidden] is overwritten. */
+ * layer_forward_multi, src/clef/model.rs:526-620), with the W8A8 arithmetic
+ * of the reference's expert workers (EmuWorker::run, src/clef/engine.rs:
+ * 990-1043; NpuWorker/gw_matmul, src/clef/engine_npu.rs:75-207): x f32
+ * [s, hidden] and the silu·up rows are each quantized per row per 32-value
+ * group (scale max(amax/127, 1e-12), round-half-away, ±127), and every
+ * product is Σ_b (a_s[m,b]·w_s[n,b])·P_b over the Q8_0 blocks b with exact
+ * int32 P_b, accumulated in f32. silu(v) = v / (1 + e^-v) (src/clef/model.rs:
+ * 491-493). ids/wts are host arrays (bucketing runs on the host,
+ * engine.rs:284-313); y f32 [s, hidden] is overwritten. RK_E_SHAPE when
+ * s·hidden or s·top_k·inter reaches 2^31. */
 int rk_moe_experts_dev(rk_weight_id id, const float *x, int64_t s, int top_k,
                        const uint32_t *ids, const float *wts, float *y,
                        rk_stream stream);

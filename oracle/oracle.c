@@ -501,24 +501,38 @@ void orc_route(const float *logits, int64_t s, int n_experts, int top_k, int nor
   free(used);
 }
 
-static inline float silu(float x) { return x / (1.0f + expf(-x)); } /* model.rs:491 */
+static inline float silu(float x) { return x / (1.0f + expf(-x)); } /* model.rs:491-493 */
 
-/* W8A8 expert FFN over routed tokens (layer_forward_multi's MoE block,
- * src/clef/model.rs:562-620, with the NPU workers' int8 path,
- * src/clef/engine_npu.rs:149-207): per token the hidden row is quantized per
- * token, each selected expert computes g = gate·x, u = up·x with the
- * emu_matmul_gw formula against Q8_0 codes/scales, act = silu(g)·u,
- * quantized per row, y_e = down·act scaled by the router weight, and the
- * token's outputs are summed in ascending expert id (combine,
- * src/clef/engine.rs:317-338). Weights: gate/up codes [E][I][H] with scales
- * [E][I][H/32], down codes [E][H][I] with scales [E][H][I/32]. y [s][H]. */
+/* out = silu(g)·u with Clef's silu (src/clef/model.rs:491-493, used by the
+ * expert workers, src/clef/engine.rs:1025-1029), in f32 with libm's expf. */
+void orc_clef_silu_mul(const float *g, const float *u, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = silu(g[i]) * u[i];
+}
+
+/* W8A8 expert FFN over routed tokens, as the reference's host twin of the NPU
+ * expert worker computes it (EmuWorker::run, src/clef/engine.rs:990-1043; the
+ * NPU worker gw_matmul → quantize_rows(x, k, group), src/clef/engine_npu.rs:
+ * 75-110, 149-207). With the Q8_0 group g = 32 of the expert weights:
+ *   xq, xs  = x quantized per row per 32-value group (quantize_rows, int8.rs:
+ *             18-57), xs [s][H/32];
+ *   g, u    = emu_matmul_gw(xq, xs, gate / up codes and scales, group 32)
+ *             (int8.rs:101-158: Σ_b (xs[b]·w_s[n][b])·P_b in block order);
+ *   act     = silu(g)·u with silu(v) = v / (1 + exp(-v)) (model.rs:491-493);
+ *   aq, as  = act quantized per row per 32-value group;
+ *   y_e     = emu_matmul_gw(aq, as, down codes and scales, group 32), each
+ *             element then multiplied by the router weight (engine.rs:649-650);
+ * and each token's expert outputs are summed in ascending expert id (combine,
+ * src/clef/engine.rs:317-338). A token's row is quantized the same way in
+ * every expert it is routed to, so quantizing x once per token is the same.
+ * Weights: gate/up codes [E][I][H] with scales [E][I][H/32], down codes
+ * [E][H][I] with scales [E][H][I/32]. y [s][H]. */
 void orc_moe_experts(const float *x, int64_t s, int64_t H, int64_t I, int E, int top_k,
                      const uint32_t *ids, const float *wts, const int8_t *gq, const float *gs,
                      const int8_t *uq, const float *us, const int8_t *dq, const float *ds,
                      float *y, int threads) {
   int8_t *xq = (int8_t *)malloc((size_t)s * H);
-  float *xs = (float *)malloc(sizeof(float) * (size_t)s);
-  orc_quantize_rows(x, s, H, H, xq, xs, threads);
+  float *xs = (float *)malloc(sizeof(float) * (size_t)s * (H / 32));
+  orc_quantize_rows(x, s, H, 32, xq, xs, threads);
   float *yslot = (float *)malloc(sizeof(float) * (size_t)s * top_k * H);
 #pragma omp parallel num_threads(threads)
   {
@@ -526,23 +540,26 @@ void orc_moe_experts(const float *x, int64_t s, int64_t H, int64_t I, int E, int
     float *u = (float *)malloc(sizeof(float) * (size_t)I);
     float *act = (float *)malloc(sizeof(float) * (size_t)I);
     int8_t *aq = (int8_t *)malloc((size_t)I);
+    float *as = (float *)malloc(sizeof(float) * (size_t)(I / 32));
 #pragma omp for schedule(dynamic, 4)
     for (int64_t slot = 0; slot < s * top_k; ++slot) {
       const int64_t t = slot / top_k;
       const int e = (int)ids[slot];
-      float as;
-      orc_emu_matmul_gw(xq + t * H, xs + t, H, 1, H, gq + (int64_t)e * I * H, gs + (int64_t)e * I * (H / 32), 32, I, g, 1);
-      orc_emu_matmul_gw(xq + t * H, xs + t, H, 1, H, uq + (int64_t)e * I * H, us + (int64_t)e * I * (H / 32), 32, I, u, 1);
+      const int8_t *xr = xq + t * H;
+      const float *xsr = xs + t * (H / 32);
+      orc_emu_matmul_gw(xr, xsr, 32, 1, H, gq + (int64_t)e * I * H, gs + (int64_t)e * I * (H / 32), 32, I, g, 1);
+      orc_emu_matmul_gw(xr, xsr, 32, 1, H, uq + (int64_t)e * I * H, us + (int64_t)e * I * (H / 32), 32, I, u, 1);
       for (int64_t j = 0; j < I; ++j) act[j] = silu(g[j]) * u[j];
-      orc_quantize_row_groups(act, I, I, aq, &as);
+      orc_quantize_row_groups(act, I, 32, aq, as);
       float *yr = yslot + slot * H;
-      orc_emu_matmul_gw(aq, &as, I, 1, I, dq + (int64_t)e * H * I, ds + (int64_t)e * H * (I / 32), 32, H, yr, 1);
+      orc_emu_matmul_gw(aq, as, 32, 1, I, dq + (int64_t)e * H * I, ds + (int64_t)e * H * (I / 32), 32, H, yr, 1);
       for (int64_t c = 0; c < H; ++c) yr[c] *= wts[slot];
     }
     free(g);
     free(u);
     free(act);
     free(aq);
+    free(as);
   }
   /* combine: per token, slots in ascending expert id */
 #pragma omp parallel for num_threads(threads) schedule(static)

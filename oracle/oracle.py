@@ -39,6 +39,7 @@ _SIG = {
     "orc_gelu_tanh": (_f, [_f]),
     "orc_gelu_mul": (None, [_p, _p, _p, _i64]),
     "orc_silu_mul": (None, [_p, _p, _p, _i64]),
+    "orc_clef_silu_mul": (None, [_p, _p, _p, _i64]),
     "orc_rms_norm": (None, [_p, _p, _p, _i64, _i64, _c.c_float]),
     "orc_rope": (None, [_p, _p, _p, _p, _i64, _i64, _i64, _i64]),
     "orc_max_threads": (_i, []),
@@ -237,8 +238,9 @@ def route(logits, top_k, norm_topk=True):
 
 
 def moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds, threads=None):
-    """W8A8 expert FFN + combine. gq/uq [E,I,H] int8, gs/us [E,I,H/32] f32,
-    dq [E,H,I] int8, ds [E,H,I/32] f32 → y [s,H] f32."""
+    """W8A8 expert FFN + combine, activations (x and silu·up) quantized per row
+    per 32-value group as the reference's expert workers do. gq/uq [E,I,H]
+    int8, gs/us [E,I,H/32] f32, dq [E,H,I] int8, ds [E,H,I/32] f32 → y [s,H]."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     s, H = x.shape
     E, I = gq.shape[0], gq.shape[1]
@@ -287,6 +289,12 @@ def _glue(fn, gate, up):
 def silu_mul(gate, up):
     """silu(gate)·up in f32 (host.rs:30-39)."""
     return _glue(lib().orc_silu_mul, gate, up)
+
+
+def clef_silu_mul(gate, up):
+    """silu(gate)·up with Clef's silu v / (1 + e^-v) in f32, libm expf
+    (src/clef/model.rs:491-493): the MoE expert activation."""
+    return _glue(lib().orc_clef_silu_mul, gate, up)
 
 
 def gelu_mul(gate, up):

@@ -13,8 +13,8 @@ by tests/golden/make_clef_mini.py). This test restates that layer in numpy
   1e-5 (the reference test's bounds), from logits the numpy layer computes;
 * the layer output, with the expert FFN and the ascending-expert-id combine,
   must match the golden hidden states to 2e-6 of the peak (the reference's
-  bound); orc.moe_experts, the W8A8 (Q8_0 weights, per-token int8
-  activations) restatement of that FFN + combine, must stay within the
+  bound); orc.moe_experts, the W8A8 (Q8_0 weights, int8 activations per
+  32-value group) restatement of that FFN + combine, must stay within the
   quantization error of it (cosine >= 0.9999 on the layer output).
 """
 import json

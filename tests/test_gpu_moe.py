@@ -1,6 +1,9 @@
 """GPU parity of the MoE expert pipeline (K4: grouped W8A8 GEMMs over per-expert
 token lists, silu·up, down, combine) against the oracle.
 
+Both activations (x and silu(g)·u) are quantized per row per 32-value group,
+as the reference's expert workers do (src/clef/engine.rs:990-1043).
+
 The pipeline re-quantizes the intermediate activation to int8, so an f32
 rounding-order difference in stage 1 can move an activation across a code
 boundary and change one int8 code; that is a property of the two-stage W8A8
@@ -8,7 +11,7 @@ algorithm, not of the kernels. Each stage is therefore pinned separately:
 stage 1 (gate|up, silu·up) against the oracle within f32 rounding, and stages
 2-3 (re-quantize, down, router weight, combine) against the oracle fed with the
 GPU's own stage-1 output, within f32 rounding and the fp16-output gate. The end
-to end result is held to cosine >= 0.9999."""
+to end result is held to the gates: cosine >= 0.9999 and max-rel <= 1e-2."""
 import ctypes
 import sys
 
@@ -88,31 +91,41 @@ def rk_inter(rk, wid):
 
 
 def oracle_stage1(orc, x, ex, e_rows, t_rows):
-    H = x.shape[1]
-    xq, xs = orc.quantize_rows(x, H)
+    """silu(gate·x)·(up·x) of the bucket rows (e_rows, t_rows), x quantized per 32-group."""
+    xq, xs = orc.quantize_rows(x, 32)
     I = ex["gq"].shape[1]
     act = np.empty((len(e_rows), I), np.float32)
     for e in np.unique(e_rows):
         sel = np.nonzero(e_rows == e)[0]
         t = t_rows[sel]
-        g = orc.emu_matmul_gw(xq[t], xs[t], H, ex["gq"][e], ex["gs"][e], 32)
-        u = orc.emu_matmul_gw(xq[t], xs[t], H, ex["uq"][e], ex["us"][e], 32)
-        act[sel] = g / (np.float32(1) + np.exp(-g)) * u
+        g = orc.emu_matmul_gw(xq[t], xs[t], 32, ex["gq"][e], ex["gs"][e], 32)
+        u = orc.emu_matmul_gw(xq[t], xs[t], 32, ex["uq"][e], ex["us"][e], 32)
+        act[sel] = orc.clef_silu_mul(g, u)
     return act
 
 
 def oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S):
-    I = act.shape[1]
+    """Down projection of the given act rows (quantized per 32-group), router weight, combine."""
     H = ex["dq"].shape[1]
-    aq, a_s = orc.quantize_rows(act, I)
+    aq, a_s = orc.quantize_rows(act, 32)
     yb = np.empty((len(e_rows), H), np.float32)
     for e in np.unique(e_rows):
         sel = np.nonzero(e_rows == e)[0]
-        yb[sel] = orc.emu_matmul_gw(aq[sel], a_s[sel], I, ex["dq"][e], ex["ds"][e], 32) * w_rows[sel][:, None]
+        yb[sel] = orc.emu_matmul_gw(aq[sel], a_s[sel], 32, ex["dq"][e], ex["ds"][e], 32) * w_rows[sel][:, None]
     y = np.zeros((S, H), np.float32)
     for row in range(len(e_rows)):  # bucket rows are expert-ascending: the combine order
         y[t_rows[row]] += yb[row]
     return y
+
+
+def check_stage1(act, act_ref):
+    """GPU silu·up against the oracle's: equal bits except where libm's expf
+    (the oracle's, as the reference's f32::exp) is not correctly rounded
+    (~0.06 % of arguments), and there within f32 rounding."""
+    differ = (act.view(np.uint32) != act_ref.view(np.uint32)).mean()
+    note(f"stage 1: {differ:.2e} of the values differ from the oracle's bits")
+    assert differ <= 2e-3
+    assert np.abs(act - act_ref).max() <= 2e-6 * np.abs(act_ref).max()
 
 
 def check_pipeline(rk, orc, S, H, I, E, ids, wts, seed):
@@ -123,16 +136,17 @@ def check_pipeline(rk, orc, S, H, I, E, ids, wts, seed):
     act, y = run(rk, wid, x, ids, wts)
     e_rows, t_rows, s_rows = bucket_order(ids)
     w_rows = wts[t_rows, s_rows]
-    # stage 1 within f32 rounding
+    # stage 1: the reference's rounding sequence, so bit-equal but for the
+    # rare arguments where libm's expf is not correctly rounded
     act_ref = oracle_stage1(orc, x, ex, e_rows, t_rows)
-    assert np.abs(act - act_ref).max() <= 2e-5 * np.abs(act_ref).max()
+    check_stage1(act, act_ref)
     # stages 2-3 from the GPU's own activations: f32 rounding only
     y_ref2 = oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S)
     assert np.abs(y - y_ref2).max() <= 2e-5 * np.abs(y_ref2).max()
     assert orc.cosine(y, y_ref2) >= COS_MIN and orc.max_rel(y, y_ref2) <= REL_MAX
     # end to end against the full oracle pipeline
     y_ref = orc.moe_experts(x, ids, wts, ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"])
-    assert orc.cosine(y, y_ref) >= COS_MIN
+    assert orc.cosine(y, y_ref) >= COS_MIN and orc.max_rel(y, y_ref) <= REL_MAX
     return y
 
 
@@ -161,6 +175,55 @@ def test_moe_config5_shapes_on_16_experts(rk, orc):
     note(f"MoE config5 shapes S={S} H={H} I={I} E={E} top{K}")
     ids, wts = rk.moe_route(synth.normal_f32(synth.SEEDS["moe"][1], (S, E)), K)
     check_pipeline(rk, orc, S, H, I, E, ids, wts, synth.SEEDS["moe"][2])
+
+
+def random_q8_experts(seed, E, H, I):
+    """A Q8_0 expert stack drawn directly as codes and block scales: int8 codes
+    uniform in [-127, 127] (the widest int32 block sums) and f16 scales of the
+    size N(0, 0.02²) weights give (~amax/127). Drawing normals and quantizing
+    600 M weights on the host would take most of a minute."""
+    r = np.random.default_rng(seed)
+    ex = {}
+    for name, shp in (("g", (E, I, H)), ("u", (E, I, H)), ("d", (E, H, I))):
+        q = r.bit_generator.random_raw(int(np.prod(shp)) // 8).view(np.int8).reshape(shp)
+        np.maximum(q, -127, out=q)
+        d16 = r.uniform(2.5e-4, 4.5e-4, shp[:-1] + (shp[-1] // 32,)).astype(np.float16)
+        blocks = np.empty(q.size // 32 * 34, np.uint8).reshape(-1, 34)
+        blocks[:, :2] = d16.reshape(-1, 1).view(np.uint8)
+        blocks[:, 2:] = q.reshape(-1, 32).view(np.uint8)
+        ex[name + "q"], ex[name + "s"], ex[name + "b"] = q, d16.astype(np.float32), blocks.reshape(-1)
+    return dict(gq=ex["gq"], gs=ex["gs"], uq=ex["uq"], us=ex["us"], dq=ex["dq"], ds=ex["ds"],
+                blocks=[ex["gb"], ex["ub"], ex["db"]])
+
+
+def test_moe_config5_full_size(rk, orc):
+    # Config 5 as benched: 1024 tokens, 128 resident experts (hidden 2048,
+    # inter 768), top-8 of a softmax over 128 seeded router logits. The GPU
+    # runs every token; 64 tokens spread over the sequence are checked end to
+    # end against the oracle (tokens are independent), and stage 1 of every
+    # bucket row of those tokens within f32 rounding.
+    c = synth.MOE
+    S, H, I, E, K = c["s"], c["hidden"], c["inter"], c["experts"], c["top_k"]
+    note(f"MoE config5 full size S={S} H={H} I={I} E={E} top{K}: building the stack")
+    ex = random_q8_experts(5150, E, H, I)
+    wid = rk.pack_moe_q8_0(*ex["blocks"], E, H, I)
+    del ex["blocks"]
+    _INTER[int(wid)] = I
+    seeds = synth.SEEDS["moe"]
+    x = synth.normal_f32(seeds[0], (S, H))
+    ids, wts = rk.moe_route(synth.normal_f32(seeds[1], (S, E)), K)
+    note("MoE config5 full size: running")
+    act, y = run(rk, wid, x, ids, wts)
+    e_rows, t_rows, s_rows = bucket_order(ids)
+    toks = np.linspace(0, S - 1, 64).round().astype(np.int64)
+    assert len(np.unique(ids[toks])) > 100  # the checked tokens reach most experts
+    rows = np.nonzero(np.isin(t_rows, toks))[0]
+    act_ref = oracle_stage1(orc, x, ex, e_rows[rows], t_rows[rows])
+    check_stage1(act[rows], act_ref)
+    y_ref = orc.moe_experts(x[toks], ids[toks], wts[toks], ex["gq"], ex["gs"], ex["uq"], ex["us"],
+                            ex["dq"], ex["ds"])
+    note(f"MoE config5: cosine {orc.cosine(y[toks], y_ref):.7f} max-rel {orc.max_rel(y[toks], y_ref):.2e}")
+    assert orc.cosine(y[toks], y_ref) >= COS_MIN and orc.max_rel(y[toks], y_ref) <= REL_MAX
 
 
 def test_pack_moe_f32_equals_pack_from_blocks(rk, orc):
