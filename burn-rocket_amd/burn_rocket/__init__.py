@@ -97,6 +97,8 @@ SIGNATURES = {
     "rk_memset_dev": (_i, [_p, _i, _sz]),
     "rk_stream_get": (_i, [_p]),
     "rk_stream_sync": (_i, [_p]),
+    "rk_stream_create": (_i, [_p]),
+    "rk_stream_destroy": (_i, [_p]),
     "rk_event_create": (_i, [_p]),
     "rk_event_destroy": (_i, [_p]),
     "rk_event_record": (_i, [_p, _p]),
@@ -462,17 +464,21 @@ def attention_causal_block_window(q, k, v, n_head, n_kv_heads, head_dim, scale, 
 
 
 def flash_attn_f16(q, k, v, n_q, n_kv, head_dim, n_head, n_kv_heads, scale, softcap=0.0, mode=MASK_NONE,
-                   window=-1, q0=0, k0=0):
-    """Head-major fp16 attention (`RocketFaCtx::flash_attn` layout, lib.rs:294-323):
-    q [H][n_q][D], k [KV][n_kv][D], v [KV][D][n_kv] → out [H][n_q][D] (fp16)."""
+                   window=-1, q0=0, k0=0, dv=None):
+    """Head-major fp16 attention (`RocketFaCtx::flash_attn`, lib.rs:294-323):
+    q [H][n_q][head_dim], k [KV][n_kv][head_dim], v [KV][dv][n_kv] →
+    out [H][n_q][dv] (fp16); dv defaults to head_dim."""
+    dv = head_dim if dv is None else dv
     q16 = np.ascontiguousarray(q, dtype=np.float16).view(np.uint16)
     k16 = np.ascontiguousarray(k, dtype=np.float16).view(np.uint16)
     v16 = np.ascontiguousarray(v, dtype=np.float16).view(np.uint16)
-    out = np.empty(n_head * n_q * head_dim, dtype=np.uint16)
-    _check(_lib.rk_flash_attn_f16(n_q, n_kv, head_dim, head_dim, n_head, n_kv_heads, float(scale),
+    assert q16.size >= n_head * n_q * head_dim and k16.size >= n_kv_heads * n_kv * head_dim, "flash_attn/buffers"
+    assert v16.size >= n_kv_heads * dv * n_kv, "flash_attn/buffers"
+    out = np.empty(n_head * n_q * dv, dtype=np.uint16)
+    _check(_lib.rk_flash_attn_f16(n_q, n_kv, head_dim, dv, n_head, n_kv_heads, float(scale),
                                   float(softcap), mode, window, q0, k0, _ptr(q16), _ptr(k16), _ptr(v16),
                                   _ptr(out)), "rocket_flash_attn_fp16_ctx", n_q, n_kv, head_dim)
-    return out.view(np.float16).reshape(n_head, n_q, head_dim)
+    return out.view(np.float16).reshape(n_head, n_q, dv)
 
 
 def moe_route(logits, top_k, norm_topk=True):
@@ -506,6 +512,8 @@ def pack_moe_f32(gate, up, down):
 
 
 class Stats(ctypes.Structure):
+    """`burn_rocket::Stats` (ext.rs:175-183): conversion and device seconds of the
+    host-buffer ops, and the matmul / attention / MoE call count."""
     _fields_ = [("convert_s", ctypes.c_double), ("npu_s", ctypes.c_double), ("calls", ctypes.c_uint64)]
 
 
@@ -585,6 +593,17 @@ def stream():
     s = ctypes.c_void_p()
     _check(_lib.rk_stream_get(ctypes.byref(s)), "stream_get")
     return s.value
+
+
+def new_stream():
+    """A new HIP stream (default priority) owned by the caller; free with destroy_stream."""
+    s = ctypes.c_void_p()
+    _check(_lib.rk_stream_create(ctypes.byref(s)), "stream_create")
+    return s.value
+
+
+def destroy_stream(st):
+    _check(_lib.rk_stream_destroy(ctypes.c_void_p(st)), "stream_destroy")
 
 
 def synchronize(st=None):

@@ -63,9 +63,15 @@ int hip_fail(hipError_t e, const char *op) {
     if (rc_ != RK_OK) return rc_; \
   } while (0)
 
+// A named device scratch buffer. `ev` is recorded on the calling stream after
+// the work of every call that used the buffer, so a call on another stream
+// first waits for it, and the buffer is freed only once it has completed.
 struct DevBuf {
   void *p = nullptr;
   size_t bytes = 0;
+  hipEvent_t ev = nullptr;
+  hipStream_t ev_stream = nullptr;  // where ev was last recorded
+  bool recorded = false;
 };
 
 struct Weight {
@@ -95,6 +101,7 @@ struct Engine {
   std::unordered_map<std::string, DevBuf> scratch;
   double convert_s = 0, device_s = 0;
   uint64_t calls = 0;
+  hipEvent_t tev[4] = {};  // HostTimer marks
 };
 
 std::mutex g_mu;
@@ -111,23 +118,63 @@ int ensure(const char *op) {
   return RK_OK;
 }
 
-// Grow-only named device scratch.
-int scratch(const char *name, size_t bytes, void **out) {
+// The stream of one entry-point call and the scratch buffers it took: when the
+// call returns (its work is enqueued) each buffer's event is recorded on that
+// stream.
+struct CallScope {
+  hipStream_t st;
+  std::vector<DevBuf *> used;
+  explicit CallScope(hipStream_t s) : st(s) {}
+  CallScope(const CallScope &) = delete;
+  CallScope &operator=(const CallScope &) = delete;
+  ~CallScope() {
+    for (DevBuf *b : used)
+      if (hipEventRecord(b->ev, st) == hipSuccess) {
+        b->recorded = true;
+        b->ev_stream = st;
+      }
+  }
+};
+
+// Grow-only named device scratch, ordered after its last use on any stream.
+int scratch(CallScope &c, const char *name, size_t bytes, void **out) {
   DevBuf &b = g_eng->scratch[name];
+  if (!b.ev) HIP_TRY(hipEventCreateWithFlags(&b.ev, hipEventDisableTiming), "scratch");
   if (b.bytes < bytes) {
     if (b.p) {
-      HIP_TRY(hipStreamSynchronize(g_eng->stream), "scratch");
+      if (b.recorded) HIP_TRY(hipEventSynchronize(b.ev), "scratch");
       HIP_TRY(hipFree(b.p), "scratch");
     }
     b.p = nullptr;
     b.bytes = 0;
+    b.recorded = false;
     const size_t want = std::max<size_t>(bytes, 256);
     HIP_TRY(hipMalloc(&b.p, want), "scratch");
     b.bytes = want;
+  } else if (b.recorded && b.ev_stream != c.st) {
+    HIP_TRY(hipStreamWaitEvent(c.st, b.ev, 0), "scratch");
   }
+  if (std::find(c.used.begin(), c.used.end(), &b) == c.used.end()) c.used.push_back(&b);
   *out = b.p;
   return RK_OK;
 }
+
+// Conversion / device time of a host-buffer entry point, from four events on
+// its stream: [0, 1) uploads and conversions in, [1, 2) the kernels of the op,
+// [2, 3) conversions out and downloads (the split of `T_CONVERT_US` /
+// `T_NPU_US`, ext.rs:165-200). finish() runs after the stream has synchronized.
+struct HostTimer {
+  hipStream_t st;
+  explicit HostTimer(hipStream_t s) : st(s) {}
+  void mark(int i) { (void)hipEventRecord(g_eng->tev[i], st); }
+  void finish() {
+    float t[3] = {0.f, 0.f, 0.f};
+    for (int i = 0; i < 3; ++i)
+      if (hipEventElapsedTime(&t[i], g_eng->tev[i], g_eng->tev[i + 1]) != hipSuccess) t[i] = 0.f;
+    g_eng->convert_s += 1e-3 * (t[0] + t[2]);
+    g_eng->device_s += 1e-3 * t[1];
+  }
+};
 
 hipStream_t pick(rk_stream s) { return s ? (hipStream_t)s : g_eng->stream; }
 
@@ -250,6 +297,7 @@ extern "C" int rk_init(int device) {
   e->device = device;
   e->num_cus = prop.multiProcessorCount;
   hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+  for (int i = 0; i < 4 && err == hipSuccess; ++i) err = hipEventCreate(&e->tev[i]);
   if (err != hipSuccess) {
     delete e;
     return hip_fail(err, "rk_init");
@@ -293,7 +341,6 @@ extern "C" int rk_mem_stats(rk_mem_stats_t *out) {
 extern "C" int rk_trim_scratch_to(uint64_t budget) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_trim_scratch_to"));
-  HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_trim_scratch_to");
   // Largest buffers go first until the rest fits the budget.
   std::vector<std::pair<size_t, std::string>> order;
   uint64_t total = 0;
@@ -305,7 +352,9 @@ extern "C" int rk_trim_scratch_to(uint64_t budget) {
   for (auto &o : order) {
     if (total <= budget) break;
     DevBuf &b = g_eng->scratch[o.second];
+    if (b.recorded) HIP_TRY(hipEventSynchronize(b.ev), "rk_trim_scratch_to");
     HIP_TRY(hipFree(b.p), "rk_trim_scratch_to");
+    if (b.ev) (void)hipEventDestroy(b.ev);
     total -= b.bytes;
     g_eng->scratch.erase(o.second);
   }
@@ -321,9 +370,10 @@ extern "C" int rk_pack(const float *w, int64_t n, int64_t k, rk_weight_id *id) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_pack"));
   RK_TRY(check_f16_shape(n, k, "rk_pack"));
+  CallScope cs(g_eng->stream);
   void *x32, *x16;
-  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
-  RK_TRY(scratch("pack_f16", (size_t)n * k * 2, &x16));
+  RK_TRY(scratch(cs, "pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch(cs, "pack_f16", (size_t)n * k * 2, &x16));
   HIP_TRY(hipMemcpyAsync(x32, w, (size_t)n * k * 4, hipMemcpyHostToDevice, g_eng->stream), "rk_pack");
   HIP_TRY(rk_launch_f32_to_f16((const float *)x32, x16, n * k, g_eng->stream), "rk_pack");
   return pack_f16_dev(x16, n, k, id);
@@ -333,8 +383,9 @@ extern "C" int rk_pack_f16(const uint16_t *w, int64_t n, int64_t k, rk_weight_id
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_pack_f16"));
   RK_TRY(check_f16_shape(n, k, "rk_pack_f16"));
+  CallScope cs(g_eng->stream);
   void *x16;
-  RK_TRY(scratch("pack_f16", (size_t)n * k * 2, &x16));
+  RK_TRY(scratch(cs, "pack_f16", (size_t)n * k * 2, &x16));
   HIP_TRY(hipMemcpyAsync(x16, w, (size_t)n * k * 2, hipMemcpyHostToDevice, g_eng->stream),
           "rk_pack_f16");
   return pack_f16_dev(x16, n, k, id);
@@ -351,9 +402,10 @@ extern "C" int rk_pack_seg(const float *const *parts, const int64_t *ns, int npa
     n += ns[i];
   }
   RK_TRY(check_f16_shape(n, k, "rk_pack_seg"));
+  CallScope cs(g_eng->stream);
   void *x32, *x16;
-  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
-  RK_TRY(scratch("pack_f16", (size_t)n * k * 2, &x16));
+  RK_TRY(scratch(cs, "pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch(cs, "pack_f16", (size_t)n * k * 2, &x16));
   int64_t off = 0;
   for (int i = 0; i < nparts; ++i) {
     HIP_TRY(hipMemcpyAsync((char *)x32 + off * k * 4, parts[i], (size_t)ns[i] * k * 4,
@@ -394,13 +446,14 @@ extern "C" int rk_pack_i8(const float *w, int64_t n, int64_t k, int64_t group, r
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_pack_i8"));
   RK_TRY(check_i8_shape(n, k, group, "rk_pack_i8"));
+  CallScope cs(g_eng->stream);
   // Quantize on the device with the activation quantizer (same formula as
   // quantize_i8_weight, ext.rs:1001-1012), then keep codes and scales.
   void *x32, *q, *s;
   const int64_t ng = k / group;
-  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
-  RK_TRY(scratch("pack_q", (size_t)n * k, &q));
-  RK_TRY(scratch("pack_s", (size_t)n * ng * 4, &s));
+  RK_TRY(scratch(cs, "pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch(cs, "pack_q", (size_t)n * k, &q));
+  RK_TRY(scratch(cs, "pack_s", (size_t)n * ng * 4, &s));
   HIP_TRY(hipMemcpyAsync(x32, w, (size_t)n * k * 4, hipMemcpyHostToDevice, g_eng->stream),
           "rk_pack_i8");
   HIP_TRY(rk_launch_quantize_rows((const float *)x32, n, k, group, (int8_t *)q, (float *)s,
@@ -458,6 +511,7 @@ extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_pack_q8_0_f32"));
   RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_f32"));
+  CallScope cs(g_eng->stream);
   Weight wt;
   wt.kind = RK_WEIGHT_I8;
   wt.n = n;
@@ -465,7 +519,7 @@ extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_
   wt.group = 32;
   wt.ws_stride = ws_stride_for(k);
   void *x32;
-  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch(cs, "pack_f32", (size_t)n * k * 4, &x32));
   HIP_TRY(hipMalloc(&wt.codes, (size_t)n * k), "rk_pack_q8_0_f32");
   HIP_TRY(hipMalloc((void **)&wt.scales, (size_t)n * wt.ws_stride * 4), "rk_pack_q8_0_f32");
   HIP_TRY(hipMemsetAsync(wt.scales, 0, (size_t)n * wt.ws_stride * 4, g_eng->stream), "rk_pack_q8_0_f32");
@@ -514,6 +568,7 @@ extern "C" int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t 
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_pack_q8_0_glu_f32"));
   RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_glu_f32"));
+  CallScope cs(g_eng->stream);
   const int64_t rows = glu_rows(n);
   Weight wt;
   wt.kind = RK_WEIGHT_I8;
@@ -523,7 +578,7 @@ extern "C" int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t 
   wt.glu_n = n;
   wt.ws_stride = ws_stride_for(k);
   void *x32;
-  RK_TRY(scratch("pack_f32", (size_t)n * k * 4, &x32));
+  RK_TRY(scratch(cs, "pack_f32", (size_t)n * k * 4, &x32));
   HIP_TRY(hipMalloc(&wt.codes, (size_t)rows * k), "rk_pack_q8_0_glu_f32");
   HIP_TRY(hipMalloc((void **)&wt.scales, (size_t)rows * wt.ws_stride * 4), "rk_pack_q8_0_glu_f32");
   HIP_TRY(hipMemsetAsync(wt.codes, 0, (size_t)rows * k, g_eng->stream), "rk_pack_q8_0_glu_f32");
@@ -625,47 +680,56 @@ extern "C" int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, 
   if (w->moe) return fail(RK_E_UNSUPPORTED, "rk_matmul", "an expert stack is not a matmul weight");
   if (w->glu_n > 0)
     return fail(RK_E_UNSUPPORTED, "rk_matmul", "gate|up weight: use rk_matmul_w8a8_glu_dev");
-  const auto t0 = Clock::now();
   hipStream_t st = g_eng->stream;
+  CallScope cs(st);
+  HostTimer tm(st);
   const int64_t n = w->n;
   void *x32, *y32;
-  RK_TRY(scratch("mm_x32", (size_t)m * k * 4, &x32));
-  RK_TRY(scratch("mm_y32", (size_t)m * n * 4, &y32));
+  RK_TRY(scratch(cs, "mm_x32", (size_t)m * k * 4, &x32));
+  RK_TRY(scratch(cs, "mm_y32", (size_t)m * n * 4, &y32));
+  tm.mark(0);
   HIP_TRY(hipMemcpyAsync(x32, x, (size_t)m * k * 4, hipMemcpyHostToDevice, st), "rk_matmul");
   if (w->kind == RK_WEIGHT_F16) {
     void *a16, *c16;
-    RK_TRY(scratch("mm_a16", (size_t)m * k * 2, &a16));
-    RK_TRY(scratch("mm_c16", (size_t)m * n * 2, &c16));
+    RK_TRY(scratch(cs, "mm_a16", (size_t)m * k * 2, &a16));
+    RK_TRY(scratch(cs, "mm_c16", (size_t)m * n * 2, &c16));
     HIP_TRY(rk_launch_f32_to_f16((const float *)x32, a16, m * k, st), "rk_matmul");
+    tm.mark(1);
     HIP_TRY(rk_launch_gemm_f16(a16, w->codes, c16, (int)m, (int)n, (int)k, g_eng->num_cus, st),
             "rk_matmul_fp16");
+    tm.mark(2);
     HIP_TRY(rk_launch_f16_to_f32(c16, (float *)y32, m * n, st), "rk_matmul");
   } else if (w->kind == RK_WEIGHT_I8) {
     void *q, *s;
     const int64_t ng = k / w->group;
-    RK_TRY(scratch("mm_q", (size_t)m * k, &q));
-    RK_TRY(scratch("mm_s", (size_t)m * ng * 4, &s));
+    RK_TRY(scratch(cs, "mm_q", (size_t)m * k, &q));
+    RK_TRY(scratch(cs, "mm_s", (size_t)m * ng * 4, &s));
     HIP_TRY(rk_launch_quantize_rows((const float *)x32, m, k, w->group, (int8_t *)q, (float *)s, st),
             "rk_matmul");
+    tm.mark(1);
     RK_TRY(launch_i8(*w, (const int8_t *)q, (const float *)s, (int)ng, (int)(w->group / 32),
                      I8_PER_GROUP, false, m, y32, st, "rk_matmul_int8_gw"));
+    tm.mark(2);
   } else {  // QAT
     void *q, *rs, *acc;
-    RK_TRY(scratch("mm_q", (size_t)m * k, &q));
-    RK_TRY(scratch("mm_rs", (size_t)m * 4, &rs));
-    RK_TRY(scratch("mm_acc", (size_t)m * n * 4, &acc));
+    RK_TRY(scratch(cs, "mm_q", (size_t)m * k, &q));
+    RK_TRY(scratch(cs, "mm_rs", (size_t)m * 4, &rs));
+    RK_TRY(scratch(cs, "mm_acc", (size_t)m * n * 4, &acc));
     HIP_TRY(rk_launch_quantize_static((const float *)x32, m, k, w->in_scale, (int8_t *)q,
                                       (float *)rs, st),
             "rk_matmul");
+    tm.mark(1);
     RK_TRY(launch_i8(*w, (const int8_t *)q, nullptr, 0, 1, I8_RAW, false, m, acc, st,
                      "rk_matmul_int8_qat"));
     HIP_TRY(rk_launch_qat_epilogue((const int32_t *)acc, (const float *)rs, w->scales, m, n,
                                    w->out_scale, (float *)y32, st),
             "rk_matmul");
+    tm.mark(2);
   }
   HIP_TRY(hipMemcpyAsync(y, y32, (size_t)m * n * 4, hipMemcpyDeviceToHost, st), "rk_matmul");
+  tm.mark(3);
   HIP_TRY(hipStreamSynchronize(st), "rk_matmul");
-  g_eng->device_s += secs(t0, Clock::now());
+  tm.finish();
   g_eng->calls++;
   return RK_OK;
 }
@@ -825,6 +889,11 @@ int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_
              int64_t n_kv_pad, int n_head, int n_kv_heads, int head_dim, float scale, float softcap,
              int mode, int64_t window, int64_t q0, int64_t k0, bool head_major, hipStream_t st,
              const char *op, int64_t q_ts = 0, int64_t k_ts = 0, int64_t o_ts = 0) {
+  // K and Vᵀ of one kv head are addressed with 32-bit byte offsets.
+  const int64_t k_tok = head_major ? head_dim : (k_ts ? k_ts : (int64_t)n_kv_heads * head_dim);
+  if (((n_kv - 1) * k_tok + head_dim) * 2 >= ((int64_t)1 << 31) ||
+      (int64_t)rk_attn_dv_pad(head_dim) * n_kv_pad * 2 >= ((int64_t)1 << 31))
+    return fail(RK_E_SHAPE, op, "one kv head's K rows or Vᵀ reach 2 GiB");
   AttnArgs a{};
   a.q = q;
   a.k = k;
@@ -862,21 +931,26 @@ int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_
   return RK_OK;
 }
 
-int attn_dev_impl(const void *q, const void *k, const void *v, int64_t n_q, int64_t n_kv, int n_head,
-                  int n_kv_heads, int head_dim, float scale, float softcap, int mode,
-                  int64_t window, int64_t q0, int64_t k0, void *out, hipStream_t st,
+// Token-major attention on device buffers: Vᵀ into scratch, then the kernel
+// (tm, when given, is marked between the two: the Vᵀ rewrite is layout work).
+int attn_dev_impl(CallScope &cs, const void *q, const void *k, const void *v, int64_t n_q,
+                  int64_t n_kv, int n_head, int n_kv_heads, int head_dim, float scale,
+                  float softcap, int mode, int64_t window, int64_t q0, int64_t k0, void *out,
                   const char *op, int64_t q_ts = 0, int64_t k_ts = 0, int64_t v_ts = 0,
-                  int64_t o_ts = 0) {
+                  int64_t o_ts = 0, HostTimer *tm = nullptr) {
   RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, op));
   const int dvp = rk_attn_dv_pad(head_dim);
   const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
+  if ((int64_t)dvp * n_kv_pad * 2 >= ((int64_t)1 << 31))
+    return fail(RK_E_SHAPE, op, "one kv head's Vᵀ reaches 2 GiB");
   void *vt;
-  RK_TRY(scratch("attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
+  RK_TRY(scratch(cs, "attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
   HIP_TRY(rk_launch_v_transpose(v, v_ts ? v_ts : (int64_t)n_kv_heads * head_dim, head_dim,
-                                (int)n_kv, (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
+                                (int)n_kv, (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, cs.st),
           op);
+  if (tm) tm->mark(1);
   return attn_run(q, k, vt, out, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale, softcap,
-                  mode, window, q0, k0, false, st, op, q_ts, k_ts, o_ts);
+                  mode, window, q0, k0, false, cs.st, op, q_ts, k_ts, o_ts);
 }
 }  // namespace
 
@@ -886,8 +960,9 @@ extern "C" int rk_attention_dev(const void *q, const void *k, const void *v, int
                                 int64_t q0, int64_t k0, void *out, rk_stream stream) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_attention_dev"));
-  RK_TRY(attn_dev_impl(q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap, mask_mode,
-                       window, q0, k0, out, pick(stream), "rk_attention_dev"));
+  CallScope cs(pick(stream));
+  RK_TRY(attn_dev_impl(cs, q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap,
+                       mask_mode, window, q0, k0, out, "rk_attention_dev"));
   g_eng->calls++;
   return RK_OK;
 }
@@ -907,8 +982,9 @@ extern "C" int rk_attention_strided_dev(const void *q, int64_t q_stride, const v
   if ((q_stride | k_stride | v_stride | out_stride) % 8 != 0 ||
       (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) != 0)
     return fail(RK_E_SHAPE, name, "token strides must be multiples of 8 values, buffers 16-byte aligned");
-  RK_TRY(attn_dev_impl(q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap, mask_mode,
-                       window, q0, k0, out, pick(stream), name, q_stride, k_stride, v_stride,
+  CallScope cs(pick(stream));
+  RK_TRY(attn_dev_impl(cs, q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap,
+                       mask_mode, window, q0, k0, out, name, q_stride, k_stride, v_stride,
                        out_stride));
   g_eng->calls++;
   return RK_OK;
@@ -922,16 +998,18 @@ extern "C" int rk_attention(const float *q, const float *k, const float *v, int6
   RK_TRY(ensure("rk_attention"));
   int mode = mask_mode;
   RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, "rk_attention"));
-  const auto t0 = Clock::now();
   hipStream_t st = g_eng->stream;
+  CallScope cs(st);
+  HostTimer tm(st);
   const size_t nq_el = (size_t)n_q * n_head * head_dim;
   const size_t nk_el = (size_t)n_kv * n_kv_heads * head_dim;
   void *f32buf, *q16, *k16, *v16, *o16;
-  RK_TRY(scratch("at_f32", std::max(nq_el, nk_el) * 4, &f32buf));
-  RK_TRY(scratch("at_q16", nq_el * 2, &q16));
-  RK_TRY(scratch("at_k16", nk_el * 2, &k16));
-  RK_TRY(scratch("at_v16", nk_el * 2, &v16));
-  RK_TRY(scratch("at_o16", nq_el * 2, &o16));
+  RK_TRY(scratch(cs, "at_f32", std::max(nq_el, nk_el) * 4, &f32buf));
+  RK_TRY(scratch(cs, "at_q16", nq_el * 2, &q16));
+  RK_TRY(scratch(cs, "at_k16", nk_el * 2, &k16));
+  RK_TRY(scratch(cs, "at_v16", nk_el * 2, &v16));
+  RK_TRY(scratch(cs, "at_o16", nq_el * 2, &o16));
+  tm.mark(0);
   const float *srcs[3] = {q, k, v};
   void *dsts[3] = {q16, k16, v16};
   const size_t els[3] = {nq_el, nk_el, nk_el};
@@ -939,12 +1017,14 @@ extern "C" int rk_attention(const float *q, const float *k, const float *v, int6
     HIP_TRY(hipMemcpyAsync(f32buf, srcs[i], els[i] * 4, hipMemcpyHostToDevice, st), "rk_attention");
     HIP_TRY(rk_launch_f32_to_f16((const float *)f32buf, dsts[i], (int64_t)els[i], st), "rk_attention");
   }
-  RK_TRY(attn_dev_impl(q16, k16, v16, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap, mode,
-                       window, q0, k0, o16, st, "rk_attention"));
+  RK_TRY(attn_dev_impl(cs, q16, k16, v16, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap,
+                       mode, window, q0, k0, o16, "rk_attention", 0, 0, 0, 0, &tm));
+  tm.mark(2);
   HIP_TRY(rk_launch_f16_to_f32(o16, (float *)f32buf, (int64_t)nq_el, st), "rk_attention");
   HIP_TRY(hipMemcpyAsync(out, f32buf, nq_el * 4, hipMemcpyDeviceToHost, st), "rk_attention");
+  tm.mark(3);
   HIP_TRY(hipStreamSynchronize(st), "rk_attention");
-  g_eng->device_s += secs(t0, Clock::now());
+  tm.finish();
   g_eng->calls++;
   return RK_OK;
 }
@@ -954,34 +1034,65 @@ extern "C" int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv
                                  int64_t window, int64_t q0, int64_t k0, const uint16_t *q,
                                  const uint16_t *k, const uint16_t *v, uint16_t *out) {
   std::lock_guard<std::mutex> lk(g_mu);
-  RK_TRY(ensure("rk_flash_attn_f16"));
-  if (dv != head_dim) return fail(RK_E_UNSUPPORTED, "rk_flash_attn_f16", "dv must equal head_dim");
+  const char *op = "rk_flash_attn_f16";
+  RK_TRY(ensure(op));
+  if (head_dim <= 0 || dv <= 0) return fail(RK_E_SHAPE, op, "head_dim and dv must be positive");
+  // The kernel runs one width D = max(head_dim, dv) for q, k and v: zero
+  // columns added to q and k leave every score unchanged, zero rows added to
+  // Vᵀ only add zero output columns, so the first dv output columns are the
+  // attention of the given operands (the reference pads Clef's 72-wide heads
+  // to head_dim 96 / dv 80 the same way, src/clef/vision/npu.rs:211-230).
+  const int D = std::max(head_dim, dv);
   int mode = mask_mode;
-  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, "rk_flash_attn_f16"));
-  const auto t0 = Clock::now();
+  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, D, &mode, window, op));
   hipStream_t st = g_eng->stream;
-  const size_t nq_el = (size_t)n_q * n_head * head_dim;
-  const size_t nk_el = (size_t)n_kv * n_kv_heads * head_dim;
-  const int dvp = rk_attn_dv_pad(head_dim);
+  CallScope cs(st);
+  HostTimer tm(st);
+  const size_t nq_el = (size_t)n_q * n_head * D;
+  const size_t nk_el = (size_t)n_kv * n_kv_heads * D;
+  const size_t nv_in = (size_t)n_kv_heads * dv * n_kv;
+  const int dvp = rk_attn_dv_pad(D);
   const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
   void *q16, *k16, *v16, *o16, *vt;
-  RK_TRY(scratch("at_q16", nq_el * 2, &q16));
-  RK_TRY(scratch("at_k16", nk_el * 2, &k16));
-  RK_TRY(scratch("at_v16", nk_el * 2, &v16));
-  RK_TRY(scratch("at_o16", nq_el * 2, &o16));
-  RK_TRY(scratch("attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
-  HIP_TRY(hipMemcpyAsync(q16, q, nq_el * 2, hipMemcpyHostToDevice, st), "rk_flash_attn_f16");
-  HIP_TRY(hipMemcpyAsync(k16, k, nk_el * 2, hipMemcpyHostToDevice, st), "rk_flash_attn_f16");
-  HIP_TRY(hipMemcpyAsync(v16, v, nk_el * 2, hipMemcpyHostToDevice, st), "rk_flash_attn_f16");
-  // v is [KV][dv][n_kv]: element (key, head, d) at head·dv·n_kv + d·n_kv + key.
-  HIP_TRY(rk_launch_v_transpose_strided(v16, 1, (int64_t)head_dim * n_kv, n_kv, (int)n_kv,
-                                        (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
-          "rk_flash_attn_f16");
-  RK_TRY(attn_run(q16, k16, vt, o16, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale,
-                  softcap, mode, window, q0, k0, true, st, "rk_flash_attn_f16"));
-  HIP_TRY(hipMemcpyAsync(out, o16, nq_el * 2, hipMemcpyDeviceToHost, st), "rk_flash_attn_f16");
-  HIP_TRY(hipStreamSynchronize(st), "rk_flash_attn_f16");
-  g_eng->device_s += secs(t0, Clock::now());
+  RK_TRY(scratch(cs, "at_q16", nq_el * 2, &q16));
+  RK_TRY(scratch(cs, "at_k16", nk_el * 2, &k16));
+  RK_TRY(scratch(cs, "at_v16", nv_in * 2, &v16));
+  RK_TRY(scratch(cs, "at_o16", nq_el * 2, &o16));
+  RK_TRY(scratch(cs, "attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
+  tm.mark(0);
+  // q [H][n_q][head_dim] and k [KV][n_kv][head_dim] into rows of D values.
+  const struct {
+    const uint16_t *src;
+    void *dst;
+    size_t rows;
+  } qk[2] = {{q, q16, (size_t)n_head * n_q}, {k, k16, (size_t)n_kv_heads * n_kv}};
+  for (const auto &t : qk) {
+    if (head_dim < D) {
+      HIP_TRY(hipMemsetAsync(t.dst, 0, t.rows * D * 2, st), op);
+      HIP_TRY(hipMemcpy2DAsync(t.dst, (size_t)D * 2, t.src, (size_t)head_dim * 2,
+                               (size_t)head_dim * 2, t.rows, hipMemcpyHostToDevice, st),
+              op);
+    } else {
+      HIP_TRY(hipMemcpyAsync(t.dst, t.src, t.rows * D * 2, hipMemcpyHostToDevice, st), op);
+    }
+  }
+  HIP_TRY(hipMemcpyAsync(v16, v, nv_in * 2, hipMemcpyHostToDevice, st), op);
+  // v is [KV][dv][n_kv]: element (key, head, d) at head·dv·n_kv + d·n_kv + key;
+  // its dv rows fill Vᵀ, the rest of the D rows are zero.
+  HIP_TRY(rk_launch_v_transpose_strided(v16, 1, (int64_t)dv * n_kv, n_kv, (int)n_kv, (int)n_kv_pad,
+                                        n_kv_heads, dv, dvp, vt, st),
+          op);
+  tm.mark(1);
+  RK_TRY(attn_run(q16, k16, vt, o16, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, D, scale, softcap,
+                  mode, window, q0, k0, true, st, op));
+  tm.mark(2);
+  // out [H][n_q][dv]: the first dv columns of each output row.
+  HIP_TRY(hipMemcpy2DAsync(out, (size_t)dv * 2, o16, (size_t)D * 2, (size_t)dv * 2,
+                           (size_t)n_head * n_q, hipMemcpyDeviceToHost, st),
+          op);
+  tm.mark(3);
+  HIP_TRY(hipStreamSynchronize(st), op);
+  tm.finish();
   g_eng->calls++;
   return RK_OK;
 }
@@ -1143,8 +1254,9 @@ extern "C" int rk_pack_moe_f32(const float *gate, const float *up, const float *
   const int64_t H = hidden, I = inter, E = n_experts;
   Weight w;
   RK_TRY(moe_alloc(w, n_experts, H, I, "rk_pack_moe_f32"));
+  CallScope cs(g_eng->stream);
   void *x32;
-  RK_TRY(scratch("pack_f32", (size_t)I * H * 4, &x32));
+  RK_TRY(scratch(cs, "pack_f32", (size_t)I * H * 4, &x32));
   hipStream_t st = g_eng->stream;
   const int64_t gu_stride = moe_gu_code_stride(w), dn_stride = moe_dn_code_stride(w);
   for (int64_t e = 0; e < E; ++e) {
@@ -1182,14 +1294,18 @@ struct MoePlan {
   int32_t *slot = nullptr;    // [s, top_k] bucket rows of a token, ascending expert id
   MoeTile *tiles = nullptr;   // [n_tiles]
   uint64_t weight = 0;        // expert stack the plan was made for
+  // Recorded after every run that reads the lists, on that run's stream.
+  mutable hipEvent_t last_use = nullptr;
+  mutable bool used = false;
 };
 
 void plan_free(MoePlan *p) {
   if (!p) return;
-  hipFree(p->tok);
-  hipFree(p->roww);
-  hipFree(p->slot);
-  hipFree(p->tiles);
+  if (p->last_use) (void)hipEventDestroy(p->last_use);
+  (void)hipFree(p->tok);
+  (void)hipFree(p->roww);
+  (void)hipFree(p->slot);
+  (void)hipFree(p->tiles);
   delete p;
 }
 
@@ -1248,20 +1364,21 @@ int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const f
   return RK_OK;
 }
 
-int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipStream_t st,
+int moe_run(CallScope &cs, const Weight &w, const MoePlan &plan, const float *x, float *y,
             float *act_out = nullptr) {
+  hipStream_t st = cs.st;
   const int64_t H = w.hidden, I = w.inter, S = plan.s, R = std::max<int64_t>(plan.rows, 1);
   const int64_t KBh = H / 32, KBi = I / 32;  // 32-value activation groups per row
   void *xq, *xs, *act, *aq, *as, *yb;
-  RK_TRY(scratch("moe_xq", (size_t)S * H, &xq));
-  RK_TRY(scratch("moe_xs", (size_t)S * KBh * 4, &xs));
+  RK_TRY(scratch(cs, "moe_xq", (size_t)S * H, &xq));
+  RK_TRY(scratch(cs, "moe_xs", (size_t)S * KBh * 4, &xs));
   if (act_out)
     act = act_out;
   else
-    RK_TRY(scratch("moe_act", (size_t)R * I * 4, &act));
-  RK_TRY(scratch("moe_aq", (size_t)R * I, &aq));
-  RK_TRY(scratch("moe_as", (size_t)R * KBi * 4, &as));
-  RK_TRY(scratch("moe_yb", (size_t)R * H * 4, &yb));
+    RK_TRY(scratch(cs, "moe_act", (size_t)R * I * 4, &act));
+  RK_TRY(scratch(cs, "moe_aq", (size_t)R * I, &aq));
+  RK_TRY(scratch(cs, "moe_as", (size_t)R * KBi * 4, &as));
+  RK_TRY(scratch(cs, "moe_yb", (size_t)R * H * 4, &yb));
   const char *op = "rk_moe_experts_dev";
   // x and the silu·up rows are quantized per row per 32-value group, as the
   // reference's expert workers do (engine.rs:1005-1006, 1034-1035).
@@ -1280,6 +1397,13 @@ int moe_run(const Weight &w, const MoePlan &plan, const float *x, float *y, hipS
                                   (int)I, plan.roww, (float *)yb, g_eng->num_cus, st),
           op);
   HIP_TRY(rk_launch_moe_combine((const float *)yb, plan.slot, S, plan.top_k, H, y, st), op);
+  return RK_OK;
+}
+
+int plan_mark_used(const MoePlan &p, hipStream_t st) {
+  if (!p.last_use) HIP_TRY(hipEventCreateWithFlags(&p.last_use, hipEventDisableTiming), "rk_moe_plan");
+  HIP_TRY(hipEventRecord(p.last_use, st), "rk_moe_plan");
+  p.used = true;
   return RK_OK;
 }
 
@@ -1304,9 +1428,10 @@ extern "C" int rk_moe_experts_dev(rk_weight_id id, const float *x, int64_t s, in
   Weight *w;
   RK_TRY(moe_check(id, s, top_k, &w, "rk_moe_experts_dev"));
   hipStream_t st = pick(stream);
+  CallScope cs(st);
   MoePlan *plan = new MoePlan();
   int rc = moe_plan(*w, s, top_k, ids, wts, plan, st);
-  if (rc == RK_OK) rc = moe_run(*w, *plan, x, y, st);
+  if (rc == RK_OK) rc = moe_run(cs, *w, *plan, x, y);
   // The plan's lists must outlive the kernels that read them.
   hipError_t e = hipStreamSynchronize(st);
   plan_free(plan);
@@ -1343,7 +1468,9 @@ extern "C" int rk_moe_experts_planned_dev(rk_weight_id id, const void *plan, con
   RK_TRY(moe_check(id, p->s, p->top_k, &w, "rk_moe_experts_planned_dev"));
   if (p->weight != id)
     return fail(RK_E_SHAPE, "rk_moe_experts_planned_dev", "plan was made for another expert stack");
-  RK_TRY(moe_run(*w, *p, x, y, pick(stream)));
+  CallScope cs(pick(stream));
+  RK_TRY(moe_run(cs, *w, *p, x, y));
+  RK_TRY(plan_mark_used(*p, cs.st));
   g_eng->calls++;
   return RK_OK;
 }
@@ -1358,15 +1485,20 @@ extern "C" int rk_moe_gate_up_dev(rk_weight_id id, const void *plan, const float
   RK_TRY(moe_check(id, p->s, p->top_k, &w, "rk_moe_gate_up_dev"));
   if (p->weight != id)
     return fail(RK_E_SHAPE, "rk_moe_gate_up_dev", "plan was made for another expert stack");
-  RK_TRY(moe_run(*w, *p, x, nullptr, pick(stream), act));
+  CallScope cs(pick(stream));
+  RK_TRY(moe_run(cs, *w, *p, x, nullptr, act));
+  RK_TRY(plan_mark_used(*p, cs.st));
   return RK_OK;
 }
 
 extern "C" int rk_moe_plan_destroy(void *plan) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_moe_plan_destroy"));
+  MoePlan *p = (MoePlan *)plan;
+  // Runs on any stream that read the plan's lists must have finished.
+  if (p && p->used) HIP_TRY(hipEventSynchronize(p->last_use), "rk_moe_plan_destroy");
   HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_moe_plan_destroy");
-  plan_free((MoePlan *)plan);
+  plan_free(p);
   return RK_OK;
 }
 
@@ -1416,8 +1548,9 @@ int glue_host(int op, const float *a, const float *b, float *out, int64_t n, con
   if (n < 0) return fail(RK_E_SHAPE, name, "negative element count");
   if (n == 0) return RK_OK;
   if (!a || !b || !out) return fail(RK_E_SHAPE, name, "null buffer");
+  CallScope cs(g_eng->stream);
   void *d = nullptr;
-  RK_TRY(scratch("glue", (size_t)n * 12, &d));
+  RK_TRY(scratch(cs, "glue", (size_t)n * 12, &d));
   float *da = (float *)d, *db = da + n, *dout = db + n;
   hipStream_t st = g_eng->stream;
   HIP_TRY(hipMemcpyAsync(da, a, (size_t)n * 4, hipMemcpyHostToDevice, st), name);
@@ -1479,8 +1612,9 @@ int rms_host(const float *x, const float *w, float *out, int64_t rows, int64_t d
   RK_TRY(rms_check(x, out, rows, d, RK_DTYPE_F32, name));
   if (rows == 0) return RK_OK;
   const size_t n = (size_t)(rows * d);
+  CallScope cs(g_eng->stream);
   void *buf = nullptr;
-  RK_TRY(scratch("norm", (n + (size_t)d) * 4, &buf));
+  RK_TRY(scratch(cs, "norm", (n + (size_t)d) * 4, &buf));
   float *dx = (float *)buf, *dw = dx + n;
   hipStream_t st = g_eng->stream;
   HIP_TRY(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, st), name);
@@ -1584,10 +1718,11 @@ extern "C" int rk_attention_qkv_dev(void *qkv, int64_t s, int64_t row_stride, in
                          cs_dtype) == 0)
     return fail(RK_E_UNSUPPORTED, name, "head_dim / row_stride / buffer alignment allow no vector width");
   hipStream_t st = pick(stream);
+  CallScope cs(st);
   const int dvp = rk_attn_dv_pad(head_dim);
   const int64_t n_kv_pad = round_up_i(s, rk_attn_kv_tile());
   void *vt;
-  RK_TRY(scratch("attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
+  RK_TRY(scratch(cs, "attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
   HIP_TRY(rk_launch_qk_norm_rope(qkv, row_stride, (int)s, n_head, n_kv_heads, head_dim, q_norm_w,
                                  k_norm_w, (float)eps, cos, sin, cs_dtype, RK_DTYPE_F16, st, vt,
                                  (int)n_kv_pad, dvp), name);
@@ -1633,8 +1768,9 @@ extern "C" int rk_rope(const float *x, const float *cos, const float *sin, float
   RK_TRY(rope_check(x, cos, sin, out, b, s, h, d, RK_DTYPE_F32, RK_DTYPE_F32, name));
   const size_t n = (size_t)(b * s * h * d), nt = (size_t)(s * (d / 2));
   if (n == 0) return RK_OK;
+  CallScope cs(g_eng->stream);
   void *buf = nullptr;
-  RK_TRY(scratch("rope", (n + 2 * nt) * 4, &buf));
+  RK_TRY(scratch(cs, "rope", (n + 2 * nt) * 4, &buf));
   float *dx = (float *)buf, *dc = dx + n, *ds = dc + nt;
   hipStream_t st = g_eng->stream;
   HIP_TRY(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, st), name);
@@ -1665,6 +1801,23 @@ extern "C" int rk_stream_get(rk_stream *stream) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_stream_get"));
   *stream = (rk_stream)g_eng->stream;
+  return RK_OK;
+}
+extern "C" int rk_stream_create(rk_stream *stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_stream_create"));
+  if (!stream) return fail(RK_E_SHAPE, "rk_stream_create", "null output");
+  hipStream_t st = nullptr;
+  HIP_TRY(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "rk_stream_create");
+  *stream = (rk_stream)st;
+  return RK_OK;
+}
+extern "C" int rk_stream_destroy(rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_stream_destroy"));
+  if (!stream || (hipStream_t)stream == g_eng->stream)
+    return fail(RK_E_SHAPE, "rk_stream_destroy", "not a stream made by rk_stream_create");
+  HIP_TRY(hipStreamDestroy((hipStream_t)stream), "rk_stream_destroy");
   return RK_OK;
 }
 extern "C" int rk_stream_sync(rk_stream stream) {

@@ -14,7 +14,10 @@
  *     message of the last failure on the calling thread.
  *   - Calls are serialised by one engine mutex (`ext.rs:543-556`); work inside a
  *     call runs on the library's HIP stream (or the stream passed to a `_dev`
- *     entry) and is stream-ordered.
+ *     entry) and is stream-ordered. Calls may use different streams: the
+ *     library's internal scratch buffers are fenced with events, so a call
+ *     that reuses one waits on the device for the last call that used it, and
+ *     a buffer is only freed (grown, trimmed) after that use has completed.
  *   - Host entries (`rk_matmul`, `rk_attention`, ...) take and return host f32
  *     buffers, as Burn's flex tensors do; conversion to fp16 / int8 happens on
  *     the GPU. `_dev` entries take device pointers that are already resident in
@@ -92,9 +95,13 @@ const char *rk_last_error(void);
  * as `burn_rocket::Error::is_fallback` (lib.rs:142-147). */
 int rk_is_fallback(int rc);
 
-/* Op wall-time counters: `burn_rocket::stats()` / `stats_reset()`
- * (ext.rs:171-200). convert_s covers host<->device copies and format
- * conversion, device_s the kernels, calls counts op invocations. */
+/* Op time counters: `burn_rocket::stats()` / `stats_reset()` (ext.rs:165-200).
+ * The host-buffer entries (rk_matmul, rk_attention, rk_flash_attn_f16) are
+ * timed with events on their stream: convert_s is their host<->device copies,
+ * format conversions and layout passes (the reference's T_CONVERT_US), device_s
+ * the op's own kernels (T_NPU_US). calls counts matmul, attention and MoE calls,
+ * host-buffer and `_dev` alike; the `_dev` entries return before their kernels
+ * finish and add no time. */
 typedef struct {
   double convert_s;
   double device_s;
@@ -248,9 +255,14 @@ int rk_attention_strided_dev(const void *q, int64_t q_stride, const void *k, int
                              int64_t k0, void *out, int64_t out_stride, rk_stream stream);
 
 /* Head-major fp16 host buffers, the `RocketFaCtx::flash_attn` layout
- * (lib.rs:294-323; attn/mod.rs:1541-1600): q [n_head][n_q][head_dim],
- * k [n_kv_heads][n_kv][head_dim], v transposed [n_kv_heads][dv][n_kv],
- * out [n_head][n_q][dv]; dv == head_dim. */
+ * (lib.rs:294-323; attn/mod.rs:1541-1600; shape contract check_flash,
+ * attn/mod.rs:1424-1460): q [n_head][n_q][head_dim], k [n_kv_heads][n_kv]
+ * [head_dim], v transposed [n_kv_heads][dv][n_kv], out [n_head][n_q][dv].
+ * head_dim (the q·k width) and dv (the v width) are independent, as in the
+ * reference's padded calls (Clef's 72-wide vision heads as head_dim 96,
+ * dv 80: src/clef/vision/npu.rs:211-230); max(head_dim, dv) must be one of
+ * the kernel widths 64, 72, 80, 96, 112, 128. The reference's optional
+ * additive mask tensor is replaced by mask_mode / window / q0 / k0. */
 int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv,
                       int n_head, int n_kv_heads, float scale, float softcap,
                       int mask_mode, int64_t window, int64_t q0, int64_t k0,
@@ -434,6 +446,10 @@ int rk_memcpy_dtoh(void *dst, const void *src, size_t bytes);
 int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_stream stream);
 int rk_memset_dev(void *dst, int value, size_t bytes);
 int rk_stream_get(rk_stream *stream);    /* the library stream */
+/* A new non-blocking HIP stream at the default priority, and its release
+ * (after rk_stream_sync when work is pending on it). */
+int rk_stream_create(rk_stream *stream);
+int rk_stream_destroy(rk_stream stream);
 int rk_stream_sync(rk_stream stream);
 int rk_event_create(void **event);
 int rk_event_destroy(void *event);

@@ -180,6 +180,39 @@ def test_host_api_and_head_major_layout(rk, orc):
     assert (a == out).all()
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_flash_attn_clef_padded_layout(rk, orc, mode):
+    """The reference's padded head-major call (src/clef/vision/npu.rs:211-230):
+    72-wide heads with q and k zero-padded to head_dim 96 and Vᵀ padded to dv 80
+    rows, scale 72^-0.5. The first 72 output columns are the attention of the
+    72-wide data (gates against both oracles), columns 72..79 are exactly zero."""
+    s, h, d, dk, dvp = 301, 4, 72, 96, 80
+    r = np.random.default_rng(96 + mode)
+    q = r.standard_normal((s, h * d)).astype(np.float16)
+    k = r.standard_normal((s, h * d)).astype(np.float16)
+    v = r.standard_normal((s, h * d)).astype(np.float16)
+    note(f"flash_attn head_dim {dk} dv {dvp} (72-wide data), mode {mode}")
+
+    def pad_heads(x, w):  # [s, h·d] → [h][s][w], zero columns d..w
+        out = np.zeros((h, s, w), np.float16)
+        out[:, :, :d] = x.reshape(s, h, d).transpose(1, 0, 2)
+        return out
+
+    vt = np.zeros((h, dvp, s), np.float16)  # [h][dv][s], zero rows d..dv
+    vt[:, :d, :] = v.reshape(s, h, d).transpose(1, 2, 0)
+    o = rk.flash_attn_f16(pad_heads(q, dk), pad_heads(k, dk), vt, s, s, dk, h, h, d ** -0.5, 0.0, mode,
+                          dv=dvp)
+    assert o.shape == (h, s, dvp)
+    assert (o[:, :, d:] == 0).all()
+    got = o[:, :, :d].transpose(1, 0, 2).reshape(s, h * d).astype(np.float32)
+    check(orc, got, orc.attention_ref(q, k, v, h, h, d, d ** -0.5, 0.0, mode))
+    check(orc, got, orc.attention_flex(q, k, v, h, h, d, d ** -0.5, 0.0, mode))
+    # dv above head_dim: q and k are padded by the library instead
+    o2 = rk.flash_attn_f16(pad_heads(q, d), pad_heads(k, d), vt, s, s, d, h, h, d ** -0.5, 0.0, mode, dv=dvp)
+    assert (o2[:, :, d:] == 0).all()
+    check(orc, o2[:, :, :d].transpose(1, 0, 2).reshape(s, h * d).astype(np.float32), got)
+
+
 def test_attention_rejects_bad_shapes(rk):
     note("attention errors")
     lib = rk.lib()
