@@ -25,6 +25,7 @@ RK_E_SHAPE, RK_E_TILING, RK_E_NOMEM, RK_E_DEVICE = -1, -2, -3, -4
 RK_E_UNSUPPORTED, RK_E_RANGE, RK_E_IO = -5, -6, -7
 RK_WEIGHT_F16, RK_WEIGHT_I8, RK_WEIGHT_QAT = 1, 2, 3
 MASK_NONE, MASK_CAUSAL, MASK_WINDOW, MASK_CAUSAL_WINDOW = 0, 1, 2, 3
+NOALLOC_SCRATCH_BYTES = 32 << 20  # RK_NOALLOC_SCRATCH_BYTES
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 GLU_SILU, GLU_GELU = 1, 2
 
@@ -59,6 +60,7 @@ SIGNATURES = {
     "rk_matmul_i8_partials_dev": (_i, [_u64, _p, _i64, _i64, _p, _p]),
     "rk_attention": (_i, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p]),
     "rk_attention_dev": (_i, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p]),
+    "rk_attention_dev_noalloc": (_i, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p]),
     "rk_flash_attn_f16": (_i, [_i64, _i64, _i, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p, _p, _p]),
     "rk_moe_route": (_i, [_p, _i64, _i, _i, _i, _p, _p]),
     "rk_pack_moe_q8_0": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),

@@ -288,6 +288,8 @@ extern "C" int rk_init(int device) {
   if (device < 0 || device >= count)
     return fail(RK_E_DEVICE, "rk_init", "no HIP device " + std::to_string(device));
   HIP_TRY(hipSetDevice(device), "rk_init");
+  // The static scratch of rk_attention_dev_noalloc, looked up once per device.
+  HIP_TRY(rk_noalloc_setup(device), "rk_init");
   hipDeviceProp_t prop;
   HIP_TRY(hipGetDeviceProperties(&prop, device), "rk_init");
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
@@ -986,6 +988,36 @@ extern "C" int rk_attention_strided_dev(const void *q, int64_t q_stride, const v
   RK_TRY(attn_dev_impl(cs, q, k, v, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap,
                        mask_mode, window, q0, k0, out, name, q_stride, k_stride, v_stride,
                        out_stride));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_attention_dev_noalloc(const void *q, const void *k, const void *v, int64_t n_q,
+                                        int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
+                                        float scale, float softcap, int mask_mode, int64_t window,
+                                        int64_t q0, int64_t k0, void *out, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_attention_dev_noalloc";
+  RK_TRY(ensure(op));
+  int mode = mask_mode;
+  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, op));
+  const int dvp = rk_attn_dv_pad(head_dim);
+  const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
+  const int64_t need = (int64_t)n_kv_heads * dvp * n_kv_pad * 2;
+  if (need > (int64_t)RK_NOALLOC_SCRATCH_BYTES)
+    return fail(RK_E_RANGE, op,
+                "V transposed needs " + std::to_string(need) + " bytes, above the " +
+                    std::to_string(RK_NOALLOC_SCRATCH_BYTES) + "-byte static scratch");
+  void *vt = rk_noalloc_scratch(g_eng->device);
+  if (!vt) return fail(RK_E_DEVICE, op, "the static scratch was not set up on this device");
+  hipStream_t st = pick(stream);
+  // Every Vᵀ element the kernel reads (padding rows and keys included) is
+  // written here first, so nothing is left from an earlier call.
+  HIP_TRY(rk_launch_v_transpose(v, (int64_t)n_kv_heads * head_dim, head_dim, (int)n_kv,
+                                (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
+          op);
+  RK_TRY(attn_run(q, k, vt, out, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale, softcap,
+                  mode, window, q0, k0, false, st, op));
   g_eng->calls++;
   return RK_OK;
 }

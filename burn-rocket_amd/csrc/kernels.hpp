@@ -165,3 +165,9 @@ hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, int as_str
                                    hipStream_t st);
 hipError_t rk_launch_moe_combine(const float *yb, const int32_t *slot_rows, int64_t s, int top_k,
                                  int64_t h, float *y, hipStream_t st);
+
+// The static device scratch of rk_attention_dev_noalloc (noalloc.hip):
+// rk_noalloc_setup looks up the array's address on `device`, which must be
+// current, once; rk_noalloc_scratch returns it (null before setup).
+hipError_t rk_noalloc_setup(int device);
+void *rk_noalloc_scratch(int device);

@@ -243,6 +243,22 @@ int rk_attention_dev(const void *q, const void *k, const void *v, int64_t n_q,
                      int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
                      float scale, float softcap, int mask_mode, int64_t window,
                      int64_t q0, int64_t k0, void *out, rk_stream stream);
+/* No counterpart in the reference: rk_attention_dev for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It calls no allocating routine: the
+ * V-transposed operand goes to a static device array of
+ * RK_NOALLOC_SCRATCH_BYTES per GPU (held from rk_init until the process ends)
+ * instead of library scratch. Shapes whose Vᵀ, n_kv_heads · dv_pad ·
+ * round_up(n_kv, 64) · 2 bytes with dv_pad = head_dim rounded up to 16, is
+ * larger return RK_E_RANGE. All calls on one GPU share that array and each
+ * call rewrites it: calls whose work overlaps on the device (different streams
+ * with no ordering between them) race and give wrong results. Otherwise the
+ * same arguments and results as rk_attention_dev. */
+#define RK_NOALLOC_SCRATCH_BYTES (32u << 20)
+int rk_attention_dev_noalloc(const void *q, const void *k, const void *v, int64_t n_q,
+                             int64_t n_kv, int n_head, int n_kv_heads, int head_dim, float scale,
+                             float softcap, int mask_mode, int64_t window, int64_t q0, int64_t k0,
+                             void *out, rk_stream stream);
 /* rk_attention_dev with token strides (in values; multiples of 8, buffers
  * 16-byte aligned): q, k, v and out may be column ranges of wider rows, e.g.
  * the q, k and v parts of one fused q|k|v projection output, read where they
