@@ -12,8 +12,9 @@ stream around the whole timed region. `roofline` is the up-projection
 kernel's average launch time (K back-to-back launches between two events on
 the same stream, right after the timed region) against the MI355X dense int8
 MFMA peak. `extras` times the other four workloads the same way;
-`cpu_baseline` times the CPU restatement of the reference's W8A8 path on the
-host cores over a bounded sample of rows.
+`cpu_baseline` times the oracle's C restatement of the reference's W8A8 path
+on the host cores (all of them, and one core) over a bounded sample; every
+`extras` entry carries its own `cpu_baseline` of the same kind.
 """
 import argparse
 import json
@@ -33,6 +34,12 @@ METRIC = "GEMM & GQA-attn TFLOP/s + % MFMA peak on 1 MI355X vs host-CPU Burn pat
 PEAK_FP16 = 2516.6  # TFLOP/s dense
 PEAK_INT8 = 5033.2  # TOP/s dense
 PEAK_HBM = 8000.0   # GB/s
+# VALU lane-operations per second: 256 CUs × 4 SIMDs × 16 lanes × 2.4 GHz.
+PEAK_VALU = 256 * 4 * 16 * 2.4e9
+# TOP/s at which a W8A8 GEMM with one scale per 32-value block saturates the
+# VALU on its fold alone (2 operations per output element and block, each
+# worth 64 int8 operations of the product): 64 / 2 · PEAK_VALU.
+VALU_FOLD_CEILING = 64 / 2 * PEAK_VALU / 1e12
 
 
 def log(msg):
@@ -296,6 +303,9 @@ def extra_vision(iters):
     return out
 
 
+_MOE_STATE = {}  # the expert weights and routing, for the CPU baseline of the same workload
+
+
 def extra_moe(iters):
     c = synth.MOE
     S, H, E, K, I = c["s"], c["hidden"], c["experts"], c["top_k"], c["inter"]
@@ -305,9 +315,9 @@ def extra_moe(iters):
     up = synth.normal_f32(seeds[3], (E, I, H), 0.02)
     down = synth.normal_f32(seeds[4], (E, H, I), 0.02)
     wid = rk.pack_moe_f32(gate, up, down)
-    del gate, up, down
     x = synth.normal_f32(seeds[0], (S, H))
     ids, wts = rk.moe_route(synth.normal_f32(seeds[1], (S, E)), K)
+    _MOE_STATE.update(gate=gate, up=up, down=down, x=x, ids=ids, wts=wts)
     lib = rk.lib()
     import ctypes
     plan = ctypes.c_void_p()
@@ -325,6 +335,30 @@ def extra_moe(iters):
                         "gbps_algorithmic": (weight_bytes + act_bytes) / ms / 1e6,
                         "frac_hbm": (weight_bytes + act_bytes) / ms / 1e6 / PEAK_HBM},
             "attention": att}
+
+
+def extra_w8a8_forms(layers, iters):
+    """Config 2 in the reference's own W8A8 form (activations quantized per row per
+    32-value group, Σ_g (a_s·w_s)·P_g: matmul_i8 + quantize_i8_rows, ext.rs:1017-1029,
+    1505-1554), and the per-token activation quantizer the headline step runs
+    before its timed region."""
+    lib = rk.lib()
+    out = {}
+    g_ms, q_ms = 0.0, 0.0
+    for L in layers:
+        m, k = L["m"], L["k"]
+        q32, s32 = rk.DeviceBuffer(m * k), rk.DeviceBuffer(m * (k // 32) * 4)
+        call(lib.rk_quantize_rows_dev(L["dx"].ptr, m, k, 32, q32.ptr, s32.ptr, None), "quantize g32")
+        g_ms += time_launches(lambda: call(lib.rk_matmul_w8a8_dev(int(L["wid"]), q32.ptr, s32.ptr, 32, m, k,
+                                                                  L["dc"].ptr, None), "w8a8 g32"), iters)
+        q_ms += time_launches(lambda: call(lib.rk_quantize_rows_dev(L["dx"].ptr, m, k, k, L["dq"].ptr, L["ds"].ptr,
+                                                                    None), "quantize"), iters)
+    m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]
+    ops = 2 * 2.0 * m * h * i
+    out["group32_pair"] = {"ms": g_ms, "tops": ops / g_ms / 1e9, "frac_int8_peak": ops / g_ms / 1e9 / PEAK_INT8}
+    x_bytes = 4.0 * m * (h + i)
+    out["per_token_quantizer_both_inputs"] = {"ms": q_ms, "gbps": (x_bytes + x_bytes / 4) / q_ms / 1e6}
+    return out
 
 
 def extra_glue(iters):
@@ -388,44 +422,164 @@ def extra_glue(iters):
 
 
 # --------------------------------------------------------- CPU baseline ----
-def cpu_baseline(layers, budget_s):
-    """The reference's W8A8 formula (emu_matmul_gw) on the host cores."""
-    sys.path.insert(0, ROOT)
-    import oracle
-    threads = os.cpu_count() or 1
+# The oracle's C restatement of each workload (the Burn flex CPU path cannot be
+# built here), timed on the host cores in the same run: one warm-up call, then
+# timed calls of a bounded sample until the time budget is spent; the median
+# rate is the value, the best is reported beside it (the method of the
+# reference's `gemm` command, src/commands/gemm.rs:76-104). Every workload is
+# timed on all the cores this process may use and on one core.
+def _host_threads():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def _time_cpu(fn, budget_s, min_reps=3, max_reps=40):
+    fn()
+    rates, spent = [], 0.0
+    while (spent < budget_s or len(rates) < min_reps) and len(rates) < max_reps:
+        t = time.perf_counter()
+        work = fn()
+        dt = time.perf_counter() - t
+        rates.append(work / dt)
+        spent += dt
+    rates.sort()
+    return rates[-1], rates[len(rates) // 2], spent, len(rates)
+
+
+def _cpu_row(fn, unit, scale, sample_all, sample_one, budget_s):
+    """fn(threads, one_core) runs one sample and returns its algorithmic work."""
+    threads = _host_threads()
+    b_all, m_all, t_all, n_all = _time_cpu(lambda: fn(threads, False), budget_s)
+    b_one, m_one, t_one, n_one = _time_cpu(lambda: fn(1, True), budget_s)
+    return {"value": m_all / scale, "best": b_all / scale, "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{sample_all}; {n_all} timed runs, {t_all:.1f} s",
+            "single_core": {"value": m_one / scale, "best": b_one / scale, "unit": unit, "cores": 1,
+                            "sample": f"{sample_one}; {n_one} timed runs, {t_one:.1f} s"},
+            "cpu": _cpu_model()}
+
+
+def _spread_rows(n, chunks, width):
+    """`chunks` runs of `width` rows spread evenly over [0, n)."""
+    starts = np.linspace(0, n - width, chunks).round().astype(int)
+    return [(int(a), int(a) + width) for a in starts]
+
+
+def cpu_w8a8(oracle, budget_s):
+    """Config 2: per-token quantize + the emu_matmul_gw formula (src/clef/int8.rs:101-158)."""
     c = synth.W8A8
     s1, s2, s3 = synth.SEEDS["w8a8"]
-    rows = 64
     data = []
     for (k, n, sx, sw) in ((c["hidden"], c["inter"], s1, s2), (c["inter"], c["hidden"], s1 + 1000, s3)):
         x = synth.normal_f32(sx, (c["m"], k))
         w = synth.normal_f32(sw, (n, k), 0.02)
         wq, wd = oracle.q8_0_quantize(w)
         data.append((x, wq, wd.view(np.float16).astype(np.float32), k))
-    # Row chunks of the up- and down-projection, cycling over the M=3633 rows
-    # (whole passes repeat) until about budget_s seconds of CPU work are done.
-    ops_done, t_done, samples = 0.0, 0.0, []
-    r0, rows_done = 0, 0
-    while t_done < budget_s:
-        r1 = min(c["m"], r0 + rows)
-        t = time.perf_counter()
+
+    def fn(threads, one):
+        rows = 192 if one else c["m"]
         ops = 0.0
         for x, wq, ws, k in data:
-            aq, a_s = oracle.quantize_rows(x[r0:r1], k, threads)
+            aq, a_s = oracle.quantize_rows(x[:rows], k, threads)
             oracle.emu_matmul_gw(aq, a_s, k, wq, ws, 32, threads)
-            ops += 2.0 * (r1 - r0) * k * wq.shape[0]
-        dt = time.perf_counter() - t
-        samples.append(ops / dt / 1e12)
-        ops_done += ops
-        t_done += dt
-        rows_done += r1 - r0
-        r0 = 0 if r1 == c["m"] else r1
-        rows = min(rows * 2, 1024)
-    return {"value": ops_done / t_done / 1e12, "unit": "TOP/s", "cores": threads, "kind": "port",
-            "sample": f"{rows_done} rows ({rows_done / c['m']:.1f} passes over M=3633) of the up- and "
-                      f"down-projection: per-token quantize + the emu_matmul_gw formula, OpenMP over rows, "
-                      f"{t_done:.1f} s of CPU time",
-            "best": max(samples), "cpu": _cpu_model()}
+            ops += 2.0 * rows * k * wq.shape[0]
+        return ops
+    return _cpu_row(fn, "TOP/s", 1e12,
+                    f"all {c['m']} rows of the up- and down-projection (per-token quantize + emu_matmul_gw), "
+                    "OpenMP over rows", "192 rows of each projection", budget_s)
+
+
+def cpu_gemm_f16(oracle, budget_s):
+    """Config 1: fp16 inputs, f32 accumulation (src/commands/gemm.rs:79-83)."""
+    c = synth.GEMM_F16
+    s1, s2 = synth.SEEDS["gemm_f16"]
+    a = synth.normal_f16(s1, (c["m"], c["k"]))
+    b = synth.normal_f16(s2, (c["n"], c["k"]), 0.02)
+
+    def fn(threads, one):
+        rows = 48 if one else c["m"]
+        oracle.gemm_f16(a[:rows], b, threads)
+        return 2.0 * rows * c["n"] * c["k"]
+    return _cpu_row(fn, "TFLOP/s", 1e12, f"the whole {c['m']}x{c['k']}x{c['n']} product",
+                    f"48 rows of A", budget_s)
+
+
+def _cpu_attention(oracle, s, h, kv, d, causal, seeds, budget_s, rows_all, rows_one):
+    q = synth.normal_f16(seeds[0], (s, h * d))
+    k = synth.normal_f16(seeds[1], (s, kv * d))
+    v = synth.normal_f16(seeds[2], (s, kv * d))
+    mode = 1 if causal else 0
+
+    def fn(threads, one):
+        chunks = _spread_rows(s, 8, (rows_one if one else rows_all) // 8)
+        fl = 0.0
+        for a, b in chunks:
+            oracle.attention_flex(q[a:b], k, v, h, kv, d, d ** -0.5, 0.0, mode, -1, a, 0, threads)
+            keys = (np.arange(a, b) + 1).sum() if causal else (b - a) * s
+            fl += 4.0 * d * h * keys
+        return fl
+    what = (f"{{}} query rows in 8 runs spread over S={s} (TILE_KV=64 online-softmax flex restatement; "
+            f"FLOPs of the visible keys only)")
+    return _cpu_row(fn, "TFLOP/s", 1e12, what.format(rows_all), what.format(rows_one), budget_s)
+
+
+def cpu_vision(oracle, budget_s):
+    """Config 4: the four fp16 GEMMs on a row sample, and the attention."""
+    c = synth.VISION
+    s, hid, h, d, mlp = c["s"], c["hidden"], c["n_head"], c["d"], c["mlp"]
+    seeds = synth.SEEDS["vision"]
+    x = synth.normal_f16(seeds[0], (s, max(hid, mlp)))
+    ws = [(synth.normal_f16(seeds[1 + i], (n, k), 0.02), k)
+          for i, (n, k) in enumerate(((3 * hid, hid), (hid, hid), (mlp, hid), (hid, mlp)))]
+
+    def fn(threads, one):
+        rows = 16 if one else 256
+        fl = 0.0
+        for w, k in ws:
+            oracle.gemm_f16(np.ascontiguousarray(x[:rows, :k]), w, threads)
+            fl += 2.0 * rows * w.shape[0] * k
+        return fl
+    gemms = _cpu_row(fn, "TFLOP/s", 1e12, "256 of the 2394 rows through qkv, out, fc1 and fc2",
+                     "16 rows through the four GEMMs", budget_s)
+    att = _cpu_attention(oracle, s, h, h, d, False, seeds[6:9], budget_s, 128, 16)
+    return {"gemms": gemms, "attention": att}
+
+
+def cpu_moe(oracle, state, budget_s):
+    """Config 5: the expert FFN of sampled tokens (orc_moe_experts: the reference's
+    EmuWorker arithmetic, group-32 activations), and the 32/4-head attention."""
+    c = synth.MOE
+    S, H, E, K, I = c["s"], c["hidden"], c["experts"], c["top_k"], c["inter"]
+    import concurrent.futures as cf
+    threads = _host_threads()
+
+    def q8(w):  # host Q8_0 of [E, rows, cols] in row chunks on a thread pool
+        w2 = w.reshape(-1, w.shape[-1])
+        q = np.empty(w2.shape, np.int8)
+        dd = np.empty((w2.shape[0], w2.shape[1] // 32), np.float32)
+        bounds = [(r, min(r + 4096, w2.shape[0])) for r in range(0, w2.shape[0], 4096)]
+
+        def job(b):
+            qq, d16 = oracle.q8_0_quantize(w2[b[0]:b[1]])
+            q[b[0]:b[1]] = qq
+            dd[b[0]:b[1]] = d16.view(np.float16).astype(np.float32)
+        with cf.ThreadPoolExecutor(max_workers=threads) as ex:
+            list(ex.map(job, bounds))
+        return q.reshape(w.shape), dd.reshape(*w.shape[:-1], -1)
+    (gq, gs), (uq, us), (dq, ds) = q8(state["gate"]), q8(state["up"]), q8(state["down"])
+    x, ids, wts = state["x"], state["ids"], state["wts"]
+    per_tok = 2.0 * K * (2 * I * H + H * I)
+
+    def fn(threads_, one):
+        toks = np.linspace(0, S - 1, 8 if one else 256).round().astype(np.int64)
+        oracle.moe_experts(x[toks], ids[toks], wts[toks], gq, gs, uq, us, dq, ds, threads_)
+        return per_tok * len(toks)
+    experts = _cpu_row(fn, "TOP/s", 1e12, f"256 of the {S} tokens spread over the sequence, all {K} routed experts "
+                       "each", "8 tokens", budget_s)
+    att = _cpu_attention(oracle, S, c["attn_heads"], c["attn_kv"], c["attn_d"], True, synth.SEEDS["moe"][6:9],
+                         budget_s, 128, 16)
+    return {"experts": experts, "attention": att}
 
 
 def _cpu_model():
@@ -445,7 +599,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=1.0,
+                    help="timed CPU seconds per baseline row (all cores, then one core)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the launches the rocprofv3 --pmc byte counts are taken from")
     ap.add_argument("--probe-all", action="store_true",
@@ -481,7 +636,8 @@ def main():
 
     extras = {}
     if not a.no_extras:
-        for key, fn in (("gemm_f16_512x1024x3072", lambda: extra_gemm_f16(200)),
+        for key, fn in (("w8a8_forms_3633", lambda: extra_w8a8_forms(layers, 50)),
+                        ("gemm_f16_512x1024x3072", lambda: extra_gemm_f16(200)),
                         ("gqa_causal_3633", lambda: time_attention(
                             synth.GQA_CAUSAL["s"], synth.GQA_CAUSAL["n_head"], synth.GQA_CAUSAL["n_kv"],
                             synth.GQA_CAUSAL["d"], True, synth.SEEDS["gqa"], 50)),
@@ -493,8 +649,20 @@ def main():
 
     cpu = None
     if not a.no_cpu_baseline:
-        log("CPU baseline")
-        cpu = cpu_baseline(layers, a.cpu_seconds)
+        sys.path.insert(0, ROOT)
+        import oracle
+        budget = a.cpu_seconds
+        log("CPU baseline: W8A8 pair")
+        cpu = cpu_w8a8(oracle, budget)
+        if not a.no_extras:
+            for key, fn in (("gemm_f16_512x1024x3072", lambda: cpu_gemm_f16(oracle, budget)),
+                            ("gqa_causal_3633", lambda: _cpu_attention(
+                                oracle, synth.GQA_CAUSAL["s"], synth.GQA_CAUSAL["n_head"], synth.GQA_CAUSAL["n_kv"],
+                                synth.GQA_CAUSAL["d"], True, synth.SEEDS["gqa"], budget, 256, 32)),
+                            ("vision_layer_2394", lambda: cpu_vision(oracle, budget)),
+                            ("moe_30b_a3b_1024", lambda: cpu_moe(oracle, _MOE_STATE, budget))):
+                log(f"CPU baseline: {key}")
+                extras[key]["cpu_baseline"] = fn()
 
     out = {
         "metric": METRIC,
@@ -511,12 +679,18 @@ def main():
         "data": "synthetic: splitmix64 + Box-Muller normals, seeds " + str(synth.SEEDS["w8a8"]),
         "config": {"workload": "Q8_0/W8A8 MLP GEMMs, M=3633 tokens: up K=1024->N=3072 + down K=3072->N=1024, "
                                "per-token int8 activations, Q8_0 (32-value block) weights, f32 out",
+                   "timed_region": "the two GEMM launches per step on int8 activations already quantized; the "
+                                   "per-token quantizer runs before it (its time: extras.w8a8_forms_3633)",
                    "ops_per_step": 2 * ops_gemm, "sha256_x_up": layers[0]["sha_x"][:16],
                    "sha256_w_up": layers[0]["sha_w"][:16], "wall_s": round(wall, 4)},
         "roofline": {"bound": "mfma", "kernel": "gemm_i8_q8_kernel (up-projection 3633x1024->3072, per-token, f32 out)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8, "unit": "TOP/s",
                      "frac": round(achieved / PEAK_INT8, 4),
                      "frac_of_fp16_peak": round(achieved / PEAK_FP16, 4),
+                     "limiter": "valu: the exact per-32-block scale fold, a convert and an FMA per output "
+                                "element and block",
+                     "ceilings": {"mfma_int8": PEAK_INT8, "valu_fold": round(VALU_FOLD_CEILING, 1)},
+                     "frac_of_valu_fold_ceiling": round(achieved / VALU_FOLD_CEILING, 4),
                      "avg_launch_ms": round(up_ms, 5), "algorithmic_ops_per_launch": ops_gemm,
                      "traffic": load_traffic("w8a8_up")},
         "cpu_baseline": cpu,
