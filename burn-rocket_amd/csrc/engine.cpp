@@ -209,44 +209,6 @@ int upload_block_scales(const std::vector<float> &blk, int64_t n, int64_t kb, fl
   return RK_OK;
 }
 
-float f16_bits_to_f32(uint16_t h) {
-  const uint32_t sign = (uint32_t)(h & 0x8000) << 16;
-  const uint32_t exp = (h >> 10) & 0x1f;
-  uint32_t man = h & 0x3ff;
-  uint32_t bits;
-  if (exp == 0) {
-    if (man == 0) {
-      bits = sign;
-    } else {  // subnormal: renormalise
-      int e = -1;
-      do {
-        ++e;
-        man <<= 1;
-      } while ((man & 0x400) == 0);
-      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3ff) << 13);
-    }
-  } else if (exp == 31) {
-    bits = sign | 0x7f800000u | (man << 13);
-  } else {
-    bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
-  }
-  float f;
-  std::memcpy(&f, &bits, 4);
-  return f;
-}
-
-// Parse [n][k/32] GGUF Q8_0 blocks into codes [n][k] and scales [n][k/32].
-void parse_q8_0(const uint8_t *blocks, int64_t n, int64_t k, int8_t *codes, float *scales) {
-  const int64_t kb = k / 32;
-  for (int64_t r = 0; r < n; ++r)
-    for (int64_t b = 0; b < kb; ++b) {
-      const uint8_t *blk = blocks + (r * kb + b) * 34;
-      const uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
-      scales[r * kb + b] = f16_bits_to_f32(d);
-      std::memcpy(codes + r * k + b * 32, blk + 2, 32);
-    }
-}
-
 int pack_f16_dev(const void *src_f16_dev, int64_t n, int64_t k, uint64_t *id) {
   Weight w;
   w.kind = RK_WEIGHT_F16;
@@ -499,14 +461,47 @@ extern "C" int rk_rewrite_i8(rk_weight_id id, const int8_t *codes, const float *
   return RK_OK;
 }
 
+namespace {
+// Resident Q8_0 weight of `rows` rows from GGUF blocks that are uploaded once and
+// split into codes and f32 scales on the device. Each (blocks, grp_off) source
+// lands at rows (r/16)·grp_stride + grp_off + r%16; other rows stay zero.
+int pack_q8_0_blocks(CallScope &cs, const uint8_t *const *srcs, const int *grp_offs, int nsrc,
+                     int64_t n, int64_t k, int64_t rows, int grp_stride, Weight &wt,
+                     const char *op) {
+  wt.kind = RK_WEIGHT_I8;
+  wt.n = rows;
+  wt.k = k;
+  wt.group = 32;
+  wt.ws_stride = ws_stride_for(k);
+  const size_t blk_bytes = (size_t)n * (k / 32) * 34;
+  void *dblk;
+  RK_TRY(scratch(cs, "pack_blk", blk_bytes, &dblk));
+  HIP_TRY(hipMalloc(&wt.codes, (size_t)rows * k), op);
+  HIP_TRY(hipMalloc((void **)&wt.scales, (size_t)rows * wt.ws_stride * 4), op);
+  HIP_TRY(hipMemsetAsync(wt.codes, 0, (size_t)rows * k, cs.st), op);
+  HIP_TRY(hipMemsetAsync(wt.scales, 0, (size_t)rows * wt.ws_stride * 4, cs.st), op);
+  for (int i = 0; i < nsrc; ++i) {
+    HIP_TRY(hipMemcpyAsync(dblk, srcs[i], blk_bytes, hipMemcpyHostToDevice, cs.st), op);
+    HIP_TRY(rk_launch_q8_0_unpack(dblk, n, k, grp_stride, grp_offs[i], (int8_t *)wt.codes, wt.scales,
+                                  wt.ws_stride, false, cs.st),
+            op);
+  }
+  HIP_TRY(hipStreamSynchronize(cs.st), op);
+  wt.bytes = (size_t)rows * k + (size_t)rows * wt.ws_stride * 4;
+  return RK_OK;
+}
+}  // namespace
+
 extern "C" int rk_pack_q8_0(const uint8_t *blocks, int64_t n, int64_t k, rk_weight_id *id) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_pack_q8_0"));
   RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0"));
-  std::vector<int8_t> codes((size_t)n * k);
-  std::vector<float> scales((size_t)n * (k / 32));
-  parse_q8_0(blocks, n, k, codes.data(), scales.data());
-  return pack_i8_host(codes.data(), scales, n, k, 32, id, "rk_pack_q8_0");
+  CallScope cs(g_eng->stream);
+  Weight wt;
+  const int off = 0;
+  RK_TRY(pack_q8_0_blocks(cs, &blocks, &off, 1, n, k, n, 16, wt, "rk_pack_q8_0"));
+  *id = insert(wt);
+  return RK_OK;
 }
 
 extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_id *id) {
@@ -549,19 +544,13 @@ extern "C" int rk_pack_q8_0_glu(const uint8_t *gate_blocks, const uint8_t *up_bl
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_pack_q8_0_glu"));
   RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_glu"));
-  const int64_t rows = glu_rows(n), kb = k / 32;
-  std::vector<int8_t> codes((size_t)n * k), all((size_t)rows * k, 0);
-  std::vector<float> scales((size_t)n * kb), all_s((size_t)rows * kb, 0.f);
-  for (int part = 0; part < 2; ++part) {
-    parse_q8_0(part ? up_blocks : gate_blocks, n, k, codes.data(), scales.data());
-    for (int64_t r = 0; r < n; ++r) {
-      const int64_t d = glu_row(r, part);
-      memcpy(&all[d * k], &codes[r * k], (size_t)k);
-      memcpy(&all_s[d * kb], &scales[r * kb], (size_t)kb * 4);
-    }
-  }
-  RK_TRY(pack_i8_host(all.data(), all_s, rows, k, 32, id, "rk_pack_q8_0_glu"));
-  g_eng->weights[*id].glu_n = n;
+  CallScope cs(g_eng->stream);
+  Weight wt;
+  const uint8_t *srcs[2] = {gate_blocks, up_blocks};
+  const int offs[2] = {0, 16};  // gate rows at 32t + j, up rows at 32t + 16 + j
+  RK_TRY(pack_q8_0_blocks(cs, srcs, offs, 2, n, k, glu_rows(n), 32, wt, "rk_pack_q8_0_glu"));
+  wt.glu_n = n;
+  *id = insert(wt);
   return RK_OK;
 }
 
@@ -1171,83 +1160,7 @@ namespace {
 int64_t moe_gu_code_stride(const Weight &w) { return 2 * w.inter * w.gu_ws_stride * 32; }
 int64_t moe_dn_code_stride(const Weight &w) { return w.hidden * w.dn_ws_stride * 32; }
 
-// Row-major codes [n, k] and scales [n, ws_stride] → fragment-major.
-void to_fragment_major(const int8_t *codes, const float *scales, int64_t n, int64_t k,
-                       int ws_stride, int8_t *fcodes, float *fscales) {
-  std::fill(fcodes, fcodes + n * ws_stride * 32, (int8_t)0);
-  std::fill(fscales, fscales + n * ws_stride, 0.f);
-  for (int64_t r = 0; r < n; ++r)
-    for (int64_t b = 0; b < k / 32; ++b) {
-      for (int j = 0; j < 32; ++j)
-        fcodes[q8_code_offset(r, b, j, k, ws_stride, 1)] = codes[r * k + b * 32 + j];
-      fscales[q8_scale_offset(r, b, ws_stride, 1)] = scales[r * ws_stride + b];
-    }
-}
 }  // namespace
-
-extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
-                                int n_experts, int64_t hidden, int64_t inter, rk_weight_id *id) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  RK_TRY(ensure("rk_pack_moe_q8_0"));
-  if (n_experts <= 0 || hidden <= 0 || inter <= 0 || hidden % 32 || inter % 32)
-    return fail(RK_E_SHAPE, "rk_pack_moe_q8_0", "hidden and inter must be multiples of 32");
-  const int64_t H = hidden, I = inter, E = n_experts;
-  Weight w;
-  w.moe = true;
-  w.n_experts = n_experts;
-  w.hidden = H;
-  w.inter = I;
-  w.n = H;
-  w.k = H;
-  w.group = 32;
-  w.gu_ws_stride = ws_stride_for(H);
-  w.dn_ws_stride = ws_stride_for(I);
-  const size_t gu_codes = (size_t)E * moe_gu_code_stride(w), dn_codes = (size_t)E * moe_dn_code_stride(w);
-  const size_t gu_sc = (size_t)E * 2 * I * w.gu_ws_stride, dn_sc = (size_t)E * H * w.dn_ws_stride;
-  HIP_TRY(hipMalloc((void **)&w.gu_codes, gu_codes), "rk_pack_moe_q8_0");
-  HIP_TRY(hipMalloc((void **)&w.dn_codes, dn_codes), "rk_pack_moe_q8_0");
-  HIP_TRY(hipMalloc((void **)&w.gu_scales, gu_sc * 4), "rk_pack_moe_q8_0");
-  HIP_TRY(hipMalloc((void **)&w.dn_scales, dn_sc * 4), "rk_pack_moe_q8_0");
-  w.bytes = gu_codes + dn_codes + (gu_sc + dn_sc) * 4;
-  // Per expert: parse gate/up/down, interleave gate|up per 16-row slice.
-  std::vector<int8_t> gc(I * H), uc(I * H), dc(H * I), guc(2 * I * H);
-  std::vector<float> gs(I * (H / 32)), us(I * (H / 32)), ds(H * (I / 32));
-  std::vector<float> gus((size_t)2 * I * w.gu_ws_stride), dss((size_t)H * w.dn_ws_stride);
-  std::vector<int8_t> guf(moe_gu_code_stride(w)), dnf(moe_dn_code_stride(w));
-  std::vector<float> gusf(gus.size()), dssf(dss.size());
-  const size_t gblk = (size_t)I * (H / 32) * 34, dblk = (size_t)H * (I / 32) * 34;
-  for (int64_t e = 0; e < E; ++e) {
-    parse_q8_0(gate + e * gblk, I, H, gc.data(), gs.data());
-    parse_q8_0(up + e * gblk, I, H, uc.data(), us.data());
-    parse_q8_0(down + e * dblk, H, I, dc.data(), ds.data());
-    std::fill(gus.begin(), gus.end(), 0.f);
-    std::fill(dss.begin(), dss.end(), 0.f);
-    for (int64_t r = 0; r < I; ++r) {
-      const int64_t t = r / 16, j = r % 16;
-      const int64_t rg = 32 * t + j, ru = 32 * t + 16 + j;
-      std::memcpy(&guc[rg * H], &gc[r * H], H);
-      std::memcpy(&guc[ru * H], &uc[r * H], H);
-      std::memcpy(&gus[rg * w.gu_ws_stride], &gs[r * (H / 32)], 4 * (H / 32));
-      std::memcpy(&gus[ru * w.gu_ws_stride], &us[r * (H / 32)], 4 * (H / 32));
-    }
-    for (int64_t r = 0; r < H; ++r)
-      std::memcpy(&dss[r * w.dn_ws_stride], &ds[r * (I / 32)], 4 * (I / 32));
-    to_fragment_major(guc.data(), gus.data(), 2 * I, H, w.gu_ws_stride, guf.data(), gusf.data());
-    to_fragment_major(dc.data(), dss.data(), H, I, w.dn_ws_stride, dnf.data(), dssf.data());
-    HIP_TRY(hipMemcpy(w.gu_codes + e * guf.size(), guf.data(), guf.size(), hipMemcpyHostToDevice),
-            "rk_pack_moe_q8_0");
-    HIP_TRY(hipMemcpy(w.dn_codes + e * dnf.size(), dnf.data(), dnf.size(), hipMemcpyHostToDevice),
-            "rk_pack_moe_q8_0");
-    HIP_TRY(hipMemcpy(w.gu_scales + e * 2 * I * w.gu_ws_stride, gusf.data(), gusf.size() * 4,
-                      hipMemcpyHostToDevice),
-            "rk_pack_moe_q8_0");
-    HIP_TRY(hipMemcpy(w.dn_scales + e * H * w.dn_ws_stride, dssf.data(), dssf.size() * 4,
-                      hipMemcpyHostToDevice),
-            "rk_pack_moe_q8_0");
-  }
-  *id = insert(w);
-  return RK_OK;
-}
 
 namespace {
 int moe_alloc(Weight &w, int n_experts, int64_t H, int64_t I, const char *op) {
@@ -1276,6 +1189,42 @@ int moe_alloc(Weight &w, int n_experts, int64_t H, int64_t I, const char *op) {
   return RK_OK;
 }
 }  // namespace
+
+extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const uint8_t *down,
+                                int n_experts, int64_t hidden, int64_t inter, rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_pack_moe_q8_0";
+  RK_TRY(ensure(op));
+  if (n_experts <= 0 || hidden <= 0 || inter <= 0 || hidden % 32 || inter % 32)
+    return fail(RK_E_SHAPE, op, "hidden and inter must be multiples of 32");
+  const int64_t H = hidden, I = inter, E = n_experts;
+  Weight w;
+  RK_TRY(moe_alloc(w, n_experts, H, I, op));
+  CallScope cs(g_eng->stream);
+  hipStream_t st = cs.st;
+  // Per expert: one upload of its gate, up and down blocks, split on the device
+  // into the fragment-major stacks (gate|up interleaved per 16-row slice).
+  const size_t gblk = (size_t)I * (H / 32) * 34, dblk = (size_t)H * (I / 32) * 34;
+  void *dev;
+  RK_TRY(scratch(cs, "pack_blk", 2 * gblk + dblk, &dev));
+  uint8_t *dg = (uint8_t *)dev, *du = dg + gblk, *dd = du + gblk;
+  const int64_t gu_stride = moe_gu_code_stride(w), dn_stride = moe_dn_code_stride(w);
+  for (int64_t e = 0; e < E; ++e) {
+    HIP_TRY(hipMemcpyAsync(dg, gate + e * gblk, gblk, hipMemcpyHostToDevice, st), op);
+    HIP_TRY(hipMemcpyAsync(du, up + e * gblk, gblk, hipMemcpyHostToDevice, st), op);
+    HIP_TRY(hipMemcpyAsync(dd, down + e * dblk, dblk, hipMemcpyHostToDevice, st), op);
+    int8_t *guc = w.gu_codes + e * gu_stride;
+    float *gus = w.gu_scales + e * 2 * I * w.gu_ws_stride;
+    HIP_TRY(rk_launch_q8_0_unpack(dg, I, H, 32, 0, guc, gus, w.gu_ws_stride, true, st), op);
+    HIP_TRY(rk_launch_q8_0_unpack(du, I, H, 32, 16, guc, gus, w.gu_ws_stride, true, st), op);
+    HIP_TRY(rk_launch_q8_0_unpack(dd, H, I, 16, 0, w.dn_codes + e * dn_stride,
+                                  w.dn_scales + e * H * w.dn_ws_stride, w.dn_ws_stride, true, st),
+            op);
+  }
+  HIP_TRY(hipStreamSynchronize(st), op);
+  *id = insert(w);
+  return RK_OK;
+}
 
 extern "C" int rk_pack_moe_f32(const float *gate, const float *up, const float *down, int n_experts,
                                int64_t hidden, int64_t inter, rk_weight_id *id) {

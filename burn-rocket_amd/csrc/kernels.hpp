@@ -99,6 +99,12 @@ hipError_t rk_launch_q8_0_quantize(const float *w, int64_t n, int64_t k, int grp
                                    int grp_off, int8_t *codes, float *scales, int ws_stride,
                                    bool frag, hipStream_t st);
 
+// GGUF Q8_0 blocks [n][k/32] of 34 bytes (f16 d, 32 int8 codes), resident on
+// the device (2-byte aligned), split into the layout rk_launch_q8_0_quantize
+// writes for the same row remap and `frag` choice; d is widened to f32 exactly.
+hipError_t rk_launch_q8_0_unpack(const void *blocks, int64_t n, int64_t k, int grp_stride,
+                                 int grp_off, int8_t *codes, float *scales, int ws_stride,
+                                 bool frag, hipStream_t st);
 // Fragment-major Q8_0 layout of the MoE expert weights: per 32-row block
 // (r/32) and 128-value stage (b/4), 4 KB of codes [block b%4][lane][16 bytes]
 // with lane 32·h + r%32 holding values 16h..16h+15 of block b of row r, and

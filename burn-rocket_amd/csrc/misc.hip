@@ -273,6 +273,47 @@ hipError_t rk_launch_q8_0_quantize(const float *w, int64_t n, int64_t k, int grp
   return hipGetLastError();
 }
 
+// GGUF Q8_0 blocks (34 bytes: f16 d little-endian, then 32 int8 codes;
+// src/util/gguf.rs:125-200) already on the device → codes and f32 scales in
+// the layout rk_launch_q8_0_quantize writes (rows remapped the same way). One
+// thread per block; blocks are 2-byte aligned, so they are read as 16-bit words.
+__device__ __forceinline__ float f16_bits_to_f32_exact(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0x1fu) return __uint_as_float(sign | 0x7f800000u | (m << 13));
+  if (e != 0) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+  // zero or subnormal: m·2^-24, exact in f32
+  return __uint_as_float(sign) + (sign ? -1.0f : 1.0f) * (float)m * 5.9604644775390625e-08f;
+}
+
+__global__ void q8_0_unpack_kernel(const uint16_t *__restrict__ blocks, int64_t n, int64_t k,
+                                   int grp_stride, int grp_off, int8_t *__restrict__ codes,
+                                   float *__restrict__ scales, int ws_stride, int frag) {
+  const int64_t nb = k / 32;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * nb) return;
+  const int64_t r = i / nb, b = i % nb;
+  const uint16_t *blk = blocks + i * 17;  // 34 bytes = 17 16-bit words
+  uint32_t w[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w[j] = (uint32_t)blk[1 + 2 * j] | ((uint32_t)blk[2 + 2 * j] << 16);
+  const int64_t dr = (r / 16) * grp_stride + grp_off + (r % 16);
+  // codes 0..15 and 16..31 are each 16 contiguous bytes in both layouts
+  *(uintx4 *)(codes + q8_code_offset(dr, b, 0, k, ws_stride, frag)) = uintx4{w[0], w[1], w[2], w[3]};
+  *(uintx4 *)(codes + q8_code_offset(dr, b, 16, k, ws_stride, frag)) = uintx4{w[4], w[5], w[6], w[7]};
+  scales[q8_scale_offset(dr, b, ws_stride, frag)] = f16_bits_to_f32_exact(blk[0]);
+}
+
+hipError_t rk_launch_q8_0_unpack(const void *blocks, int64_t n, int64_t k, int grp_stride,
+                                 int grp_off, int8_t *codes, float *scales, int ws_stride,
+                                 bool frag, hipStream_t st) {
+  const int64_t total = n * (k / 32);
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(q8_0_unpack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                     (const uint16_t *)blocks, n, k, grp_stride, grp_off, codes, scales, ws_stride,
+                     (int)frag);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // MLP glue: out = silu(gate)·up or gelu_tanh(gate)·up elementwise
 // (rocket_silu_mul / rocket_gelu_mul, ext.rs:603-608 and 1057-1090, with the

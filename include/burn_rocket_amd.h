@@ -150,7 +150,9 @@ int rk_pack_i8_codes(const int8_t *codes, const float *scales, int64_t n,
  * (`I8Context::rewrite_weight_gw`, int8.rs:521). */
 int rk_rewrite_i8(rk_weight_id id, const int8_t *codes, const float *scales);
 /* GGUF Q8_0 weight: [N, K/32] blocks of 34 bytes {f16 d, int8 q[32]}
- * (src/util/gguf.rs:125-200). Stored as codes + f32(d), group 32. */
+ * (src/util/gguf.rs:125-200), e.g. a pointer into an mmapped GGUF tensor. The
+ * blocks cross PCIe once, as they are, and are split on the GPU into codes
+ * [N, K] and f32(d) scales (exact, f16 subnormals included); group 32. */
 int rk_pack_q8_0(const uint8_t *blocks, int64_t n, int64_t k, rk_weight_id *id);
 /* GGUF Q8_0 weight quantized on the device from f32 [N, K] with llama.cpp's
  * rule (crates/rocket-npu/src/bin/q8_bench.rs:200-220): per 32 values
@@ -297,7 +299,9 @@ int rk_moe_route(const float *logits, int64_t s, int n_experts, int top_k,
 
 /* Resident expert stack: n_experts Q8_0 expert FFNs, each gate [inter, hidden],
  * up [inter, hidden], down [hidden, inter], as GGUF Q8_0 blocks
- * (src/clef/engine_npu.rs:110-207 packs gate|up and down per expert). */
+ * (src/clef/engine_npu.rs:110-207 packs gate|up and down per expert). Each
+ * expert's blocks are uploaded as they are and split on the GPU into the
+ * fragment-major layout the expert kernels stream. */
 int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up,
                      const uint8_t *down, int n_experts, int64_t hidden,
                      int64_t inter, rk_weight_id *id);

@@ -251,6 +251,36 @@ def test_device_q8_0_packer_equals_gguf_blocks(rk, orc):
     assert (s2 == (wq.astype(np.float32) * np.repeat(d32, 32, axis=1)).T).all()
 
 
+def test_q8_0_blocks_split_on_the_device_keep_every_scale_exactly(rk, orc):
+    # rk_pack_q8_0 uploads the 34-byte GGUF blocks once and splits them into
+    # codes and f32 scales on the GPU (src/util/gguf.rs:125-200). Block scales
+    # cover f16 subnormals, ±0, the largest finite value and negative values;
+    # codes are random int8. One-hot activations with unit scale return
+    # d·code exactly (an f16 times an int8 is exact in f32).
+    note("device Q8_0 unpack: special scales")
+    r = np.random.default_rng(31)
+    n, k = 40, 256
+    q = r.integers(-127, 128, (n, k), dtype=np.int8)
+    d16 = (r.uniform(1e-4, 2.0, (n, k // 32))).astype(np.float16).view(np.uint16)
+    special = np.array([0x0000, 0x8000, 0x0001, 0x03ff, 0x0200, 0x7bff, 0xbc00, 0x8001, 0x3c00], np.uint16)
+    d16.reshape(-1)[:special.size] = special
+    blocks = orc.q8_0_blocks(q, d16)
+    wid = rk.pack_q8_0(blocks, n, k)
+    eye = np.zeros((k, k), np.int8)
+    np.fill_diagonal(eye, 1)
+    assert (raw_dev(rk, wid, eye) == q.T.astype(np.int32)).all()
+    dq, ds = dev(rk, eye), dev(rk, np.ones((k, 1), np.float32))
+    got = w8a8_dev(rk, wid, dq, ds, k, k, k)
+    want = (q.astype(np.float32) * np.repeat(orc.f16_to_f32(d16), 32, axis=1)).T
+    assert (got == want).all()  # ±0 compare equal: the fold starts from +0
+    # and through the real W8A8 path against the oracle's decode of the same blocks
+    x = r.standard_normal((64, k)).astype(np.float32)
+    aq, a_s = orc.quantize_rows(x, k)
+    dqx, dsx = quantize_dev(rk, x, k)
+    ref = orc.emu_matmul_gw(aq, a_s, k, q, orc.f16_to_f32(d16), 32)
+    assert np.abs(w8a8_dev(rk, wid, dqx, dsx, k, 64, k) - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
 # Fused gate|up GEMM with the MLP glue in the epilogue: glue(gate·x, up·x)
 # against the oracle's two W8A8 products and its glue (host.rs:12-39).
 # Shapes select each tile configuration of the fused launch on a 256-CU
