@@ -418,6 +418,27 @@ def extra_glue(iters):
     ops = 2.0 * m * hid * 2 * inter
     out["w8a8_gate_up_silu_3633x1024x2x3072"] = {"ms": ms, "tops": ops / ms / 1e9,
                                                  "frac_int8_peak": ops / ms / 1e9 / PEAK_INT8}
+    # fp16 gate|up GEMM with silu·up in its epilogue (f32 out), against the
+    # unfused pair: the gate and up fp16 GEMMs, then silu_mul on their f32-widened outputs
+    x16 = dev(synth.normal_f16(14, (m, hid)).view(np.uint16))
+    wglu = rk.pack_f16_glu(gate, up)
+    ms = time_launches(lambda: call(lib.rk_matmul_f16_glu_dev(int(wglu), x16.ptr, m, hid, 1, o32.ptr, 0, None),
+                                    "f16 glu"), iters)
+    out["f16_gate_up_silu_3633x1024x2x3072"] = {"ms": ms, "tflops": ops / ms / 1e9,
+                                                "frac_fp16_peak": ops / ms / 1e9 / PEAK_FP16}
+    wg, wu = rk.pack(gate), rk.pack(up)
+    cg, cu = rk.DeviceBuffer(m * inter * 2), rk.DeviceBuffer(m * inter * 2)
+    fg, fu = rk.DeviceBuffer(m * inter * 4), rk.DeviceBuffer(m * inter * 4)
+
+    def unfused():
+        call(lib.rk_matmul_f16_dev(int(wg), x16.ptr, m, hid, cg.ptr, None), "f16")
+        call(lib.rk_matmul_f16_dev(int(wu), x16.ptr, m, hid, cu.ptr, None), "f16")
+        call(lib.rk_cast_dev(cg.ptr, rk.DTYPE_F16, fg.ptr, rk.DTYPE_F32, m * inter, None), "widen")
+        call(lib.rk_cast_dev(cu.ptr, rk.DTYPE_F16, fu.ptr, rk.DTYPE_F32, m * inter, None), "widen")
+        call(lib.rk_silu_mul_dev(fg.ptr, fu.ptr, o32.ptr, m * inter, rk.DTYPE_F32, None), "silu")
+    ms_u = time_launches(unfused, iters)
+    out["f16_gate_up_silu_unfused_pair"] = {"ms": ms_u, "tflops": ops / ms_u / 1e9,
+                                            "what": "two fp16 GEMMs, two f16->f32 widenings, silu_mul f32"}
     return out
 
 

@@ -53,6 +53,8 @@ SIGNATURES = {
     "rk_weight_info": (_i, [_u64, _p, _p, _p, _p]),
     "rk_matmul": (_i, [_u64, _p, _i64, _i64, _p]),
     "rk_matmul_f16_dev": (_i, [_u64, _p, _i64, _i64, _p, _p]),
+    "rk_pack_f16_glu": (_i, [_p, _p, _i64, _i64, _p]),
+    "rk_matmul_f16_glu_dev": (_i, [_u64, _p, _i64, _i64, _i, _p, _i, _p]),
     "rk_quantize_rows_dev": (_i, [_p, _i64, _i64, _i64, _p, _p, _p]),
     "rk_matmul_w8a8_dev": (_i, [_u64, _p, _p, _i64, _i64, _i64, _p, _p]),
     "rk_matmul_w8a8_f16out_dev": (_i, [_u64, _p, _p, _i64, _i64, _i64, _p, _p]),
@@ -97,6 +99,7 @@ SIGNATURES = {
     "rk_rms_norm_noscale": (_i, [_p, _p, _i64, _i64, _c.c_double]),
     "rk_rope": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64]),
     "rk_memset_dev": (_i, [_p, _i, _sz]),
+    "rk_cast_dev": (_i, [_p, _i, _p, _i, _i64, _p]),
     "rk_stream_get": (_i, [_p]),
     "rk_stream_sync": (_i, [_p]),
     "rk_stream_create": (_i, [_p]),
@@ -263,6 +266,16 @@ def pack_q8_0_glu_f32(gate, up):
     n, k = g.shape
     out = ctypes.c_uint64()
     _check(_lib.rk_pack_q8_0_glu_f32(_ptr(g), _ptr(u), n, k, ctypes.byref(out)), "rocket_q8_0_glu_pack", 0, k, n)
+    return WeightId(out.value)
+
+
+def pack_f16_glu(gate, up):
+    """fp16 gate|up weight for rk_matmul_f16_glu_dev from f32 gate, up [n, k]."""
+    g, u = _f32(gate), _f32(up)
+    assert g.shape == u.shape and g.ndim == 2
+    n, k = g.shape
+    out = ctypes.c_uint64()
+    _check(_lib.rk_pack_f16_glu(_ptr(g), _ptr(u), n, k, ctypes.byref(out)), "rocket_weights_pack_glu", 0, k, n)
     return WeightId(out.value)
 
 

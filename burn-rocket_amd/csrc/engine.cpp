@@ -590,6 +590,36 @@ extern "C" int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t 
   return RK_OK;
 }
 
+// fp16 gate|up weight for rk_matmul_f16_glu_dev: rows interleaved per 16 as
+// rk_pack_q8_0_glu lays them out, padding rows zero.
+extern "C" int rk_pack_f16_glu(const float *gate, const float *up, int64_t n, int64_t k,
+                               rk_weight_id *id) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_pack_f16_glu";
+  RK_TRY(ensure(op));
+  RK_TRY(check_f16_shape(n, k, op));
+  if (!gate || !up) return fail(RK_E_SHAPE, op, "null weight");
+  CallScope cs(g_eng->stream);
+  const int64_t rows = glu_rows(n);
+  Weight w;
+  w.kind = RK_WEIGHT_F16;
+  w.n = rows;
+  w.k = k;
+  w.glu_n = n;
+  w.bytes = (size_t)rows * k * 2;
+  void *x32;
+  RK_TRY(scratch(cs, "pack_f32", (size_t)n * k * 4, &x32));
+  HIP_TRY(hipMalloc(&w.codes, w.bytes), op);
+  HIP_TRY(hipMemsetAsync(w.codes, 0, w.bytes, cs.st), op);
+  for (int part = 0; part < 2; ++part) {
+    HIP_TRY(hipMemcpyAsync(x32, part ? up : gate, (size_t)n * k * 4, hipMemcpyHostToDevice, cs.st), op);
+    HIP_TRY(rk_launch_f32_to_f16_rows((const float *)x32, n, k, 32, 16 * part, w.codes, cs.st), op);
+  }
+  HIP_TRY(hipStreamSynchronize(cs.st), op);
+  *id = insert(w);
+  return RK_OK;
+}
+
 extern "C" int rk_pack_qat(const int8_t *codes, const float *w_scale, int64_t n, int64_t k,
                            float in_scale, float out_scale, rk_weight_id *id) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -733,9 +763,28 @@ extern "C" int rk_matmul_f16_dev(rk_weight_id id, const void *a, int64_t m, int6
   RK_TRY(check_m(m, k, w, "rk_matmul_f16_dev"));
   if (w->kind != RK_WEIGHT_F16 || w->moe)
     return fail(RK_E_UNSUPPORTED, "rk_matmul_f16_dev", "weight is not fp16");
+  if (w->glu_n > 0)
+    return fail(RK_E_UNSUPPORTED, "rk_matmul_f16_dev", "gate|up weight: use rk_matmul_f16_glu_dev");
   HIP_TRY(rk_launch_gemm_f16(a, w->codes, c, (int)m, (int)w->n, (int)k, g_eng->num_cus,
                              pick(stream)),
           "rk_matmul_f16_dev");
+  g_eng->calls++;
+  return RK_OK;
+}
+
+extern "C" int rk_matmul_f16_glu_dev(rk_weight_id id, const void *a, int64_t m, int64_t k, int glu,
+                                     void *out, int out_f16, rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_matmul_f16_glu_dev";
+  RK_TRY(ensure(op));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, op));
+  if (w->kind != RK_WEIGHT_F16 || w->moe || w->glu_n <= 0)
+    return fail(RK_E_UNSUPPORTED, op, "weight was not packed by rk_pack_f16_glu");
+  if (glu != RK_GLU_SILU && glu != RK_GLU_GELU) return fail(RK_E_SHAPE, op, "unknown glu kind");
+  HIP_TRY(rk_launch_gemm_f16_glu(a, w->codes, out, (int)m, (int)w->n, (int)k, (int)w->glu_n, glu,
+                                 out_f16 != 0, g_eng->num_cus, pick(stream)),
+          op);
   g_eng->calls++;
   return RK_OK;
 }
@@ -1770,6 +1819,19 @@ extern "C" int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_strea
   HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice,
                          stream ? (hipStream_t)stream : g_eng->stream),
           "rk_memcpy_dtod");
+  return RK_OK;
+}
+extern "C" int rk_cast_dev(const void *x, int x_dtype, void *y, int y_dtype, int64_t n,
+                           rk_stream stream) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_cast_dev";
+  RK_TRY(ensure(op));
+  if (n < 0) return fail(RK_E_SHAPE, op, "negative element count");
+  if (x_dtype < RK_DTYPE_F32 || x_dtype > RK_DTYPE_BF16 || y_dtype < RK_DTYPE_F32 ||
+      y_dtype > RK_DTYPE_BF16)
+    return fail(RK_E_SHAPE, op, "unknown dtype");
+  if (n > 0 && (!x || !y)) return fail(RK_E_SHAPE, op, "null buffer");
+  HIP_TRY(rk_launch_cast(x, x_dtype, y, y_dtype, n, pick(stream)), op);
   return RK_OK;
 }
 extern "C" int rk_memset_dev(void *dst, int value, size_t bytes) {

@@ -38,10 +38,30 @@ constexpr int KS = 64;    // K values per stage
 constexpr int ROWB = 128;  // bytes per LDS row of one stage
 }  // namespace
 
-template <int BM, int BN, int WM, int WN, int ST, int MINW>
+// MLP glue of a gate|up product, in f32 in the reference's operation order
+// with no FMA contraction (host.rs:12-39): 1 silu(g)·u, 2 gelu_tanh(g)·u.
+template <int GLU>
+__device__ __forceinline__ float f16_glu(float g, float u) {
+#pragma clang fp contract(off)
+  if constexpr (GLU == 1) {
+    const float sigmoid = 1.0f / (1.0f + expf(-g));
+    return g * sigmoid * u;
+  } else {
+    constexpr float k = (float)(1.12837916709551257390 * 0.70710678118654752440);  // sqrt(2/pi)
+    const float inner = (g + g * g * g * 0.044715f) * k;
+    return ((g * (tanhf(inner) + 1.0f)) * 0.5f) * u;
+  }
+}
+
+// GLU = 0: C [M, N] fp16. GLU = 1 / 2: B holds gate and up rows interleaved
+// per 16 (rows 32t..32t+15 gate rows 16t.., rows 32t+16.. the matching up
+// rows), so tiles j (even) and j+1 of a lane hold gate and up of the same
+// outputs; each is rounded to fp16 as the plain GEMM's output would be, the
+// glue runs in f32, and C is [M, n_out] f32 (OUT_F16: fp16).
+template <int BM, int BN, int WM, int WN, int ST, int MINW, int GLU = 0, bool OUT_F16 = true>
 __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
-    const f16 *__restrict__ A, const f16 *__restrict__ B, f16 *__restrict__ C, int M, int N, int K,
-    int tiles_m, int tiles_n, int group_m) {
+    const f16 *__restrict__ A, const f16 *__restrict__ B, void *__restrict__ Cv, int M, int N, int K,
+    int tiles_m, int tiles_n, int group_m, int n_out) {
   constexpr int NW = WM * WN;
   constexpr int STAGE = (BM + BN) * ROWB;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -175,6 +195,46 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   WAIT_VMCNT(0);  // no copy may still be writing LDS when the workgroup ends
 
   // Epilogue: lane holds C[row lane%16][cols 4·(lane/16) + 0..3] of each tile.
+  if constexpr (GLU != 0) {
+    static_assert(TN % 2 == 0 && WTN % 32 == 0, "gate/up tile pairs start at 32-row groups");
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * WTM + i * 16 + frow;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; j += 2) {
+        // output column of element e: 16·(group) + 4·(lane/16) + e
+        const int oc = ((n0 + wn * WTN + j * 16) >> 1) + 4 * (lane >> 4);
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float g = (float)(f16)acc[i][j][e], u = (float)(f16)acc[i][j + 1][e];
+          y[e] = f16_glu<GLU>(g, u);
+        }
+        if constexpr (OUT_F16) {
+          f16 *crow_p = (f16 *)Cv + (size_t)m * n_out;
+          if ((n_out % 4) == 0 && oc + 3 < n_out) {
+            *(half4 *)(crow_p + oc) = half4{(f16)y[0], (f16)y[1], (f16)y[2], (f16)y[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (oc + e < n_out) crow_p[oc + e] = (f16)y[e];
+          }
+        } else {
+          float *crow_p = (float *)Cv + (size_t)m * n_out;
+          if ((n_out % 4) == 0 && oc + 3 < n_out) {
+            *(floatx4 *)(crow_p + oc) = floatx4{y[0], y[1], y[2], y[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (oc + e < n_out) crow_p[oc + e] = y[e];
+          }
+        }
+      }
+    }
+    return;
+  }
+  f16 *C = (f16 *)Cv;
   const bool vec = (N % 4) == 0;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -196,12 +256,12 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int MINW>
-static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, f16 *C, int M, int N, int K,
-                                  hipStream_t st) {
+template <int BM, int BN, int WM, int WN, int ST, int MINW, int GLU = 0, bool OUT_F16 = true>
+static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, void *C, int M, int N, int K,
+                                  hipStream_t st, int n_out = 0) {
   constexpr int smem = ST * (BM + BN) * ROWB;
   static_assert(smem <= 160 * 1024, "LDS per workgroup");
-  auto kern = gemm_f16_kernel<BM, BN, WM, WN, ST, MINW>;
+  auto kern = gemm_f16_kernel<BM, BN, WM, WN, ST, MINW, GLU, OUT_F16>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -215,7 +275,7 @@ static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, f16 *C, int M, int
   // streaming all of A (vision fc2 2394x4304x1152: 40.6 -> 37.3 us on MI355X,
   // 185 MB fetched per launch row-fastest over the whole grid).
   hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, A, B, C, M, N, K, tm, tn,
-                     rk_knob("RK_TILE_GROUP_M", 3));
+                     rk_knob("RK_TILE_GROUP_M", 3), n_out);
   return hipGetLastError();
 }
 
@@ -262,14 +322,20 @@ hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, i
   return hipErrorInvalidValue;
 }
 
+// The configurations whose waves hold whole 32-row gate|up groups (BN/WN a
+// multiple of 32), the ones the glue epilogue is instantiated for.
+constexpr int F16_GLU_CFGS[] = {0, 1, 2, 3, 4, 8};
+
 // Choose the configuration with the least estimated time: rounds of
 // workgroups over the CUs, each round a fixed ~3 us (launch, pipeline fill,
 // output store) plus the work of the tiles one CU holds at that tile's
-// sustained MFMA efficiency.
-int choose_cfg(int M, int N, int K, int num_cus) {
+// sustained MFMA efficiency. glu: only the glue-epilogue configurations.
+int choose_cfg(int M, int N, int K, int num_cus, bool glu = false) {
   int best = 4;
   double best_t = 1e300;
   for (int c = 0; c < N_F16_CFGS; ++c) {
+    if (glu && std::find(std::begin(F16_GLU_CFGS), std::end(F16_GLU_CFGS), c) == std::end(F16_GLU_CFGS))
+      continue;
     const F16Cfg &f = F16_CFGS[c];
     const long tiles = ((M + f.bm - 1) / f.bm) * (long)((N + f.bn - 1) / f.bn);
     const long slots = (long)num_cus * f.per_cu;
@@ -290,4 +356,35 @@ hipError_t rk_launch_gemm_f16(const void *A, const void *B, void *C, int M, int 
   const int c = rk_knob("RK_F16_TILE", -1);
   return launch_cfg(c >= 0 && c < N_F16_CFGS ? c : choose_cfg(M, N, K, num_cus), (const f16 *)A,
                     (const f16 *)B, (f16 *)C, M, N, K, st);
+}
+
+namespace {
+template <int GLU, bool OUT_F16>
+hipError_t launch_glu_cfg(int c, const f16 *a, const f16 *b, void *d, int M, int N, int K, int n_out,
+                          hipStream_t st) {
+  switch (c) {
+    case 0: return launch_gemm_f16<256, 128, 4, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
+    case 1: return launch_gemm_f16<192, 192, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
+    case 2: return launch_gemm_f16<128, 128, 2, 2, 4, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
+    case 3: return launch_gemm_f16<128, 64, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
+    case 4: return launch_gemm_f16<64, 64, 2, 2, 4, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
+    case 8: return launch_gemm_f16<192, 128, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
+  }
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+hipError_t rk_launch_gemm_f16_glu(const void *A, const void *B, void *C, int M, int N, int K,
+                                  int n_out, int glu, bool out_f16, int num_cus, hipStream_t st) {
+  int c = rk_knob("RK_F16_TILE", -1);
+  if (std::find(std::begin(F16_GLU_CFGS), std::end(F16_GLU_CFGS), c) == std::end(F16_GLU_CFGS))
+    c = choose_cfg(M, N, K, num_cus, true);
+  const f16 *a = (const f16 *)A, *b = (const f16 *)B;
+  if (glu == 1)
+    return out_f16 ? launch_glu_cfg<1, true>(c, a, b, C, M, N, K, n_out, st)
+                   : launch_glu_cfg<1, false>(c, a, b, C, M, N, K, n_out, st);
+  if (glu == 2)
+    return out_f16 ? launch_glu_cfg<2, true>(c, a, b, C, M, N, K, n_out, st)
+                   : launch_glu_cfg<2, false>(c, a, b, C, M, N, K, n_out, st);
+  return hipErrorInvalidValue;
 }

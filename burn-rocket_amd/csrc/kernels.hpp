@@ -19,6 +19,18 @@ static inline int rk_knob(const char *name, int dflt) {
 hipError_t rk_launch_gemm_f16(const void *A, const void *B, void *C, int M, int N, int K,
                               int num_cus, hipStream_t st);
 
+// fp16 GEMM with a gate|up glue epilogue: B [N, K] holds gate and up rows
+// interleaved per 16 (N = 32·ceil(n_out/16)); C [M, n_out] = glue(gate·a,
+// up·a) with both products rounded to fp16 first; glu 1 silu·up, 2 gelu·up;
+// C f32 or (out_f16) fp16.
+hipError_t rk_launch_gemm_f16_glu(const void *A, const void *B, void *C, int M, int N, int K,
+                                  int n_out, int glu, bool out_f16, int num_cus, hipStream_t st);
+// Element type conversion (RK_DTYPE_* src → dst), round to nearest even.
+hipError_t rk_launch_cast(const void *x, int src, void *y, int dst, int64_t n, hipStream_t st);
+// f32 rows [n, k] → fp16 (RNE) rows (r/16)·grp_stride + grp_off + r%16 of out.
+hipError_t rk_launch_f32_to_f16_rows(const float *x, int64_t n, int64_t k, int grp_stride,
+                                     int grp_off, void *out, hipStream_t st);
+
 enum I8Mode { I8_PER_TOKEN = 0, I8_PER_GROUP = 1, I8_RAW = 2, I8_PARTIALS = 3 };
 
 struct I8GemmArgs {

@@ -39,6 +39,55 @@ hipError_t rk_launch_f32_to_f16(const float *x, void *y, int64_t n, hipStream_t 
   return hipGetLastError();
 }
 
+// Element type conversion between f32, fp16 and bf16 (RK_DTYPE_*), rounding
+// to nearest even, four elements per thread.
+template <int SRC, int DST>
+__global__ __launch_bounds__(256) void cast_kernel(const void *__restrict__ x, void *__restrict__ y,
+                                                   int64_t n) {
+  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (i0 + e < n) dt_store<DST>(y, i0 + e, dt_load<SRC>(x, i0 + e));
+}
+
+template <int SRC>
+static hipError_t launch_cast_from(const void *x, void *y, int64_t n, int dst, hipStream_t st) {
+  const dim3 grid((unsigned)((n + 1023) / 1024)), block(256);
+  switch (dst) {
+    case RK_DTYPE_F32: hipLaunchKernelGGL((cast_kernel<SRC, RK_DTYPE_F32>), grid, block, 0, st, x, y, n); break;
+    case RK_DTYPE_F16: hipLaunchKernelGGL((cast_kernel<SRC, RK_DTYPE_F16>), grid, block, 0, st, x, y, n); break;
+    case RK_DTYPE_BF16: hipLaunchKernelGGL((cast_kernel<SRC, RK_DTYPE_BF16>), grid, block, 0, st, x, y, n); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t rk_launch_cast(const void *x, int src, void *y, int dst, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  switch (src) {
+    case RK_DTYPE_F32: return launch_cast_from<RK_DTYPE_F32>(x, y, n, dst, st);
+    case RK_DTYPE_F16: return launch_cast_from<RK_DTYPE_F16>(x, y, n, dst, st);
+    case RK_DTYPE_BF16: return launch_cast_from<RK_DTYPE_BF16>(x, y, n, dst, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+__global__ void f32_to_f16_rows_kernel(const float *__restrict__ x, int64_t n, int64_t k,
+                                       int grp_stride, int grp_off, f16 *__restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * k) return;
+  const int64_t r = i / k, c = i % k;
+  y[((r / 16) * grp_stride + grp_off + r % 16) * k + c] = (f16)x[i];
+}
+
+hipError_t rk_launch_f32_to_f16_rows(const float *x, int64_t n, int64_t k, int grp_stride,
+                                     int grp_off, void *out, hipStream_t st) {
+  if (n * k <= 0) return hipSuccess;
+  hipLaunchKernelGGL(f32_to_f16_rows_kernel, dim3((unsigned)((n * k + 255) / 256)), dim3(256), 0, st,
+                     x, n, k, grp_stride, grp_off, (f16 *)out);
+  return hipGetLastError();
+}
+
 hipError_t rk_launch_f16_to_f32(const void *x, float *y, int64_t n, hipStream_t st) {
   if (n <= 0) return hipSuccess;
   int64_t threads = (n + 3) / 4;

@@ -98,6 +98,11 @@ unsafe extern "C" {
     pub fn rk_matmul_f16_dev(
         id: WeightId, a: *const c_void, m: i64, k: i64, c: *mut c_void, stream: Stream
     ) -> c_int;
+    pub fn rk_pack_f16_glu(gate: *const f32, up: *const f32, n: i64, k: i64, id: *mut WeightId) -> c_int;
+    pub fn rk_matmul_f16_glu_dev(
+        id: WeightId, a: *const c_void, m: i64, k: i64, glu: c_int, out: *mut c_void, out_f16: c_int,
+        stream: Stream
+    ) -> c_int;
     pub fn rk_quantize_rows_dev(
         x: *const f32, m: i64, k: i64, group: i64, q: *mut i8, scale: *mut f32, stream: Stream
     ) -> c_int;
@@ -230,6 +235,9 @@ unsafe extern "C" {
     pub fn rk_memcpy_dtoh(dst: *mut c_void, src: *const c_void, bytes: usize) -> c_int;
     pub fn rk_memcpy_dtod(
         dst: *mut c_void, src: *const c_void, bytes: usize, stream: Stream
+    ) -> c_int;
+    pub fn rk_cast_dev(
+        x: *const c_void, x_dtype: c_int, y: *mut c_void, y_dtype: c_int, n: i64, stream: Stream
     ) -> c_int;
     pub fn rk_memset_dev(dst: *mut c_void, value: c_int, bytes: usize) -> c_int;
     pub fn rk_stream_get(stream: *mut Stream) -> c_int;

@@ -190,6 +190,22 @@ int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, float *y);
 int rk_matmul_f16_dev(rk_weight_id id, const void *a, int64_t m, int64_t k,
                       void *c, rk_stream stream);
 
+/* A gated MLP's first projection as one fp16 GEMM with the glue in its
+ * epilogue: out [M, n] = glue(gate·x, up·x), glue = silu_mul (RK_GLU_SILU) or
+ * gelu_mul (RK_GLU_GELU). It fuses what the reference's Qwen3 MLP runs as one
+ * fp16 matmul on the pack2 of gate and up, a slice into the two halves and a
+ * glue op (src/qwen3_embedding/model.rs:592-600 with the weights of
+ * load.rs:221-238; matmul_f16 ext.rs:1437-1499, whose fp16 output is widened
+ * to f32; rocket_silu_mul / rocket_gelu_mul ext.rs:603-608 with the formulas
+ * of host.rs:12-39): each product is accumulated in f32, rounded to fp16 as
+ * the plain GEMM's output is, then the glue runs in f32 with no FMA
+ * contraction. a fp16 [M, K]; out f32 or (out_f16) fp16 [M, n]. The weight
+ * comes from rk_pack_f16_glu (f32 gate and up, each [n, K], rounded to fp16
+ * and interleaved per 16 rows); such a weight is only accepted here. */
+int rk_pack_f16_glu(const float *gate, const float *up, int64_t n, int64_t k, rk_weight_id *id);
+int rk_matmul_f16_glu_dev(rk_weight_id id, const void *a, int64_t m, int64_t k, int glu, void *out,
+                          int out_f16, rk_stream stream);
+
 /* Per-row activation quantizer on device (`quantize_i8_rows`, ext.rs:1017;
  * quantize_row_groups, host.rs:77-90): x f32 [M, K] → q int8 [M, K] and
  * scale f32 [M, K/group]. group == K is per-token quantization. */
@@ -465,6 +481,12 @@ int rk_memcpy_dtoh(void *dst, const void *src, size_t bytes);
 /* Device-to-device copy, ordered on `stream` (NULL: the library stream). */
 int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_stream stream);
 int rk_memset_dev(void *dst, int value, size_t bytes);
+/* y = x converted element by element between f32, fp16 and bf16 (RK_DTYPE_*),
+ * rounded to nearest even: the host f32_to_f16_par / f16_to_f32_par passes
+ * either side of every reference op (ext.rs:2144-2170), on device buffers.
+ * x and y must not overlap unless they are the same buffer and the types
+ * have the same size. */
+int rk_cast_dev(const void *x, int x_dtype, void *y, int y_dtype, int64_t n, rk_stream stream);
 int rk_stream_get(rk_stream *stream);    /* the library stream */
 /* A new non-blocking HIP stream at the default priority, and its release
  * (after rk_stream_sync when work is pending on it). */

@@ -118,3 +118,78 @@ def test_glue_errors(rk):
         rk.silu_mul(np.ones(3, np.float32), np.ones(3, np.float16))
     with pytest.raises(AssertionError):
         rk.gelu_mul(np.ones(3, np.float32), np.ones(4, np.float32))
+
+
+# fp16 gate|up GEMM with the glue in its epilogue (the reference's Qwen3 MLP:
+# one fp16 matmul on pack2(gate, up), slice, silu_mul; src/qwen3_embedding/
+# model.rs:592-600). Against the oracle: the two fp16 products rounded to fp16,
+# then its glue; against the unfused GPU path (two fp16 GEMMs, then the glue op
+# on their f32-widened outputs): bit for bit, since each output element sees
+# the same f32 accumulation, the same fp16 rounding and the same glue formula.
+@pytest.mark.parametrize("glu", ["silu", "gelu"])
+@pytest.mark.parametrize("m,k,n", [(3633, 1024, 3072), (100, 256, 72), (257, 512, 200)])
+def test_f16_glu_gemm(rk, orc, m, k, n, glu):
+    note(f"fp16 gate|up GEMM + {glu}: m={m} k={k} n={n}")
+    lib = rk.lib()
+    r = np.random.default_rng(m + n + (glu == "gelu"))
+    x = r.standard_normal((m, k)).astype(np.float16)
+    gate = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    up = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    code = rk.GLU_SILU if glu == "silu" else rk.GLU_GELU
+    wid = rk.pack_f16_glu(gate, up)
+    dx = rk.DeviceBuffer.from_array(x.view(np.uint16))
+    outs = {}
+    for f16out in (0, 1):
+        do = rk.DeviceBuffer(m * n * (2 if f16out else 4))
+        assert lib.rk_matmul_f16_glu_dev(int(wid), dx.ptr, m, k, code, do.ptr, f16out, None) == 0, \
+            lib.rk_last_error()
+        rk.synchronize()
+        outs[f16out] = (do.download((m, n), np.uint16).view(np.float16).astype(np.float32) if f16out
+                        else do.download((m, n), np.float32))
+    # oracle: fp16 products (f32 accumulation, rounded to fp16), then the glue
+    g16 = orc.f16_to_f32(orc.f32_to_f16(orc.gemm_f16(x, orc.f32_to_f16(gate))))
+    u16 = orc.f16_to_f32(orc.f32_to_f16(orc.gemm_f16(x, orc.f32_to_f16(up))))
+    ref = orc.silu_mul(g16, u16) if glu == "silu" else orc.gelu_mul(g16, u16)
+    for f16out, got in outs.items():
+        cos, rel = orc.cosine(got, ref), orc.max_rel(got, ref)
+        assert cos >= 0.9999 and rel <= 1e-2, (f16out, cos, rel)
+    # unfused GPU path on the same data
+    prods = []
+    for w in (gate, up):
+        wq = rk.pack(w)
+        dc = rk.DeviceBuffer(m * n * 2)
+        assert lib.rk_matmul_f16_dev(int(wq), dx.ptr, m, k, dc.ptr, None) == 0
+        rk.synchronize()
+        prods.append(dc.download((m, n), np.uint16).view(np.float16).astype(np.float32))
+    fn = rk.silu_mul if glu == "silu" else rk.gelu_mul
+    assert (outs[0] == fn(prods[0], prods[1])).all()
+    assert (outs[1] == fn(prods[0].astype(np.float16), prods[1].astype(np.float16)).astype(np.float32)).all()
+    # the interleaved weight is refused by the plain fp16 GEMM
+    assert lib.rk_matmul_f16_dev(int(wid), dx.ptr, m, k, rk.DeviceBuffer(m * 2 * n * 2).ptr, None) == rk.RK_E_UNSUPPORTED
+
+
+def test_cast_dev_every_type_pair_rounds_to_nearest_even(rk, orc):
+    # rk_cast_dev: the f32 <-> f16 / bf16 conversions either side of every op
+    # (ext.rs:2144-2170), bit for bit against the oracle's RNE conversions
+    # (`half` 2.7.1), including ties, subnormals, overflow and ±0.
+    note("rk_cast_dev")
+    lib = rk.lib()
+    r = np.random.default_rng(77)
+    x = np.concatenate([r.standard_normal(100001).astype(np.float32) * 10.0 ** r.integers(-8, 6, 100001),
+                        np.array([0.0, -0.0, 65504.0, 65520.0, 1e30, -1e30, 5.96e-8, 2.98e-8, 1e-40],
+                                 np.float32)]).astype(np.float32)
+    as_f32 = {rk.DTYPE_F32: x, rk.DTYPE_F16: orc.f16_to_f32(orc.f32_to_f16(x)),
+              rk.DTYPE_BF16: orc.bf16_to_f32(orc.f32_to_bf16(x))}
+    bits = {rk.DTYPE_F32: lambda v: v.view(np.uint32), rk.DTYPE_F16: orc.f32_to_f16, rk.DTYPE_BF16: orc.f32_to_bf16}
+    size = {rk.DTYPE_F32: 4, rk.DTYPE_F16: 2, rk.DTYPE_BF16: 2}
+    for src in (rk.DTYPE_F32, rk.DTYPE_F16, rk.DTYPE_BF16):
+        src_bits = bits[src](as_f32[src])
+        dx = rk.DeviceBuffer.from_array(src_bits)
+        for dst in (rk.DTYPE_F32, rk.DTYPE_F16, rk.DTYPE_BF16):
+            dy = rk.DeviceBuffer(x.size * size[dst])
+            assert lib.rk_cast_dev(dx.ptr, src, dy.ptr, dst, x.size, None) == 0, lib.rk_last_error()
+            rk.synchronize()
+            got = dy.download(x.size, np.uint32 if dst == rk.DTYPE_F32 else np.uint16)
+            want = bits[dst](as_f32[src])  # the source value is exact in f32
+            nan = np.isnan(as_f32[src])
+            assert (got[~nan] == want[~nan]).all(), (src, dst)
