@@ -114,6 +114,41 @@ __device__ __forceinline__ float sum4groups(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Key tiles a query tile reads: its rows (query heads × queries q_lo..q_hi)
+// see absolute keys in per-row intervals whose ends never decrease with the
+// query position, so the union of the rows' intervals and "some row sees no
+// key at all" (degenerate: then every key tile is swept) follow from the first
+// and the last query. full_lo..full_hi: relative keys every row of the tile
+// sees.
+struct TileKeys {
+  int kt_begin, kt_end, full_lo, full_hi;
+  bool degenerate;
+};
+__device__ __forceinline__ TileKeys tile_keys(const AttnArgs &a, int qt, int BQ) {
+  const int n_kt = (a.n_kv + BK - 1) / BK;
+  const int q_lo = qt * BQ, q_hi = min(qt * BQ + BQ, a.n_q) - 1;
+  const int64_t t_min = a.q0 + q_lo, t_max = a.q0 + q_hi;
+  const int64_t kabs0 = a.k0, kabs1 = a.k0 + a.n_kv - 1;
+  int64_t lo_a, hi_a, lo_b, hi_b;
+  vis_range(a.mask_mode, a.window, t_min, lo_a, hi_a);
+  vis_range(a.mask_mode, a.window, t_max, lo_b, hi_b);
+  TileKeys t;
+  // a row t sees no key iff lo(t) > kabs1, hi(t) < kabs0 or lo(t) > hi(t);
+  // lo - hi is the same for every row
+  t.degenerate = hi_a < kabs0 || lo_b > kabs1 || lo_a > hi_a;
+  t.full_lo = (int)min(max(lo_b - a.k0, (int64_t)0), (int64_t)a.n_kv);
+  t.full_hi = (int)max(min(hi_a - a.k0, (int64_t)a.n_kv - 1), (int64_t)-1);
+  t.kt_begin = 0;
+  t.kt_end = n_kt;
+  if (!t.degenerate) {
+    const int64_t any_lo = max(lo_a, kabs0) - a.k0;  // relative key indices
+    const int64_t any_hi = min(hi_b, kabs1) - a.k0;
+    t.kt_begin = (int)(max(any_lo, (int64_t)0) / BK);
+    t.kt_end = (int)min((any_hi / BK) + 1, (int64_t)n_kt);
+  }
+  return t;
+}
+
 template <int D>
 struct AttnGeom {
   static constexpr int DQ = (D + 15) / 16 * 16;  // padded head dim
@@ -149,7 +184,6 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   static_assert(Gm::SMEM <= 160 * 1024, "LDS");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  __shared__ int s_flag;
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -227,39 +261,11 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       tab[qb] = a.q0 + (rok[qb] ? qi[qb] : 0);
     }
 
-    // ---- tile query range, key range, degenerate rows
-    const int q_lo = qt * BQ, q_hi = min(qt * BQ + BQ, a.n_q) - 1;
-    const int64_t t_min = a.q0 + q_lo, t_max = a.q0 + q_hi;
-    const int64_t kabs0 = a.k0, kabs1 = a.k0 + a.n_kv - 1;
-    if (threadIdx.x == 0) s_flag = 0;
-    __syncthreads();
-    if (grp == 0) {
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        if (rok[qb]) {
-          int64_t lo, hi;
-          vis_range(a.mask_mode, a.window, tab[qb], lo, hi);
-          if (max(lo, kabs0) > min(hi, kabs1)) s_flag = 1;  // no visible key
-        }
-      }
-    }
-    __syncthreads();
-    const bool degenerate = s_flag != 0;
-    int kt_begin = 0, kt_end = n_kt;
-    int full_lo, full_hi;  // relative keys visible to every row of the tile
-    {
-      int64_t lo_a, hi_a, lo_b, hi_b;
-      vis_range(a.mask_mode, a.window, t_min, lo_a, hi_a);
-      vis_range(a.mask_mode, a.window, t_max, lo_b, hi_b);
-      full_lo = (int)min(max(lo_b - a.k0, (int64_t)0), (int64_t)a.n_kv);
-      full_hi = (int)max(min(hi_a - a.k0, (int64_t)a.n_kv - 1), (int64_t)-1);
-      if (!degenerate) {
-        const int64_t any_lo = max(lo_a, kabs0) - a.k0;  // relative key indices
-        const int64_t any_hi = min(hi_b, kabs1) - a.k0;
-        kt_begin = (int)(max(any_lo, (int64_t)0) / BK);
-        kt_end = (int)min((any_hi / BK) + 1, (int64_t)n_kt);
-      }
-    }
+    // ---- key range of the tile, degenerate rows
+    const TileKeys tkeys = tile_keys(a, qt, BQ);
+    const bool degenerate = tkeys.degenerate;
+    const int full_lo = tkeys.full_lo, full_hi = tkeys.full_hi;
+    const int kt_begin = tkeys.kt_begin, kt_end = tkeys.kt_end;
     const float masked_x = degenerate ? MASKED_SCORE * LOG2E : -INFINITY;
     // Visible keys of each of this lane's queries as a relative key interval
     // [klo, khi] (every mask mode is an interval), clipped to [0, n_kv).

@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/burn_rocket_amd.h"
@@ -63,15 +64,22 @@ int hip_fail(hipError_t e, const char *op) {
     if (rc_ != RK_OK) return rc_; \
   } while (0)
 
-// A named device scratch buffer. `ev` is recorded on the calling stream after
-// the work of every call that used the buffer, so a call on another stream
-// first waits for it, and the buffer is freed only once it has completed.
+// A named device scratch buffer and the point after the last call that used
+// it: a call on another stream first waits for that point, and the buffer is
+// freed only once it has passed. On a caller's stream the point is an event
+// recorded when the call returns. On a stream the library owns (its own, or
+// one from rk_stream_create) nothing is recorded per call: the event is
+// recorded on that stream only when another stream or a free needs the point
+// (everything enqueued there by then includes the last use). An event record
+// costs the GPU ~5 µs after the preceding kernel on MI355X, a large share of
+// the short ops when it was paid per call and buffer.
 struct DevBuf {
   void *p = nullptr;
   size_t bytes = 0;
   hipEvent_t ev = nullptr;
-  hipStream_t ev_stream = nullptr;  // where ev was last recorded
-  bool recorded = false;
+  hipStream_t ev_stream = nullptr;  // stream of the last call that used the buffer
+  bool recorded = false;            // ev marks the end of that call's work
+  bool pending = false;             // that call ran on a library stream; ev not recorded yet
 };
 
 struct Weight {
@@ -95,6 +103,7 @@ struct Weight {
 struct Engine {
   int device = 0;
   hipStream_t stream = nullptr;
+  std::unordered_set<hipStream_t> own_streams;  // made by rk_stream_create
   int num_cus = 256;
   std::unordered_map<uint64_t, Weight> weights;
   uint64_t next_id = 1;
@@ -118,9 +127,11 @@ int ensure(const char *op) {
   return RK_OK;
 }
 
+bool own_stream(hipStream_t s) { return s == g_eng->stream || g_eng->own_streams.count(s) != 0; }
+
 // The stream of one entry-point call and the scratch buffers it took: when the
-// call returns (its work is enqueued) each buffer's event is recorded on that
-// stream.
+// call returns (its work is enqueued) each buffer notes the stream, and on a
+// caller's stream gets its event recorded there (DevBuf).
 struct CallScope {
   hipStream_t st;
   std::vector<DevBuf *> used;
@@ -128,13 +139,25 @@ struct CallScope {
   CallScope(const CallScope &) = delete;
   CallScope &operator=(const CallScope &) = delete;
   ~CallScope() {
-    for (DevBuf *b : used)
-      if (hipEventRecord(b->ev, st) == hipSuccess) {
-        b->recorded = true;
-        b->ev_stream = st;
-      }
+    const bool own = own_stream(st);
+    for (DevBuf *b : used) {
+      b->ev_stream = st;
+      b->pending = own;
+      b->recorded = false;
+      if (!own && hipEventRecord(b->ev, st) == hipSuccess) b->recorded = true;
+    }
   }
 };
+
+// Make b.ev mark the end of the buffer's last use (see DevBuf).
+int fence_point(DevBuf &b, const char *op) {
+  if (b.pending) {
+    HIP_TRY(hipEventRecord(b.ev, b.ev_stream), op);
+    b.pending = false;
+    b.recorded = true;
+  }
+  return RK_OK;
+}
 
 // Grow-only named device scratch, ordered after its last use on any stream.
 int scratch(CallScope &c, const char *name, size_t bytes, void **out) {
@@ -142,16 +165,19 @@ int scratch(CallScope &c, const char *name, size_t bytes, void **out) {
   if (!b.ev) HIP_TRY(hipEventCreateWithFlags(&b.ev, hipEventDisableTiming), "scratch");
   if (b.bytes < bytes) {
     if (b.p) {
+      RK_TRY(fence_point(b, "scratch"));
       if (b.recorded) HIP_TRY(hipEventSynchronize(b.ev), "scratch");
       HIP_TRY(hipFree(b.p), "scratch");
     }
     b.p = nullptr;
     b.bytes = 0;
     b.recorded = false;
+    b.pending = false;
     const size_t want = std::max<size_t>(bytes, 256);
     HIP_TRY(hipMalloc(&b.p, want), "scratch");
     b.bytes = want;
-  } else if (b.recorded && b.ev_stream != c.st) {
+  } else if ((b.recorded || b.pending) && b.ev_stream != c.st) {
+    RK_TRY(fence_point(b, "scratch"));
     HIP_TRY(hipStreamWaitEvent(c.st, b.ev, 0), "scratch");
   }
   if (std::find(c.used.begin(), c.used.end(), &b) == c.used.end()) c.used.push_back(&b);
@@ -316,6 +342,7 @@ extern "C" int rk_trim_scratch_to(uint64_t budget) {
   for (auto &o : order) {
     if (total <= budget) break;
     DevBuf &b = g_eng->scratch[o.second];
+    RK_TRY(fence_point(b, "rk_trim_scratch_to"));
     if (b.recorded) HIP_TRY(hipEventSynchronize(b.ev), "rk_trim_scratch_to");
     HIP_TRY(hipFree(b.p), "rk_trim_scratch_to");
     if (b.ev) (void)hipEventDestroy(b.ev);
@@ -1324,14 +1351,16 @@ struct MoePlan {
   int32_t *slot = nullptr;    // [s, top_k] bucket rows of a token, ascending expert id
   MoeTile *tiles = nullptr;   // [n_tiles]
   uint64_t weight = 0;        // expert stack the plan was made for
-  // Recorded after every run that reads the lists, on that run's stream.
-  mutable hipEvent_t last_use = nullptr;
-  mutable bool used = false;
+  // Streams of the runs that read the lists: a library stream is
+  // synchronized when the plan is destroyed; a caller's stream gets an event
+  // recorded after each run there.
+  mutable std::vector<std::pair<hipStream_t, hipEvent_t>> uses;
 };
 
 void plan_free(MoePlan *p) {
   if (!p) return;
-  if (p->last_use) (void)hipEventDestroy(p->last_use);
+  for (auto &u : p->uses)
+    if (u.second) (void)hipEventDestroy(u.second);
   (void)hipFree(p->tok);
   (void)hipFree(p->roww);
   (void)hipFree(p->slot);
@@ -1431,9 +1460,14 @@ int moe_run(CallScope &cs, const Weight &w, const MoePlan &plan, const float *x,
 }
 
 int plan_mark_used(const MoePlan &p, hipStream_t st) {
-  if (!p.last_use) HIP_TRY(hipEventCreateWithFlags(&p.last_use, hipEventDisableTiming), "rk_moe_plan");
-  HIP_TRY(hipEventRecord(p.last_use, st), "rk_moe_plan");
-  p.used = true;
+  auto it = std::find_if(p.uses.begin(), p.uses.end(), [&](const auto &u) { return u.first == st; });
+  if (it == p.uses.end()) {
+    p.uses.push_back({st, nullptr});
+    it = p.uses.end() - 1;
+  }
+  if (own_stream(st)) return RK_OK;
+  if (!it->second) HIP_TRY(hipEventCreateWithFlags(&it->second, hipEventDisableTiming), "rk_moe_plan");
+  HIP_TRY(hipEventRecord(it->second, st), "rk_moe_plan");
   return RK_OK;
 }
 
@@ -1525,8 +1559,13 @@ extern "C" int rk_moe_plan_destroy(void *plan) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_moe_plan_destroy"));
   MoePlan *p = (MoePlan *)plan;
-  // Runs on any stream that read the plan's lists must have finished.
-  if (p && p->used) HIP_TRY(hipEventSynchronize(p->last_use), "rk_moe_plan_destroy");
+  // Runs on any stream that read the plan's lists must have finished (a
+  // library stream destroyed since was synchronized then).
+  if (p)
+    for (auto &u : p->uses) {
+      if (u.second) HIP_TRY(hipEventSynchronize(u.second), "rk_moe_plan_destroy");
+      else if (own_stream(u.first)) HIP_TRY(hipStreamSynchronize(u.first), "rk_moe_plan_destroy");
+    }
   HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_moe_plan_destroy");
   plan_free(p);
   return RK_OK;
@@ -1852,15 +1891,23 @@ extern "C" int rk_stream_create(rk_stream *stream) {
   if (!stream) return fail(RK_E_SHAPE, "rk_stream_create", "null output");
   hipStream_t st = nullptr;
   HIP_TRY(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "rk_stream_create");
+  g_eng->own_streams.insert(st);
   *stream = (rk_stream)st;
   return RK_OK;
 }
 extern "C" int rk_stream_destroy(rk_stream stream) {
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_stream_destroy"));
-  if (!stream || (hipStream_t)stream == g_eng->stream)
+  hipStream_t st = (hipStream_t)stream;
+  if (!stream || st == g_eng->stream || !g_eng->own_streams.count(st))
     return fail(RK_E_SHAPE, "rk_stream_destroy", "not a stream made by rk_stream_create");
-  HIP_TRY(hipStreamDestroy((hipStream_t)stream), "rk_stream_destroy");
+  // The stream's work completes first: buffers and MoE plans last used there
+  // then need no further fence.
+  HIP_TRY(hipStreamSynchronize(st), "rk_stream_destroy");
+  for (auto &kv : g_eng->scratch)
+    if (kv.second.ev_stream == st) kv.second.pending = kv.second.recorded = false;
+  HIP_TRY(hipStreamDestroy(st), "rk_stream_destroy");
+  g_eng->own_streams.erase(st);
   return RK_OK;
 }
 extern "C" int rk_stream_sync(rk_stream stream) {
