@@ -88,6 +88,7 @@ struct Weight {
   void *codes = nullptr;     // fp16 [N,K] or int8 [N,K]
   float *scales = nullptr;   // I8: [N, ws_stride] per 32-block; QAT: [N]
   int ws_stride = 0;
+  bool ws_f16 = false;       // I8: every block scale is an fp16 value (GGUF Q8_0 d)
   int64_t glu_n = 0;  // > 0: gate|up rows interleaved for rk_matmul_w8a8_glu_dev, n = glu_n outputs
   float in_scale = 0.f, out_scale = 0.f;
   size_t bytes = 0;
@@ -419,6 +420,8 @@ int pack_i8_host(const int8_t *codes, const std::vector<float> &block_scales, in
   HIP_TRY(hipMalloc(&w.codes, (size_t)n * k), op);
   HIP_TRY(hipMemcpy(w.codes, codes, (size_t)n * k, hipMemcpyHostToDevice), op);
   RK_TRY(upload_block_scales(block_scales, n, k / 32, &w.scales, &w.ws_stride, op));
+  w.ws_f16 = std::all_of(block_scales.begin(), block_scales.end(),
+                         [](float d) { return (float)(_Float16)d == d; });
   w.bytes = (size_t)n * k + (size_t)n * w.ws_stride * 4;
   *id = insert(w);
   return RK_OK;
@@ -496,6 +499,7 @@ int pack_q8_0_blocks(CallScope &cs, const uint8_t *const *srcs, const int *grp_o
                      int64_t n, int64_t k, int64_t rows, int grp_stride, Weight &wt,
                      const char *op) {
   wt.kind = RK_WEIGHT_I8;
+  wt.ws_f16 = true;  // GGUF Q8_0: fp16 d per block
   wt.n = rows;
   wt.k = k;
   wt.group = 32;
@@ -538,6 +542,7 @@ extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_
   CallScope cs(g_eng->stream);
   Weight wt;
   wt.kind = RK_WEIGHT_I8;
+  wt.ws_f16 = true;  // GGUF Q8_0: fp16 d per block
   wt.n = n;
   wt.k = k;
   wt.group = 32;
@@ -590,6 +595,7 @@ extern "C" int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t 
   const int64_t rows = glu_rows(n);
   Weight wt;
   wt.kind = RK_WEIGHT_I8;
+  wt.ws_f16 = true;  // GGUF Q8_0: fp16 d per block
   wt.n = rows;
   wt.k = k;
   wt.group = 32;
@@ -697,6 +703,7 @@ int launch_i8(const Weight &w, const int8_t *a, const float *as, int as_stride, 
   g.W = (const int8_t *)w.codes;
   g.WS = w.scales;
   g.ws_stride = w.ws_stride;
+  g.ws_f16 = w.ws_f16;
   g.gb = (int)(w.group / 32);
   g.C = c;
   g.M = (int)m;

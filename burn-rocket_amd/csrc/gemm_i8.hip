@@ -14,7 +14,8 @@
 //
 // Modes (template parameter MODE):
 //   PER_TOKEN  c[m,n] = as[m] · Σ_g ws[n,g]·P_g        (per-token activations)
-//   PER_GROUP  c[m,n] = Σ_g (as[m,g]·ws[n,g])·P_g      (reference matmul_gw)
+//   PER_GROUP  c[m,n] = Σ_g (as[m,g]·ws[n,g])·P_g      (reference matmul_gw;
+//              group 32 on both sides runs on gemm_i8_q8_kernel below)
 //   RAW        c[m,n] = Σ_k a[m,k]·w[n,k]   as int32  (exact)
 //   PARTIALS   p[m,n,g] = P_g                 as int32  (exactness checks)
 //
@@ -321,16 +322,18 @@ __device__ __forceinline__ float glu_apply(float g, float u) {
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2,
-          int GLU = GLU_NONE>
+          int GLU = GLU_NONE, bool WSF16 = false>
 __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     const int8_t *__restrict__ A, const float *__restrict__ AS, const int8_t *__restrict__ W,
     const float *__restrict__ WS, int ws_stride, void *__restrict__ Cout, int M, int N, int K,
-    int tiles_m, int tiles_n, int group_m, int n_out) {
-  static_assert(MODE == MODE_PER_TOKEN || MODE == MODE_RAW, "per-token or raw");
+    int tiles_m, int tiles_n, int group_m, int n_out, int as_stride) {
+  static_assert(MODE == MODE_PER_TOKEN || MODE == MODE_PER_GROUP || MODE == MODE_RAW,
+                "per-token, per-group or raw");
   constexpr int NW = WM * WN;
   constexpr int NT = NW * 64;
   constexpr int ROWB = 128;  // K bytes of one stage row
-  constexpr bool SCALED = (MODE == MODE_PER_TOKEN);
+  constexpr bool GROUPED = (MODE == MODE_PER_GROUP);
+  constexpr bool SCALED = (MODE == MODE_PER_TOKEN) || GROUPED;
   constexpr int CODE_BYTES = (BM + BN) * ROWB;
   constexpr int WS_BYTES = SCALED ? BN * 16 : 0;
   constexpr int STAGE_BYTES = CODE_BYTES + WS_BYTES;
@@ -345,9 +348,18 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   static_assert(QA % 2 == 0, "A copies keep the swizzle parity of B copies");
   static_assert(WS_INS <= NW && (!SCALED || WS_INS * 64 == BN), "scale split");
   static_assert(TM * 32 * WM == BM && TN * 32 * WN == BN, "mfma split");
+  // Per-group activation scales as[m, g] of a stage (4 blocks) sit in their
+  // own ring of STAGES + 1 slots, [block][row], filled by 4-byte copies
+  // (AS_INS of 64 per stage): a slot outlives its stage's code slot, which is
+  // refilled while the last block's last tile is still to be folded. One row
+  // of 32 tiles per wave (TM = 1) keeps two 16-row scale sets in registers.
+  constexpr int AS_SLOT = GROUPED ? BM * 16 : 0;
+  constexpr int AS_INS = GROUPED ? BM * 4 / 64 : 0;
+  static_assert(!GROUPED || (TM == 1 && TN == 1), "per-group mode: one 32x32 tile per wave");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  float *s_as = (float *)(smem + STAGES * STAGE_BYTES);  // [BM] activation scales
+  float *s_as = (float *)(smem + STAGES * STAGE_BYTES);  // [BM] per-token activation scales
+  uint8_t *s_asg = smem + STAGES * STAGE_BYTES;          // per-group ring (GROUPED)
 
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -369,8 +381,15 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   const uint32_t voff_even = r8 * K + ((p8 ^ (r8 >> 1)) << 4);
   const uint32_t voff_odd = r8 * K + ((p8 ^ (4 + (r8 >> 1))) << 4);
   const uint32_t voff_ws = lane * ws_stride * 4;
+  // per-group scale copy c: float f = 64c + lane of the slot = (block f / BM, row f % BM)
+  const rsrc_t ras = make_rsrc(GROUPED ? AS + (size_t)m0 * as_stride : AS,
+                               GROUPED ? (int64_t)(M - m0) * as_stride * 4 : 0);
+  auto as_voff = [&](int c) -> uint32_t {
+    const int f = 64 * c + lane;
+    return (uint32_t)(((f % BM) * as_stride + f / BM) * 4);
+  };
 
-  if constexpr (SCALED) {
+  if constexpr (MODE == MODE_PER_TOKEN) {
     for (int r = threadIdx.x; r < BM; r += NT) s_as[r] = AS[min(m0 + r, M - 1)];
   }
 
@@ -392,6 +411,15 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     if constexpr (WS_INS > 0) {
       if (wave < WS_INS)
         bdma16(rs, sb + CODE_BYTES + wave * 1024, voff_ws, wave * 64 * ws_stride * 4 + kt * 16);
+    }
+    if constexpr (AS_INS > 0) {
+      // from the last wave down, away from the waves that copy weight scales
+      uint8_t *ab = s_asg + (kt % (STAGES + 1)) * AS_SLOT;
+#pragma unroll
+      for (int c = 0; c < AS_INS; ++c)
+        if (wave == NW - 1 - c % NW)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(ras, LDS_PTR(ab + c * 256), 4, as_voff(c),
+                                                   (uint32_t)(kt * 16), 0, 0);
     }
   };
   // Make stage kt visible to every wave. Copies return in issue order, so
@@ -426,6 +454,16 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     b_off[b] = BM * ROWB + (wn * WTN + fcol) * ROWB + ch;
   }
   const uint32_t s_off = CODE_BYTES + (wn * WTN + fcol) * 16;
+  // lane's 16 rows of a 32-row tile: 8·q + 4·(lane/32) + 0..3, q = 0..3
+  const uint32_t asg_off = (uint32_t)((wm * WTM + fh * 4) * 4);
+  floatx4 as_pend[4];  // per-group scales of the block whose tile is folded next
+#pragma unroll
+  for (int q = 0; q < 4; ++q) as_pend[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto load_as = [&](floatx4(&dst)[4], int g) {
+    const uint8_t *ab = s_asg + ((g >> 2) % (STAGES + 1)) * AS_SLOT + (g & 3) * BM * 4 + asg_off;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = *(const floatx4 *)(ab + q * 32);
+  };
 
   intx4 af[2][TM], bf[2][TN];
   float dsc[2][TN];
@@ -476,10 +514,37 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
 #pragma unroll
   for (int r = 0; r < 16; ++r) ires[0][r] = ires[1][r] = 0;
   float dpend = 0.f;  // scale of the pending tile (the last tile of the previous block)
-  auto fold = [&](auto p_c, auto i_c, auto j_c, float d) {
-    constexpr int P = decltype(p_c)::value, I = decltype(i_c)::value, J = decltype(j_c)::value;
+  // Per-group mode with fp16 weight scales (WSF16): each MFMA starts from the
+  // int32 bits of 1.5·2^23 (GBIAS_BITS), so its result read as a float is
+  // exactly 1.5·2^23 + P_g (|P_g| < 2^19); fma(F, d, -1.5·2^23·d) is then
+  // P_g·d rounded once (an fp16 d makes 1.5·2^23·d exact), and a second FMA
+  // applies as[m, g]: two VALU operations per element and block instead of a
+  // convert, a multiply and an FMA. Other scales take the latter.
+  constexpr bool BIASED = GROUPED && WSF16;
+  constexpr int GBIAS_BITS = 0x4B400000;
+  constexpr float GBIAS = 12582912.0f;
+  intx16 cinit;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) facc[I][J][r] = __builtin_fmaf((float)ires[P][r], d, facc[I][J][r]);
+  for (int r = 0; r < 16; ++r) cinit[r] = BIASED ? GBIAS_BITS : 0;
+  auto fold = [&](auto p_c, auto i_c, auto j_c, float d, const floatx4(&asr)[4]) {
+    constexpr int P = decltype(p_c)::value, I = decltype(i_c)::value, J = decltype(j_c)::value;
+    if constexpr (GROUPED && !WSF16) {
+      // (as[m, g] · ws[n, g]) · P_g, the reference's order (emu_matmul_gw)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        facc[I][J][r] = __builtin_fmaf((float)ires[P][r], asr[r >> 2][r & 3] * d, facc[I][J][r]);
+    } else if constexpr (GROUPED) {
+      const float nbd = -GBIAS * d;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int bits = ires[P][r];  // element to a scalar first (ext-vector bit_cast)
+        const float y = __builtin_fmaf(__int_as_float(bits), d, nbd);
+        facc[I][J][r] = __builtin_fmaf(y, asr[r >> 2][r & 3], facc[I][J][r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) facc[I][J][r] = __builtin_fmaf((float)ires[P][r], d, facc[I][J][r]);
+    }
   };
 
   // Block step: global block g sits at slot S, block B of its stage, and uses
@@ -514,11 +579,13 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
       // previous block's last tile.
       constexpr int P0 = (B * T) & 1;
       const float dlast = dsc[CUR][TN - 1];
-      ires[P0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bf[CUR][0], intx16{}, 0, 0, 0);
+      ires[P0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][0], bf[CUR][0], cinit, 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
       load_frags(ic<NXT>{}, ic<NS>{}, ic<NB>{});
       __builtin_amdgcn_sched_barrier(0);
-      fold(ic<P0 ^ 1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+      fold(ic<P0 ^ 1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend, as_pend);
+      // the scales of this block's tile, folded in the next step
+      if constexpr (GROUPED) load_as(as_pend, g);
       __builtin_amdgcn_sched_barrier(0);
       // Tiles 1..T-1: MFMA of tile u, then the fold of tile u-1.
       static_for<T - 1>([&](auto uc) {
@@ -527,7 +594,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
         constexpr int PI = (u - 1) / TN, PJ = (u - 1) % TN;
         ires[(P0 + u) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][I], bf[CUR][J], intx16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        fold(ic<(P0 + u - 1) & 1>{}, ic<PI>{}, ic<PJ>{}, dsc[CUR][PJ]);
+        fold(ic<(P0 + u - 1) & 1>{}, ic<PI>{}, ic<PJ>{}, dsc[CUR][PJ], as_pend);
         __builtin_amdgcn_sched_barrier(0);
       });
       dpend = dlast;
@@ -549,16 +616,16 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   if constexpr (SCALED) {
     // The last block's last tile sits in set ((NBLK-1)·T + T-1) & 1.
     if (((NBLK * T - 1) & 1) != 0)
-      fold(ic<1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+      fold(ic<1>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend, as_pend);
     else
-      fold(ic<0>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend);
+      fold(ic<0>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend, as_pend);
   }
 
   // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of column lane%32.
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     floatx4 as4[4];
-    if constexpr (SCALED) {
+    if constexpr (MODE == MODE_PER_TOKEN) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) as4[q] = *(const floatx4 *)(s_as + wm * WTM + i * 32 + q * 8 + fh * 4);
     }
@@ -592,7 +659,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
           if constexpr (MODE == MODE_RAW) {
             ((int32_t *)Cout)[(size_t)m * N + n] = iacc[i][j][r];
           } else {
-            const float v = as4[r >> 2][r & 3] * facc[i][j][r];
+            const float v = GROUPED ? facc[i][j][r] : as4[r >> 2][r & 3] * facc[i][j][r];
             if constexpr (OUT_F16)
               ((f16 *)Cout)[(size_t)m * N + n] = (f16)v;
             else
@@ -605,11 +672,13 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2,
-          int GLU = GLU_NONE>
+          int GLU = GLU_NONE, bool WSF16 = false>
 static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
-  constexpr int smem =
-      STAGES * ((BM + BN) * 128 + (MODE == MODE_PER_TOKEN ? BN * 16 : 0)) + BM * 4;
-  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16, MINW, GLU>;
+  constexpr bool SCALED = MODE == MODE_PER_TOKEN || MODE == MODE_PER_GROUP;
+  constexpr int smem = STAGES * ((BM + BN) * 128 + (SCALED ? BN * 16 : 0)) +
+                       (MODE == MODE_PER_GROUP ? (STAGES + 1) * BM * 16 : BM * 4);
+  static_assert(smem <= 160 * 1024, "LDS");
+  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16, MINW, GLU, WSF16>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -620,7 +689,7 @@ static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, g.A, g.AS, g.W, g.WS,
                      g.ws_stride, g.C, g.M, g.N, g.K, tm, tn, rk_knob("RK_TILE_GROUP_M", 0),
-                     GLU != GLU_NONE ? g.n_out : g.N);
+                     GLU != GLU_NONE ? g.n_out : g.N, g.as_stride);
   return hipGetLastError();
 }
 
@@ -713,6 +782,16 @@ static hipError_t dispatch_scaled(const I8GemmArgs &g, hipStream_t st) {
   return g.out_f16 ? dispatch_i8<MODE, true, false>(g, st) : dispatch_i8<MODE, false, false>(g, st);
 }
 
+// Group-32 activations on the pipelined kernel, one 32x32 tile per wave:
+// 0 128x128 on 16 waves, 1 128x64 on 8, 2 64x128 on 8 (the default: config-2
+// pair 100 us against 111 and 105 us on MI355X).
+template <bool OUT_F16, bool WSF16>
+static hipError_t launch_q8g(int c, const I8GemmArgs &g, hipStream_t st) {
+  if (c == 0) return launch_q8<128, 128, 4, 4, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+  if (c == 1) return launch_q8<128, 64, 4, 2, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+  return launch_q8<64, 128, 2, 4, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+}
+
 hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
   switch (g.mode) {
     case I8_PER_TOKEN:
@@ -727,6 +806,14 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
       if (g.glu != 0) return hipErrorInvalidValue;
       return dispatch_scaled<MODE_PER_TOKEN>(g, st);
     case I8_PER_GROUP:
+      // Group-32 activations against a group-32 weight: pipelined kernel
+      // (launch_q8g; RK_Q8G_TILE selects the tile).
+      if (g.gb == 1 && g.a_gb == 1 && g.glu == 0) {
+        const int knob = rk_knob("RK_Q8G_TILE", -1);
+        const int c = knob >= 0 ? knob : 2;
+        return g.ws_f16 ? (g.out_f16 ? launch_q8g<true, true>(c, g, st) : launch_q8g<false, true>(c, g, st))
+                        : (g.out_f16 ? launch_q8g<true, false>(c, g, st) : launch_q8g<false, false>(c, g, st));
+      }
       return dispatch_scaled<MODE_PER_GROUP>(g, st);
     case I8_RAW:
       return launch_q8<128, 128, 2, 2, 2, MODE_RAW, false>(g, st);

@@ -41,6 +41,7 @@ struct I8GemmArgs {
   const int8_t *W;     // [N, K]
   const float *WS;     // weight scale per 32-block [N, ws_stride]
   int ws_stride;       // K/32 rounded up to a multiple of 4
+  bool ws_f16 = false; // every weight scale is an fp16 value
   int gb;              // weight group / 32
   void *C;             // f32 / fp16 [M, N], int32 [M, N] (RAW), int32 [M, N, K/32] (PARTIALS)
   int M, N, K;

@@ -136,6 +136,45 @@ def test_per_token_w8a8_full_config2(rk, orc, config2, f16out):
             assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("f16out", [False, True])
+def test_group32_w8a8_full_config2(rk, orc, config2, f16out):
+    # The reference's own W8A8 form at config 2: activations quantized per row
+    # per 32-value group (quantize_i8_rows, ext.rs:1505-1554), Σ_g (a_s·w_s)·P_g.
+    for name in ("up", "down"):
+        d = config2[name]
+        m, k = d["x"].shape
+        note(f"W8A8 group-32 {name} m={m} k={k} f16out={f16out}")
+        dq, ds = quantize_dev(rk, d["x"], 32)
+        got = w8a8_dev(rk, d["wid"], dq, ds, 32, m, k, f16out)
+        aq, a_s = orc.quantize_rows(d["x"], 32)
+        ref = orc.emu_matmul_gw(aq, a_s, 32, d["wq"], d["ws"], 32)
+        check(orc, got, ref)
+        if not f16out:
+            assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+# Every tile configuration of the group-32 pipelined path (RK_Q8G_TILE), with
+# ragged M and N, odd and even block counts and a K tail inside a stage.
+@pytest.mark.parametrize("tile", [0, 1, 2])
+def test_group32_w8a8_every_tile_config(rk, orc, tile, monkeypatch):
+    monkeypatch.setenv("RK_Q8G_TILE", str(tile))
+    for m, k, n in ((300, 416, 200), (257, 1024, 392), (1, 32, 1)):
+        note(f"W8A8 group-32 RK_Q8G_TILE={tile} m={m} k={k} n={n}")
+        r = np.random.default_rng(tile * 5 + m + k + n)
+        x = r.standard_normal((m, k)).astype(np.float32)
+        w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+        wq, wd = orc.q8_0_quantize(w)
+        wid = rk.pack_q8_0(orc.q8_0_blocks(wq, wd), n, k)
+        aq, a_s = orc.quantize_rows(x, 32)
+        dq, ds = quantize_dev(rk, x, 32)
+        ref = orc.emu_matmul_gw(aq, a_s, 32, wq, wd.view(np.float16).astype(np.float32), 32)
+        for f16out in (False, True):
+            got = w8a8_dev(rk, wid, dq, ds, 32, m, k, f16out)
+            check(orc, got, ref)
+            if not f16out:
+                assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_group_wise_host_matmul_matches_matmul_gw(rk, orc, group):
     note(f"rk_matmul pack_i8 group={group}")
