@@ -340,22 +340,27 @@ def extra_moe(iters):
 def extra_w8a8_forms(layers, iters):
     """Config 2 in the reference's own W8A8 form (activations quantized per row per
     32-value group, Σ_g (a_s·w_s)·P_g: matmul_i8 + quantize_i8_rows, ext.rs:1017-1029,
-    1505-1554), and the per-token activation quantizer the headline step runs
-    before its timed region."""
+    1505-1554), the raw int32 product of the same codes (no scale fold: the pipeline's
+    own ceiling at this shape), and the per-token activation quantizer the headline step
+    runs before its timed region."""
     lib = rk.lib()
     out = {}
-    g_ms, q_ms = 0.0, 0.0
+    g_ms, q_ms, r_ms = 0.0, 0.0, 0.0
     for L in layers:
         m, k = L["m"], L["k"]
         q32, s32 = rk.DeviceBuffer(m * k), rk.DeviceBuffer(m * (k // 32) * 4)
         call(lib.rk_quantize_rows_dev(L["dx"].ptr, m, k, 32, q32.ptr, s32.ptr, None), "quantize g32")
         g_ms += time_launches(lambda: call(lib.rk_matmul_w8a8_dev(int(L["wid"]), q32.ptr, s32.ptr, 32, m, k,
                                                                   L["dc"].ptr, None), "w8a8 g32"), iters)
+        # raw int32 product (I8Context::matmul, int8.rs:606-640): no scale fold at all
+        r_ms += time_launches(lambda: call(lib.rk_matmul_i8_raw_dev(int(L["wid"]), L["dq"].ptr, m, k, L["dc"].ptr,
+                                                                    None), "w8a8 raw"), iters)
         q_ms += time_launches(lambda: call(lib.rk_quantize_rows_dev(L["dx"].ptr, m, k, k, L["dq"].ptr, L["ds"].ptr,
                                                                     None), "quantize"), iters)
     m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]
     ops = 2 * 2.0 * m * h * i
     out["group32_pair"] = {"ms": g_ms, "tops": ops / g_ms / 1e9, "frac_int8_peak": ops / g_ms / 1e9 / PEAK_INT8}
+    out["raw_int32_pair"] = {"ms": r_ms, "tops": ops / r_ms / 1e9, "frac_int8_peak": ops / r_ms / 1e9 / PEAK_INT8}
     x_bytes = 4.0 * m * (h + i)
     out["per_token_quantizer_both_inputs"] = {"ms": q_ms, "gbps": (x_bytes + x_bytes / 4) / q_ms / 1e6}
     return out
