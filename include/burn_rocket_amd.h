@@ -454,11 +454,14 @@ int rk_attention_qkv_dev(void *qkv, int64_t s, int64_t row_stride, int n_head, i
                          const void *cos, const void *sin, int cs_dtype, float scale,
                          float softcap, int mask_mode, int64_t window, int64_t q0, int64_t k0,
                          void *out, int64_t out_stride, rk_stream stream);
-/* RMSNorm then per-token int8 quantization in one pass, the activation input
- * of a per-token W8A8 GEMM after a norm (the Qwen3 MLP: `post_attention_layernorm`
- * through `burn_rocket::rms_norm` ext.rs:2112-2119, then `matmul` on an I8
- * weight, whose host side quantizes each row, ext.rs:1017-1029 with
- * quantize_row_groups host.rs:77-90): y = rk_rms_norm_dev's result in dtype
+/* RMSNorm then per-token int8 quantization in one pass: the activation input
+ * of a per-token W8A8 GEMM (rk_matmul_w8a8_dev with a_group = K) after a norm,
+ * e.g. the Qwen3 MLP input (`post_attention_layernorm` through
+ * `burn_rocket::rms_norm`, ext.rs:2112-2119). It is not the reference's own
+ * I8 matmul input: that quantizes each row per weight group (ext.rs:1017-1029
+ * with quantize_row_groups host.rs:77-90; 32 values for Q8_0 weights), which
+ * rk_rms_norm_dev followed by rk_quantize_rows_dev with group 32 produces.
+ * y = rk_rms_norm_dev's result in dtype
  * (w NULL: scale-free; else w_dtype must equal dtype), then q_scale[row] =
  * max(amax(y)/127, 1e-12) and q = round-half-away(y·(1/q_scale)) clamped to
  * ±127, q int8 [rows, d]. RK_E_UNSUPPORTED unless d·sizeof(dtype) is a
