@@ -691,8 +691,12 @@ static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
     attr_set = true;
   }
   const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+  // Tiles in groups of 8 tile rows (row-fastest inside a group): one XCD's run
+  // of consecutive tiles re-reads a few A row blocks from its L2 instead of
+  // streaming all of A (M=3633 down-projection: 108 MB fetched per launch
+  // row-fastest over the whole grid; 3-4 % faster on both projections).
   hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, g.A, g.AS, g.W, g.WS,
-                     g.ws_stride, g.C, g.M, g.N, g.K, tm, tn, rk_knob("RK_TILE_GROUP_M", 0),
+                     g.ws_stride, g.C, g.M, g.N, g.K, tm, tn, rk_knob("RK_TILE_GROUP_M", 8),
                      GLU != GLU_NONE ? g.n_out : g.N, g.as_stride);
   return hipGetLastError();
 }
