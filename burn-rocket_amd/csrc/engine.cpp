@@ -1353,6 +1353,7 @@ struct MoePlan {
   int top_k = 0;
   int64_t rows = 0;
   int n_tiles = 0;
+  int tile_rows = 128;        // rows per tile at most (the kernels' tile size)
   int32_t *tok = nullptr;     // [rows] token of each bucket row
   float *roww = nullptr;      // [rows] router weight of each bucket row
   int32_t *slot = nullptr;    // [s, top_k] bucket rows of a token, ascending expert id
@@ -1376,7 +1377,9 @@ void plan_free(MoePlan *p) {
 }
 
 // Bucket the (token, slot) pairs per expert in ascending token order
-// (engine.rs:292-305), list ≤128-row tiles, and sort each token's slot rows by
+// (engine.rs:292-305), list tiles of ≤ rk_moe_tile_rows() rows (two tiles of
+// one expert sit next to each other, so the second read of its weights is
+// mostly served from cache), and sort each token's slot rows by
 // expert id for the combine; the lists are copied into the plan's buffers.
 int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const float *wts,
              MoePlan *plan, hipStream_t st) {
@@ -1405,9 +1408,10 @@ int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const f
   // slots by row is ordering them by expert id.
   for (int64_t t = 0; t < s; ++t) std::sort(slot.begin() + t * top_k, slot.begin() + (t + 1) * top_k);
   std::vector<MoeTile> tiles;
+  const int tr = rk_moe_tile_rows();
   for (int e = 0; e < E; ++e)
-    for (int64_t r = off[e]; r < off[e + 1]; r += 128)
-      tiles.push_back(MoeTile{e, (int)r, (int)std::min<int64_t>(128, off[e + 1] - r)});
+    for (int64_t r = off[e]; r < off[e + 1]; r += tr)
+      tiles.push_back(MoeTile{e, (int)r, (int)std::min<int64_t>(tr, off[e + 1] - r)});
   HIP_TRY(hipMalloc((void **)&plan->tok, std::max<size_t>(R, 1) * 4), op);
   HIP_TRY(hipMalloc((void **)&plan->roww, std::max<size_t>(R, 1) * 4), op);
   HIP_TRY(hipMalloc((void **)&plan->slot, std::max<size_t>(slot.size(), 1) * 4), op);
@@ -1427,6 +1431,7 @@ int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const f
   plan->top_k = top_k;
   plan->rows = R;
   plan->n_tiles = (int)tiles.size();
+  plan->tile_rows = tr;
   return RK_OK;
 }
 
@@ -1449,7 +1454,7 @@ int moe_run(CallScope &cs, const Weight &w, const MoePlan &plan, const float *x,
   // x and the silu·up rows are quantized per row per 32-value group, as the
   // reference's expert workers do (engine.rs:1005-1006, 1034-1035).
   HIP_TRY(rk_launch_quantize_rows(x, S, H, 32, (int8_t *)xq, (float *)xs, st), op);
-  HIP_TRY(rk_launch_moe_gemm_gu((const int8_t *)xq, (const float *)xs, (int)KBh, plan.tok, S,
+  HIP_TRY(rk_launch_moe_gemm_gu(plan.tile_rows, (const int8_t *)xq, (const float *)xs, (int)KBh, plan.tok, S,
                                 plan.tiles, plan.n_tiles, w.gu_codes, w.gu_scales,
                                 moe_gu_code_stride(w), 2 * I * w.gu_ws_stride, w.gu_ws_stride,
                                 (int)(2 * I), (int)H, (float *)act, g_eng->num_cus, st),
@@ -1457,7 +1462,7 @@ int moe_run(CallScope &cs, const Weight &w, const MoePlan &plan, const float *x,
   if (!y) return RK_OK;  // stage 1 only
   HIP_TRY(rk_launch_quantize_rows((const float *)act, plan.rows, I, 32, (int8_t *)aq, (float *)as, st),
           op);
-  HIP_TRY(rk_launch_moe_gemm_down((const int8_t *)aq, (const float *)as, (int)KBi, plan.rows,
+  HIP_TRY(rk_launch_moe_gemm_down(plan.tile_rows, (const int8_t *)aq, (const float *)as, (int)KBi, plan.rows,
                                   plan.tiles, plan.n_tiles, w.dn_codes, w.dn_scales,
                                   moe_dn_code_stride(w), H * w.dn_ws_stride, w.dn_ws_stride, (int)H,
                                   (int)I, plan.roww, (float *)yb, g_eng->num_cus, st),

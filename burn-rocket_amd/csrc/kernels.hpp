@@ -172,12 +172,15 @@ struct MoeTile {
 // a_rows: rows of the activation buffer (s tokens for gate|up, bucket rows
 // for down); offsets into it are 32-bit, so a_rows·K < 2^31. The activation
 // scales are per row per 32-value group: [a_rows, stride] with stride = K/32.
-hipError_t rk_launch_moe_gemm_gu(const int8_t *xq, const float *xs, int xs_stride,
+// Tiles hold at most tile_rows (64 or 128) bucket rows: rk_moe_tile_rows() is
+// the size a new plan lists (RK_MOE_ROWS), the launches take the plan's.
+int rk_moe_tile_rows();
+hipError_t rk_launch_moe_gemm_gu(int tile_rows, const int8_t *xq, const float *xs, int xs_stride,
                                  const int32_t *tok, int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
                                  const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                  int ws_stride, int N, int K, float *act, int num_cus,
                                  hipStream_t st);
-hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, int as_stride, int64_t rows,
+hipError_t rk_launch_moe_gemm_down(int tile_rows, const int8_t *aq, const float *as, int as_stride, int64_t rows,
                                    const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
                                    int64_t w_stride_e, int64_t ws_stride_e, int ws_stride,
                                    int N, int K, const float *row_w, float *yb, int num_cus,

@@ -52,19 +52,21 @@
 #include "kernels.hpp"
 
 namespace {
-constexpr int MOE_BM = 128;    // rows per tile (the host lists tiles of ≤128 rows)
 constexpr int MOE_ROWB = 128;  // K bytes of one stage row
-constexpr int MOE_A_STAGE = MOE_BM * MOE_ROWB;  // token-row codes of one stage
-constexpr int MOE_S_STAGE = 4 * MOE_BM * 4;     // their scales, [block 0..3][row]
-constexpr int MOE_SLOT = MOE_A_STAGE + MOE_S_STAGE;
 constexpr int MOE_BIAS_BITS = 0x4B400000;  // 1.5·2^23 as f32 bits
 constexpr float MOE_BIAS = 12582912.0f;
 
+// Per BM-row tile (BM = 64 or 128, the host's tile size): token-row codes of
+// one stage, their scales [block 0..3][row], one LDS ring slot.
+template <int BM> constexpr int moe_a_stage() { return BM * MOE_ROWB; }
+template <int BM> constexpr int moe_s_stage() { return 4 * BM * 4; }
+template <int BM> constexpr int moe_slot() { return moe_a_stage<BM>() + moe_s_stage<BM>(); }
+
 // LDS: the (PD+1)-slot ring of token-row stages with their scales, then the
 // router weight of each tile row.
-template <int PD>
+template <int PD, int BM>
 constexpr int moe_smem() {
-  return (PD + 1) * MOE_SLOT + MOE_BM * 4;
+  return (PD + 1) * moe_slot<BM>() + BM * 4;
 }
 }  // namespace
 
@@ -78,16 +80,17 @@ __device__ __forceinline__ void bdma4(rsrc_t r, void *lds_base, uint32_t voff, u
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds_base), 4, voff, soff, 0, 0);
 }
 
-template <bool GU, int NW, int PD, int NRB>
+template <bool GU, int NW, int PD, int BM, int NRB>
 __device__ __forceinline__ void moe_body(
     const int8_t *__restrict__ A, const float *__restrict__ AS, int as_stride,
     const int32_t *__restrict__ tok, int64_t a_rows, const MoeTile &tile,
     const int8_t *__restrict__ We, const float *__restrict__ WSe, int ws_stride, int N, int K,
     int n0, const float *__restrict__ row_w, float *__restrict__ out, int out_ld, uint8_t *smem) {
-  constexpr int BM = MOE_BM, ROWB = MOE_ROWB, NSLOT = PD + 1;
+  constexpr int ROWB = MOE_ROWB, NSLOT = PD + 1;
+  constexpr int MOE_A_STAGE = moe_a_stage<BM>(), MOE_SLOT = moe_slot<BM>();
   constexpr int QA = BM / 8;     // 8-row copies of token rows per stage
   constexpr int CPA = QA / NW;   // of them per wave
-  constexpr int SC = 8;          // 4-byte scale copies per stage: 4 blocks × 2 halves of 64 rows
+  constexpr int SC = BM / 16;    // 4-byte scale copies per stage: 4 blocks × BM/64 runs of 64 rows
   constexpr int SPW = SC / NW;   // of them per wave
   constexpr int VM = CPA + 4 + 1 + SPW;  // memory ops per wave and stage
   static_assert(CPA * NW == QA && SPW * NW == SC, "copies per wave");
@@ -158,7 +161,7 @@ __device__ __forceinline__ void moe_body(
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
       const int c = wave + i * NW;
-      bdma4(ras, sb + MOE_A_STAGE + (c & 3) * 512 + (c >> 2) * 256, voff_as[i], kt * 16);
+      bdma4(ras, sb + MOE_A_STAGE + (c & 3) * (BM * 4) + (c >> 2) * 256, voff_as[i], kt * 16);
     }
   };
 
@@ -180,7 +183,7 @@ __device__ __forceinline__ void moe_body(
   auto load_as = [&](float(&v)[16], auto slot_c, auto b_c, auto u_c) {
     constexpr int slot = decltype(slot_c)::value, b = decltype(b_c)::value,
                   u = decltype(u_c)::value;
-    const float *p = (const float *)(smem + slot * MOE_SLOT + MOE_A_STAGE + b * 512) + u * 32 + fh * 4;
+    const float *p = (const float *)(smem + slot * MOE_SLOT + MOE_A_STAGE + b * (BM * 4)) + u * 32 + fh * 4;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const floatx4 t = *(const floatx4 *)(p + q * 8);
@@ -355,7 +358,7 @@ __device__ __forceinline__ void moe_body(
   }
 }
 
-template <bool GU, int NW, int PD>
+template <bool GU, int NW, int PD, int BM>
 __global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
     const int8_t *__restrict__ A, const float *__restrict__ AS, int as_stride,
     const int32_t *__restrict__ tok, int64_t a_rows, const MoeTile *__restrict__ tiles, int n_col_tiles,
@@ -370,35 +373,26 @@ __global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
   const int n0 = (L % n_col_tiles) * 32 * NW;
   const int8_t *We = W + (int64_t)tile.expert * w_stride_e;
   const float *WSe = WS + (int64_t)tile.expert * ws_stride_e;
-  switch ((tile.rows + 31) >> 5) {
-    case 1:
-      moe_body<GU, NW, PD, 1>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
-                              row_w, out, out_ld, smem);
-      break;
-    case 2:
-      moe_body<GU, NW, PD, 2>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
-                              row_w, out, out_ld, smem);
-      break;
-    case 3:
-      moe_body<GU, NW, PD, 3>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
-                              row_w, out, out_ld, smem);
-      break;
-    default:
-      moe_body<GU, NW, PD, 4>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
-                              row_w, out, out_ld, smem);
-      break;
-  }
+  // The body is instantiated per count of 32-row blocks holding rows; the
+  // registers of the largest (BM / 32) set the kernel's.
+  const int nrb = (tile.rows + 31) >> 5;
+  static_for<BM / 32>([&](auto u_c) {
+    constexpr int NRB = decltype(u_c)::value + 1;
+    if (nrb == NRB || (NRB == BM / 32 && nrb > NRB))
+      moe_body<GU, NW, PD, BM, NRB>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
+                                    row_w, out, out_ld, smem);
+  });
 }
 
-template <bool GU, int NW, int PD>
+template <bool GU, int NW, int PD, int BM>
 static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, int as_stride, const int32_t *tok,
                                  int64_t a_rows, const MoeTile *tiles, int n_tiles,
                                  const int8_t *w, const float *ws, int64_t w_stride_e,
                                  int64_t ws_stride_e, int ws_stride, int N, int K,
                                  const float *row_w, float *out, int out_ld, hipStream_t st) {
-  constexpr int smem = moe_smem<PD>();
+  constexpr int smem = moe_smem<PD, BM>();
   static_assert(smem <= 160 * 1024, "LDS per workgroup");
-  auto kern = moe_q8_kernel<GU, NW, PD>;
+  auto kern = moe_q8_kernel<GU, NW, PD, BM>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -413,49 +407,58 @@ static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, int as_stride
   return hipGetLastError();
 }
 
-// Workgroup shapes (RK_MOE_TILE): 0 = 4 waves × 128 columns, weights 2
-// stages ahead (two workgroups per CU); 1 = 8 waves × 256 columns, 3 ahead;
-// 2 = 4 waves, 3 ahead; 3 = 4 waves, 4 ahead (one workgroup per CU by LDS).
+int rk_moe_tile_rows() { return rk_knob("RK_MOE_ROWS", 64) == 128 ? 128 : 64; }
+
+// Workgroup shapes (RK_MOE_TILE) for tiles of ≤128 rows: 0 = 4 waves × 128
+// columns, weights 2 stages ahead (two workgroups per CU); 1 = 8 waves × 256
+// columns, 3 ahead; 2 = 4 waves, 3 ahead; 3 = 4 waves, 4 ahead (one workgroup
+// per CU by LDS). Tiles of ≤64 rows (half the accumulator and fragment
+// registers): 4 waves × 128 columns, weights PD stages ahead, RK_MOE_TILE
+// 0 / 2 / 3 / 4 for PD = 4 / 2 / 3 / 5.
 template <bool GU>
-static hipError_t launch_moe(const int8_t *A, const float *AS, int as_stride, const int32_t *tok,
+static hipError_t launch_moe(int tile_rows, const int8_t *A, const float *AS, int as_stride, const int32_t *tok,
                              int64_t a_rows,
                              const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
                              int64_t w_stride_e, int64_t ws_stride_e, int ws_stride, int N,
                              int K, const float *row_w, float *out, int out_ld, hipStream_t st) {
   if (n_tiles == 0) return hipSuccess;
-  switch (rk_knob("RK_MOE_TILE", 0)) {
-    case 1:
-      return launch_moe_cfg<GU, 8, 3>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
-                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
-    case 2:
-      return launch_moe_cfg<GU, 4, 3>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
-                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
-    case 3:
-      return launch_moe_cfg<GU, 4, 4>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
-                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
-    default:
-      return launch_moe_cfg<GU, 4, 2>(A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e,
-                                      ws_stride_e, ws_stride, N, K, row_w, out, out_ld, st);
+#define RK_MOE_ARGS A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e, ws_stride, N, K, \
+                    row_w, out, out_ld, st
+  if (tile_rows == 64) {
+    switch (rk_knob("RK_MOE_TILE", 0)) {
+      case 2: return launch_moe_cfg<GU, 4, 2, 64>(RK_MOE_ARGS);
+      case 3: return launch_moe_cfg<GU, 4, 3, 64>(RK_MOE_ARGS);
+      case 4: return launch_moe_cfg<GU, 4, 5, 64>(RK_MOE_ARGS);
+      default: return launch_moe_cfg<GU, 4, 4, 64>(RK_MOE_ARGS);
+    }
   }
+  if (tile_rows != 128) return hipErrorInvalidValue;
+  switch (rk_knob("RK_MOE_TILE", 0)) {
+    case 1: return launch_moe_cfg<GU, 8, 3, 128>(RK_MOE_ARGS);
+    case 2: return launch_moe_cfg<GU, 4, 3, 128>(RK_MOE_ARGS);
+    case 3: return launch_moe_cfg<GU, 4, 4, 128>(RK_MOE_ARGS);
+    default: return launch_moe_cfg<GU, 4, 2, 128>(RK_MOE_ARGS);
+  }
+#undef RK_MOE_ARGS
 }
 
-hipError_t rk_launch_moe_gemm_gu(const int8_t *xq, const float *xs, int xs_stride,
+hipError_t rk_launch_moe_gemm_gu(int tile_rows, const int8_t *xq, const float *xs, int xs_stride,
                                  const int32_t *tok, int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
                                  const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                  int ws_stride, int N, int K, float *act, int num_cus,
                                  hipStream_t st) {
   (void)num_cus;
-  return launch_moe<true>(xq, xs, xs_stride, tok, s, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
+  return launch_moe<true>(tile_rows, xq, xs, xs_stride, tok, s, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
                           ws_stride, N, K, nullptr, act, N / 2, st);
 }
 
-hipError_t rk_launch_moe_gemm_down(const int8_t *aq, const float *as, int as_stride, int64_t rows,
+hipError_t rk_launch_moe_gemm_down(int tile_rows, const int8_t *aq, const float *as, int as_stride, int64_t rows,
                                    const MoeTile *tiles, int n_tiles, const int8_t *w,
                                    const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                    int ws_stride, int N, int K, const float *row_w, float *yb,
                                    int num_cus, hipStream_t st) {
   (void)num_cus;
-  return launch_moe<false>(aq, as, as_stride, nullptr, rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
+  return launch_moe<false>(tile_rows, aq, as, as_stride, nullptr, rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
                            ws_stride, N, K, row_w, yb, N, st);
 }
 

@@ -245,13 +245,17 @@ def test_pack_moe_f32_equals_pack_from_blocks(rk, orc):
     assert (a1 == a2).all() and (y1 == y2).all()
 
 
-# Every workgroup shape of the expert kernels (RK_MOE_TILE): 4 or 8 waves,
-# 2 or 3 stages; tiles of 1..4 row blocks, several tiles per expert, and a
-# gate|up width (2·inter = 128) below one 256-column slice.
-@pytest.mark.parametrize("tile", [0, 1, 2, 3])
-def test_moe_every_tile_config(rk, orc, tile, monkeypatch):
+# Every workgroup shape of the expert kernels: tiles of ≤128 rows (RK_MOE_ROWS
+# 128; RK_MOE_TILE 0-3: 4 or 8 waves, 2-4 stages ahead) and of ≤64 rows (the
+# default; RK_MOE_TILE 0, 2, 3, 4: 4, 2, 3, 5 stages ahead); tiles of 1..4 row
+# blocks, several tiles per expert, and a gate|up width (2·inter = 128) below
+# one 256-column slice.
+@pytest.mark.parametrize("rows,tile", [(128, 0), (128, 1), (128, 2), (128, 3), (64, 0), (64, 2), (64, 3),
+                                       (64, 4)])
+def test_moe_every_tile_config(rk, orc, rows, tile, monkeypatch):
+    monkeypatch.setenv("RK_MOE_ROWS", str(rows))
     monkeypatch.setenv("RK_MOE_TILE", str(tile))
-    note(f"MoE RK_MOE_TILE={tile}")
+    note(f"MoE RK_MOE_ROWS={rows} RK_MOE_TILE={tile}")
     r = np.random.default_rng(40 + tile)
     ids, wts = rk.moe_route(r.standard_normal((300, 8)).astype(np.float32), 8)
     check_pipeline(rk, orc, 300, 256, 128, 8, ids, wts, 1200 + tile)
