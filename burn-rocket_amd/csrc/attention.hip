@@ -31,7 +31,9 @@
 //               the rest): fp16-rounded P alone leaves ~2^-12 relative noise
 //               per probability, above the parity gate for small outputs;
 //   Oᵀ += Vᵀ·Pᵀ A = Vᵀ rows from LDS, B = P hi and lo; Oᵀ keeps the query per
-//               lane, so the online-softmax rescale is a per-lane scalar.
+//               lane, so the online-softmax rescale is a per-lane scalar. With
+//               a padded head dim (72 → 80) Vᵀ row 72 is all ones in LDS and
+//               Oᵀ row 72 is the row sum of P.
 //
 // LDS: per group two buffers of {K tile: 64 rows of KPC 16-byte chunks (8
 // for d ≤ 64, else 16: 256-byte rows) with chunk c of row r at
@@ -177,7 +179,15 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   constexpr bool TAIL16 = Gm::TAIL16;
   constexpr int KROW = Gm::KROW, KPC = Gm::KPC;
   constexpr int K_BYTES = Gm::K_BYTES, BUF_BYTES = Gm::BUF_BYTES;
-  constexpr int K_INS = Gm::K_INS, V_INS = Gm::V_INS;
+  constexpr int K_INS = Gm::K_INS;
+  // A head dim padded to DV (72 → 80): Vᵀ row D of every LDS buffer holds ones,
+  // so O row D of the PV product is the softmax row sum l (the MFMAs compute it
+  // from the same hi + lo probabilities, and the rescale of O rescales it), and
+  // the VALU slot keeps no sums. The rows D..DV-1 are written once and never
+  // copied.
+  constexpr bool LROW = D < DV;
+  static_assert(!LROW || D % 8 == 0, "Vᵀ copies move 8-row groups");
+  constexpr int V_INS = LROW ? D / 8 : Gm::V_INS;
   constexpr int CPW = (K_INS + V_INS + NWG - 1) / NWG;  // copies per wave of a group
   // Reads ahead: fewer with 3 waves per SIMD, whose register budget is 168.
   constexpr int LAW = NWG == 4 ? LA : 3;
@@ -474,10 +484,21 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
           phi[qb][c2] = __builtin_bit_cast(half8, hw);
           plo[qb][c2] = __builtin_bit_cast(half8, lw);
         }
-        l_run[qb] += lsum;
+        if constexpr (!LROW) l_run[qb] += lsum;
       }
       WAIT_VMCNT(0);  // K(j+1) and Vᵀ(j) land before the next MFMA slot
     };
+    if constexpr (LROW) {
+      // Vᵀ rows D..DV-1 of the four buffers: row D = 1.0 per key slot, the rest 0.
+      for (int i = threadIdx.x; i < 4 * (DV - D) * 8; i += 2 * NWG * 64) {
+        const int buf = i / ((DV - D) * 8), j = i % ((DV - D) * 8);
+        const int row = D + j / 8;
+        const unsigned one2 = row == D ? 0x3c003c00u : 0u;  // two fp16 1.0
+        *(uintx4 *)(smem + buf * BUF_BYTES + K_BYTES + row * 128 + (j % 8) * 16) =
+            uintx4{one2, one2, one2, one2};
+      }
+      WAIT_LGKMCNT0();
+    }
     issue(nj > 0 ? kt_begin + grp : -1, 0, -1, 0);
     WAIT_VMCNT(0);
     BARRIER();
@@ -509,7 +530,14 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     BARRIER();  // all compute done: the K/V buffers are free
     float lt[2];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) lt[qb] = sum4groups(l_run[qb]);
+    for (int qb = 0; qb < 2; ++qb) {
+      if constexpr (LROW) {
+        // O row D (block D/16, lane group (D%16)/4, element D%4) of this query.
+        lt[qb] = __shfl(o[D / 16][qb][D % 4], l16 + 16 * ((D % 16) / 4));
+      } else {
+        lt[qb] = sum4groups(l_run[qb]);
+      }
+    }
     if (grp == 1) {
       float *p = xch + lane;
 #pragma unroll
