@@ -352,10 +352,11 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   // own ring of STAGES + 1 slots, [block][row], filled by 4-byte copies
   // (AS_INS of 64 per stage): a slot outlives its stage's code slot, which is
   // refilled while the last block's last tile is still to be folded. One row
-  // of 32 tiles per wave (TM = 1) keeps two 16-row scale sets in registers.
+  // of 32 tiles per wave (TM = 1) keeps one 16-row scale set in registers,
+  // shared by the wave's TN column tiles.
   constexpr int AS_SLOT = GROUPED ? BM * 16 : 0;
   constexpr int AS_INS = GROUPED ? BM * 4 / 64 : 0;
-  static_assert(!GROUPED || (TM == 1 && TN == 1), "per-group mode: one 32x32 tile per wave");
+  static_assert(!GROUPED || TM == 1, "per-group mode: one row of 32x32 tiles per wave");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float *s_as = (float *)(smem + STAGES * STAGE_BYTES);  // [BM] per-token activation scales
@@ -592,7 +593,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
         constexpr int u = decltype(uc)::value + 1;
         constexpr int I = u / TN, J = u % TN;
         constexpr int PI = (u - 1) / TN, PJ = (u - 1) % TN;
-        ires[(P0 + u) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][I], bf[CUR][J], intx16{}, 0, 0, 0);
+        ires[(P0 + u) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[CUR][I], bf[CUR][J], cinit, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         fold(ic<(P0 + u - 1) & 1>{}, ic<PI>{}, ic<PJ>{}, dsc[CUR][PJ], as_pend);
         __builtin_amdgcn_sched_barrier(0);
@@ -790,13 +791,27 @@ static hipError_t dispatch_scaled(const I8GemmArgs &g, hipStream_t st) {
   return g.out_f16 ? dispatch_i8<MODE, true, false>(g, st) : dispatch_i8<MODE, false, false>(g, st);
 }
 
-// Group-32 activations on the pipelined kernel, one 32x32 tile per wave:
-// 0 128x128 on 16 waves, 1 128x64 on 8, 2 64x128 on 8 (the default: config-2
-// pair 100 us against 111 and 105 us on MI355X).
+// Group-32 activations on the pipelined kernel. Each wave owns one row of
+// 32x32 tiles (its 16 activation scales per block serve every tile of the
+// row). By default 128x128 tiles on 4 waves of 32x128 (7) when there are at
+// least as many 128x128 tiles as CUs, else 128x64 on 4 waves of 32x64 (8):
+// two workgroups per CU with up to 256 registers per wave. On MI355X at
+// M=3633 the up-projection 3072x1024 takes 40.6 us with 7 against 46-49 us
+// with 2 (64x128 on 8 waves of 32x32), the down-projection 1024x3072 40.4 us
+// with 8 against 43.5 us. Wider wave tiles on 8 waves (3-6) spill under their
+// 128-register budget. RK_Q8G_TILE selects a configuration by number.
 template <bool OUT_F16, bool WSF16>
 static hipError_t launch_q8g(int c, const I8GemmArgs &g, hipStream_t st) {
   if (c == 0) return launch_q8<128, 128, 4, 4, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
   if (c == 1) return launch_q8<128, 64, 4, 2, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+  if (c == 3) return launch_q8<128, 128, 4, 2, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+  if (c == 4) return launch_q8<128, 256, 4, 4, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+  if (c == 5) return launch_q8<256, 128, 8, 2, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+  if (c == 6) return launch_q8<64, 128, 2, 2, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
+  if (c == 7) return launch_q8<128, 128, 4, 1, 2, MODE_PER_GROUP, OUT_F16, 2, GLU_NONE, WSF16>(g, st);
+  if (c == 8) return launch_q8<128, 64, 4, 1, 2, MODE_PER_GROUP, OUT_F16, 2, GLU_NONE, WSF16>(g, st);
+  if (c == 9) return launch_q8<64, 128, 2, 1, 2, MODE_PER_GROUP, OUT_F16, 2, GLU_NONE, WSF16>(g, st);
+  if (c == 10) return launch_q8<128, 128, 4, 1, 3, MODE_PER_GROUP, OUT_F16, 2, GLU_NONE, WSF16>(g, st);
   return launch_q8<64, 128, 2, 4, 2, MODE_PER_GROUP, OUT_F16, 4, GLU_NONE, WSF16>(g, st);
 }
 
@@ -818,7 +833,8 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
       // (launch_q8g; RK_Q8G_TILE selects the tile).
       if (g.gb == 1 && g.a_gb == 1 && g.glu == 0) {
         const int knob = rk_knob("RK_Q8G_TILE", -1);
-        const int c = knob >= 0 ? knob : 2;
+        const long t128 = ((g.M + 127) / 128) * (long)((g.N + 127) / 128);
+        const int c = knob >= 0 ? knob : (t128 >= g.num_cus ? 7 : 8);
         return g.ws_f16 ? (g.out_f16 ? launch_q8g<true, true>(c, g, st) : launch_q8g<false, true>(c, g, st))
                         : (g.out_f16 ? launch_q8g<true, false>(c, g, st) : launch_q8g<false, false>(c, g, st));
       }

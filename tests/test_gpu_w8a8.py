@@ -155,7 +155,7 @@ def test_group32_w8a8_full_config2(rk, orc, config2, f16out):
 
 # Every tile configuration of the group-32 pipelined path (RK_Q8G_TILE), with
 # ragged M and N, odd and even block counts and a K tail inside a stage.
-@pytest.mark.parametrize("tile", [0, 1, 2])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 def test_group32_w8a8_every_tile_config(rk, orc, tile, monkeypatch):
     monkeypatch.setenv("RK_Q8G_TILE", str(tile))
     for m, k, n in ((300, 416, 200), (257, 1024, 392), (1, 32, 1)):
