@@ -629,7 +629,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=100)
+    # ~65 ms of warm-up steps: the card's clocks take tens of ms of sustained work to settle
+    # (100 steps, ~7 ms, leave the pair at 67 us per step against 60 us once settled)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=1.0,
