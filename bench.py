@@ -148,14 +148,22 @@ def traffic_probe(layers, launches):
 
 def probe_all(launches):
     """A few launches of every workload's kernels (for rocprofv3 --pmc runs,
-    which serialise and count each dispatch): the W8A8 pair, the fp16 GEMMs,
-    the three attentions and the MoE experts."""
+    which serialise and count each dispatch): the W8A8 pair (per-token and
+    group-32 activations), the fp16 GEMMs, the three attentions and the MoE
+    experts."""
     layers = setup_w8a8()
+    lib = rk.lib()
     for L in layers:
         for _ in range(launches):
             gemm_w8a8(L)
+    # the same pair in the reference's group-32 activation form
+    for L in layers:
+        m, k = L["m"], L["k"]
+        q32, s32 = rk.DeviceBuffer(m * k), rk.DeviceBuffer(m * (k // 32) * 4)
+        call(lib.rk_quantize_rows_dev(L["dx"].ptr, m, k, 32, q32.ptr, s32.ptr, None), "quantize g32")
+        for _ in range(launches):
+            call(lib.rk_matmul_w8a8_dev(int(L["wid"]), q32.ptr, s32.ptr, 32, m, k, L["dc"].ptr, None), "w8a8 g32")
     rk.synchronize()
-    lib = rk.lib()
     for (m, k, n) in ((512, 1024, 3072), (2394, 1152, 3456), (2394, 1152, 1152), (2394, 1152, 4304),
                       (2394, 4304, 1152)):
         a = synth.normal_f16(11, (m, k))
