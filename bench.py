@@ -291,6 +291,32 @@ def time_attention(s, h, kv, d, causal, seeds, iters):
             "tflops": fl / ms / 1e9, "frac_fp16_peak": fl / ms / 1e9 / PEAK_FP16}
 
 
+def band_pairs(s, window):
+    """Visible (query, key) pairs of the bidirectional band |t - j| <= window over s tokens."""
+    i = np.arange(s, dtype=np.int64)
+    return int((np.minimum(s - 1, i + window) - np.maximum(0, i - window) + 1).sum())
+
+
+def extra_gemma_attention(iters):
+    c = synth.GEMMA_TEXT
+    s, h, kv, d, w = c["s"], c["n_head"], c["n_kv"], c["d"], c["window"]
+    seeds = synth.SEEDS["gemma"]
+    q = synth.normal_f16(seeds[0], (s, h * d))
+    k = synth.normal_f16(seeds[1], (s, kv * d))
+    v = synth.normal_f16(seeds[2], (s, kv * d))
+    dq, dk, dv = dev(q.view(np.uint16)), dev(k.view(np.uint16)), dev(v.view(np.uint16))
+    do = rk.DeviceBuffer(s * h * d * 2)
+    lib = rk.lib()
+    out = {}
+    for name, mode, window, pairs in (("full", 0, -1, s * s), ("sliding_512", 2, w, band_pairs(s, w))):
+        ms = time_launches(lambda: call(lib.rk_attention_dev(dq.ptr, dk.ptr, dv.ptr, s, s, h, kv, d, d ** -0.5, 0.0,
+                                                             mode, window, 0, 0, do.ptr, None), "attn"), iters)
+        fl = 4.0 * d * h * pairs  # QKᵀ and PV over the visible pairs
+        out[name] = {"shape": f"S={s} H={h} KV={kv} D={d} mode={mode} window={window}", "ms": ms,
+                     "tflops": fl / ms / 1e9, "frac_fp16_peak": fl / ms / 1e9 / PEAK_FP16}
+    return out
+
+
 def extra_vision(iters):
     c = synth.VISION
     s, hid, h, d, mlp = c["s"], c["hidden"], c["n_head"], c["d"], c["mlp"]
@@ -685,6 +711,7 @@ def main():
                             synth.GQA_CAUSAL["s"], synth.GQA_CAUSAL["n_head"], synth.GQA_CAUSAL["n_kv"],
                             synth.GQA_CAUSAL["d"], True, synth.SEEDS["gqa"], 50)),
                         ("vision_layer_2394", lambda: extra_vision(50)),
+                        ("gemma_attention_d256_2587", lambda: extra_gemma_attention(50)),
                         ("moe_30b_a3b_1024", lambda: extra_moe(20)),
                         ("glue_qwen3_3633", lambda: extra_glue(50))):
             log(f"extra {key}")

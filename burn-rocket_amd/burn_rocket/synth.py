@@ -89,6 +89,9 @@ W8A8 = dict(m=3633, hidden=1024, inter=3072)
 GQA_CAUSAL = dict(s=3633, n_head=16, n_kv=8, d=128)
 VISION = dict(s=2394, hidden=1152, n_head=16, d=72, mlp=4304)
 MOE = dict(s=1024, hidden=2048, experts=128, top_k=8, inter=768, attn_heads=32, attn_kv=4, attn_d=128)
+# EmbeddingGemma text attention: 3 query heads on one kv head of width 256, full
+# layers and 512-key sliding layers, over a 2587-token document.
+GEMMA_TEXT = dict(s=2587, n_head=3, n_kv=1, d=256, window=512)
 
 SEEDS = {
     "gemm_f16": (101, 102),
@@ -96,4 +99,5 @@ SEEDS = {
     "gqa": (301, 302, 303),
     "vision": (401, 402, 403, 404, 405, 406, 407, 408, 409),
     "moe": (501, 502, 503, 504, 505, 506, 507, 508, 509),
+    "gemma": (601, 602, 603),
 }

@@ -19,7 +19,10 @@
 // last one down, so under a causal mask the longest tiles start first and the
 // short ones fill in behind them. Unmasked calls with head dims up to 80 may
 // instead use 192-row tiles on two groups of 6 waves (3 per SIMD) when that
-// takes fewer rounds of one workgroup per CU (launch_attn below).
+// takes fewer rounds of one workgroup per CU (launch_attn below). Head dim
+// 256 walks 32-key tiles and splits Oᵀ into two 128-row chunks, one per
+// workgroup (both form the same QKᵀ and P), so that the four K/Vᵀ buffers fit
+// in LDS and the Oᵀ accumulators in registers.
 //
 // Per wave and 64-key tile (v_mfma_f32_16x16x32_f16 throughout):
 //   Sᵀ = K·Qᵀ   A = K rows from LDS, B = Q fragments held in VGPRs; a lane
@@ -126,8 +129,9 @@ struct TileKeys {
   int kt_begin, kt_end, full_lo, full_hi;
   bool degenerate;
 };
+template <int TK>
 __device__ __forceinline__ TileKeys tile_keys(const AttnArgs &a, int qt, int BQ) {
-  const int n_kt = (a.n_kv + BK - 1) / BK;
+  const int n_kt = (a.n_kv + TK - 1) / TK;
   const int q_lo = qt * BQ, q_hi = min(qt * BQ + BQ, a.n_q) - 1;
   const int64_t t_min = a.q0 + q_lo, t_max = a.q0 + q_hi;
   const int64_t kabs0 = a.k0, kabs1 = a.k0 + a.n_kv - 1;
@@ -145,37 +149,48 @@ __device__ __forceinline__ TileKeys tile_keys(const AttnArgs &a, int qt, int BQ)
   if (!t.degenerate) {
     const int64_t any_lo = max(lo_a, kabs0) - a.k0;  // relative key indices
     const int64_t any_hi = min(hi_b, kabs1) - a.k0;
-    t.kt_begin = (int)(max(any_lo, (int64_t)0) / BK);
-    t.kt_end = (int)min((any_hi / BK) + 1, (int64_t)n_kt);
+    t.kt_begin = (int)(max(any_lo, (int64_t)0) / TK);
+    t.kt_end = (int)min((any_hi / TK) + 1, (int64_t)n_kt);
   }
   return t;
 }
 
-template <int D>
+// TK keys per tile (64; 32 for head dims above 128, to fit LDS). Head dims
+// above 128 split Oᵀ into 128-row chunks, one workgroup each: each chunk's
+// workgroup computes the whole Sᵀ and softmax and multiplies its own Vᵀ rows.
+template <int D, int TK = BK>
 struct AttnGeom {
   static constexpr int DQ = (D + 15) / 16 * 16;  // padded head dim
   static constexpr int NQC = DQ / 32;            // 32-wide d chunks of QKᵀ
   static constexpr bool TAIL16 = (DQ % 32) != 0;  // one 16-wide chunk (x16 MFMA)
   static constexpr int DV = DQ;
-  static constexpr int NDB = DV / 16;            // 16-row d blocks of Oᵀ
-  static constexpr int KPC = DQ <= 64 ? 8 : 16;  // 16-byte chunks per K row in LDS
+  static constexpr int DVC = DV <= 128 ? DV : 128;  // Oᵀ rows per workgroup
+  static constexpr int NCH = DV / DVC;              // workgroups per query tile
+  static constexpr int NDB = DVC / 16;           // 16-row d blocks of Oᵀ
+  static constexpr int KPC = DQ <= 64 ? 8 : (DQ <= 128 ? 16 : DQ / 8);  // 16-byte chunks per K row
+  static constexpr int KSW = (KPC < 16 ? KPC : 16) - 1;  // K chunk swizzle mask
   static constexpr int KROW = 16 * KPC;          // bytes per K row in LDS
-  static constexpr int K_BYTES = BK * KROW;
-  static constexpr int V_BYTES = DV * 128;
+  static constexpr int NKB = TK / 16;            // 16-key blocks per tile
+  static constexpr int NC2 = TK / 32;            // 32-key chunks per tile
+  static constexpr int VRB = TK * 2;             // bytes per Vᵀ row in LDS
+  static constexpr int K_BYTES = TK * KROW;
+  static constexpr int V_BYTES = DVC * VRB;
   static constexpr int BUF_BYTES = K_BYTES + V_BYTES;
-  static constexpr int K_INS = BK * KPC / 64;    // 1 KB copies per K tile
-  static constexpr int V_INS = DV / 8;            // 8 rows per copy
-  static constexpr int SMEM = 4 * BUF_BYTES;          // 2 groups × 2 buffers
+  static constexpr int K_INS = TK * KPC / 64;    // 1 KB copies per K tile
+  static constexpr int V_INS = V_BYTES / 1024;   // 1 KB copies per Vᵀ tile
+  static constexpr int SMEM = 4 * BUF_BYTES;     // 2 groups × 2 buffers
+  static_assert(DV % DVC == 0 && (TK == 64 || TK == 32), "tile geometry");
 };
 
 }  // namespace
 
-template <int D, bool SOFTCAP, int NWG>
+template <int D, bool SOFTCAP, int NWG, int TK = BK>
 __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel(AttnArgs a, int G,
                                                                                 int BQ,
                                                                                 int n_qtiles) {
-  using Gm = AttnGeom<D>;
+  using Gm = AttnGeom<D, TK>;
   constexpr int DQ = Gm::DQ, NQC = Gm::NQC, NDB = Gm::NDB, DV = Gm::DV;
+  constexpr int DVC = Gm::DVC, NCH = Gm::NCH, NKB = Gm::NKB, NC2 = Gm::NC2, VRB = Gm::VRB;
   constexpr bool TAIL16 = Gm::TAIL16;
   constexpr int KROW = Gm::KROW, KPC = Gm::KPC;
   constexpr int K_BYTES = Gm::K_BYTES, BUF_BYTES = Gm::BUF_BYTES;
@@ -186,7 +201,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   // the VALU slot keeps no sums. The rows D..DV-1 are written once and never
   // copied.
   constexpr bool LROW = D < DV;
-  static_assert(!LROW || D % 8 == 0, "Vᵀ copies move 8-row groups");
+  static_assert(!LROW || (D % 8 == 0 && TK == 64 && NCH == 1), "Vᵀ copies move 8-row groups");
   constexpr int V_INS = LROW ? D / 8 : Gm::V_INS;
   constexpr int CPW = (K_INS + V_INS + NWG - 1) / NWG;  // copies per wave of a group
   // Reads ahead: fewer with 3 waves per SIMD, whose register budget is 168.
@@ -199,16 +214,18 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = (int)((unsigned)wave / NWG), wq = (int)((unsigned)wave % NWG);
   const int KV = a.n_kv_heads;
-  const int kvh = blockIdx.x % KV;
-  const int qt = n_qtiles - 1 - (int)(blockIdx.x / KV);  // longest causal tiles first
+  const int dch = (int)(blockIdx.x % NCH);  // Oᵀ row chunk
+  const int wgq = (int)(blockIdx.x / NCH);
+  const int kvh = wgq % KV;
+  const int qt = n_qtiles - 1 - wgq / KV;  // longest causal tiles first
   const int l16 = lane & 15, lg = lane >> 4;
 
   // ---- copy geometry (per wave of a group, constant over tiles)
   const f16 *kbase = (const f16 *)a.k + (int64_t)kvh * a.k_head_stride;
   const rsrc_t rk =
       make_rsrc(kbase, ((int64_t)(a.n_kv - 1) * a.k_tok_stride + D) * 2);
-  const f16 *vtbase = (const f16 *)a.vt + (int64_t)kvh * DV * a.n_kv_pad;
-  const rsrc_t rv = make_rsrc(vtbase, (int64_t)DV * a.n_kv_pad * 2);
+  const f16 *vtbase = (const f16 *)a.vt + ((int64_t)kvh * DV + (int64_t)dch * DVC) * a.n_kv_pad;
+  const rsrc_t rv = make_rsrc(vtbase, (int64_t)DVC * a.n_kv_pad * 2);
   const uint32_t kstride_b = (uint32_t)(a.k_tok_stride * 2);  // bytes between keys
   const uint32_t vrow_b = (uint32_t)(a.n_kv_pad * 2);         // bytes between Vᵀ rows
   // Per-lane byte offset of copy c (recomputed at issue time: a few integer
@@ -216,12 +233,18 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   auto copy_voff = [&](int c) -> uint32_t {
     if (c < K_INS) {
       const int p = 64 * c + lane, row = p / KPC;
-      const int ch = (p % KPC) ^ (row & (KPC - 1));  // logical chunk of this slot
+      const int ch = (p % KPC) ^ (row & Gm::KSW);  // logical chunk of this slot
       return (ch < D / 8) ? (uint32_t)row * kstride_b + (uint32_t)(ch * 16) : OOB_OFFSET;
     }
-    const int d = 8 * (c - K_INS) + (lane >> 3);
-    const int lch = (lane & 7) ^ (d & 7);
-    return (uint32_t)d * vrow_b + (uint32_t)(lch * 16);
+    if constexpr (TK == 64) {  // 8 Vᵀ rows of 8 chunks, chunk c of row d at c ^ (d & 7)
+      const int d = 8 * (c - K_INS) + (lane >> 3);
+      const int lch = (lane & 7) ^ (d & 7);
+      return (uint32_t)d * vrow_b + (uint32_t)(lch * 16);
+    } else {  // 16 Vᵀ rows of 4 chunks, chunk c of row d at c ^ ((d >> 2) & 3)
+      const int d = 16 * (c - K_INS) + (lane >> 2);
+      const int lch = (lane & 3) ^ ((d >> 2) & 3);
+      return (uint32_t)d * vrow_b + (uint32_t)(lch * 16);
+    }
   };
   // Copies of the K part of key tile tk into buffer bk and of the Vᵀ part of
   // key tile tv into buffer bv of this wave's group (a tile < 0: no copy).
@@ -232,29 +255,29 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       if (c < K_INS) {
         if (tk >= 0)
           bdma16(rk, smem + (grp * 2 + bk) * BUF_BYTES + c * 1024, copy_voff(c),
-                 (uint32_t)tk * (BK * kstride_b));
+                 (uint32_t)tk * (TK * kstride_b));
       } else if (c < K_INS + V_INS) {
         if (tv >= 0)
           bdma16(rv, smem + (grp * 2 + bv) * BUF_BYTES + K_BYTES + (c - K_INS) * 1024, copy_voff(c),
-                 (uint32_t)(tv * BK * 2));
+                 (uint32_t)(tv * TK * 2));
       }
     }
   };
 
   // ---- LDS fragment addresses (within a buffer)
-  const int kf = l16 & (KPC - 1);
+  const int kf = l16 & Gm::KSW;
   uint32_t k_off[NQC > 0 ? NQC : 1];  // per 32-wide d chunk c; + kb·16·KROW
 #pragma unroll
   for (int c = 0; c < NQC; ++c) k_off[c] = (uint32_t)(l16 * KROW + (((4 * c + lg) ^ kf) << 4));
   const uint32_t k_off16 =
       (uint32_t)(l16 * KROW + (((4 * NQC + (lg >> 1)) ^ kf) << 4) + (lg & 1) * 8);
-  const int vf = l16 & 7;
-  uint32_t v_off[2];  // per 32-key chunk c2; + db·16·128
+  uint32_t v_off[NC2];  // per 32-key chunk c2; + db·16·VRB
 #pragma unroll
-  for (int c2 = 0; c2 < 2; ++c2) v_off[c2] = (uint32_t)(K_BYTES + l16 * 128 + (((4 * c2 + lg) ^ vf) << 4));
+  for (int c2 = 0; c2 < NC2; ++c2)
+    v_off[c2] = TK == 64 ? (uint32_t)(K_BYTES + l16 * 128 + (((4 * c2 + lg) ^ (l16 & 7)) << 4))
+                         : (uint32_t)(K_BYTES + l16 * 64 + ((lg ^ ((l16 >> 2) & 3)) << 4));
 
   const float C = SOFTCAP ? LOG2E : a.scale * LOG2E;
-  const int n_kt = (a.n_kv + BK - 1) / BK;
   {
 
     // ---- this lane's query rows (two 16-query blocks)
@@ -272,7 +295,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     }
 
     // ---- key range of the tile, degenerate rows
-    const TileKeys tkeys = tile_keys(a, qt, BQ);
+    const TileKeys tkeys = tile_keys<TK>(a, qt, BQ);
     const bool degenerate = tkeys.degenerate;
     const int full_lo = tkeys.full_lo, full_hi = tkeys.full_hi;
     const int kt_begin = tkeys.kt_begin, kt_end = tkeys.kt_end;
@@ -326,8 +349,8 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     const int n_tiles = kt_end - kt_begin;
     const int nj = (n_tiles - grp + 1) / 2;
     const int nj_max = (n_tiles + 1) / 2;
-    floatx4 sacc[4][2];
-    half8 phi[2][2], plo[2][2];
+    floatx4 sacc[NKB][2];
+    half8 phi[2][NC2], plo[2][NC2];
     // MFMA slot j: PV of tile j-1, Sᵀ of tile j.
     auto mfma_slot = [&](int j) {
     if (j < nj) issue(j + 1 < nj ? kt_begin + 2 * (j + 1) + grp : -1, (j + 1) & 1, kt_begin + 2 * j + grp, j & 1);
@@ -336,14 +359,14 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       // the lo products of the previous fragment, so that the two MFMAs into
       // one accumulator are four MFMAs apart.
       const uint8_t *vb = smem + (grp * 2 + ((j - 1) & 1)) * BUF_BYTES;
-      constexpr int NF = 2 * NDB;  // fragments: f = c2·NDB + db
+      constexpr int NF = NC2 * NDB;  // fragments: f = c2·NDB + db
       half8 vprev = half8{};
       static_for<NF + 1>([&](auto f_c) {
         constexpr int F = decltype(f_c)::value;
         half8 vcur = half8{};
         if constexpr (F < NF) {
           constexpr int C2 = F / NDB, DB = F % NDB;
-          vcur = *(const half8 *)(vb + v_off[C2] + DB * 16 * 128);
+          vcur = *(const half8 *)(vb + v_off[C2] + DB * 16 * VRB);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
             o[DB][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vcur, phi[qb][C2], o[DB][qb], 0, 0, 0);
@@ -371,13 +394,13 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       // Sᵀ for the four 16-key blocks and two 16-query blocks of tile j.
       const uint8_t *kbuf = smem + (grp * 2 + (j & 1)) * BUF_BYTES;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) sacc[kb][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < NQC; ++c) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb) {
           const half8 kfr = *(const half8 *)(kbuf + k_off[c] + kb * 16 * KROW);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
@@ -386,7 +409,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       }
       if constexpr (TAIL16) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb) {
           const half4 kfr = *(const half4 *)(kbuf + k_off16 + kb * 16 * KROW);
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
@@ -394,7 +417,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
         }
       }
       // Each fragment read LAW reads ahead of its two MFMAs.
-      constexpr int NR = 4 * (NQC + (TAIL16 ? 1 : 0));
+      constexpr int NR = NKB * (NQC + (TAIL16 ? 1 : 0));
       __builtin_amdgcn_sched_group_barrier(0x100, LAW, 0);
       static_for<NR - LAW>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
@@ -412,20 +435,20 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     // (values up to 2^RESCALE, exact after the final normalisation).
     auto valu_slot = [&](int j) {
       if (j >= nj) return;
-      const int kb0 = (kt_begin + 2 * j + grp) * BK;
+      const int kb0 = (kt_begin + 2 * j + grp) * TK;
       if constexpr (SOFTCAP) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               sacc[kb][qb][e] = a.softcap * tanhf(sacc[kb][qb][e] * a.scale / a.softcap);
       }
-      if (!((kb0 >= full_lo) && (kb0 + BK - 1 <= full_hi) && !degenerate)) {
+      if (!((kb0 >= full_lo) && (kb0 + TK - 1 <= full_hi) && !degenerate)) {
         const float masked_raw = masked_x / C;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -441,7 +464,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       for (int qb = 0; qb < 2; ++qb) {
         float m = sacc[0][qb][0];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             if (kb | e) m = fmaxf(m, sacc[kb][qb][e]);
@@ -468,7 +491,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
         const float nm = (m_run[qb] == -INFINITY) ? 0.f : -m_run[qb];
         float lsum = 0.f;
 #pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
+        for (int c2 = 0; c2 < NC2; ++c2) {
           uintx4 hw, lw;
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
@@ -568,7 +591,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
           f16 *orow = (f16 *)a.out + (int64_t)qi[qb] * a.o_tok_stride + (int64_t)hq[qb] * a.o_head_stride;
 #pragma unroll
           for (int db = 0; db < NDB; ++db) {
-            const int d0 = db * 16 + 4 * lg;
+            const int d0 = dch * DVC + db * 16 + 4 * lg;
             if (d0 < D) {
               half4 h;
 #pragma unroll
@@ -618,15 +641,15 @@ hipError_t rk_launch_v_transpose_strided(const void *v, int64_t tok_stride, int6
   return hipGetLastError();
 }
 
-template <int D, int NWG>
+template <int D, int NWG, int TK = BK>
 static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
   const int G = a.n_head / a.n_kv_heads;
   const int BQ = 32 * NWG / G;
   const int n_qtiles = (a.n_q + BQ - 1) / BQ;
-  const int grid = n_qtiles * a.n_kv_heads;
-  auto kern0 = attn_fa_kernel<D, false, NWG>;
-  auto kern1 = attn_fa_kernel<D, true, NWG>;
-  constexpr int smem = AttnGeom<D>::SMEM;
+  const int grid = n_qtiles * a.n_kv_heads * AttnGeom<D, TK>::NCH;
+  auto kern0 = attn_fa_kernel<D, false, NWG, TK>;
+  auto kern1 = attn_fa_kernel<D, true, NWG, TK>;
+  constexpr int smem = AttnGeom<D, TK>::SMEM;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern0,
@@ -654,6 +677,10 @@ static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
 // SIMD in registers.
 template <int D>
 static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
+  // Head dims above 128: 32-key tiles and 128-row Oᵀ chunks (LDS).
+  if constexpr (D > 128) {
+    return launch_attn_nwg<D, 4, 32>(a, st);
+  } else {
   if constexpr (D <= 80) {
     // RK_ATTN_ROWS = 128 or 192 forces the tile height (any mask).
     const int G = a.n_head / a.n_kv_heads;
@@ -668,6 +695,7 @@ static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
     if (six && G <= 192) return launch_attn_nwg<D, 6>(a, st);
   }
   return launch_attn_nwg<D, 4>(a, st);
+  }
 }
 
 hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st) {
@@ -686,6 +714,8 @@ hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st) {
       return launch_attn<112>(a, st);
     case 128:
       return launch_attn<128>(a, st);
+    case 256:
+      return launch_attn<256>(a, st);
   }
   return hipErrorInvalidValue;
 }

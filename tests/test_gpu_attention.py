@@ -87,7 +87,7 @@ def test_config5_gqa_32_4_full(rk, orc):
     check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(s, 64), mode=1)
 
 
-@pytest.mark.parametrize("d", [64, 72, 80, 96, 112, 128])
+@pytest.mark.parametrize("d", [64, 72, 80, 96, 112, 128, 256])
 @pytest.mark.parametrize("h,kv", [(4, 4), (8, 2), (16, 2), (6, 3)])
 def test_head_dims_and_groups(rk, orc, d, h, kv):
     note(f"attention d={d} h={h} kv={kv}")
@@ -141,6 +141,29 @@ def test_mask_modes_and_block_offsets(rk, orc, mode, window, n_q, n_kv, q0, k0):
     got = attn_dev(rk, q, k, v, h, kv, d, 0.0884, mode=mode, window=window, q0=q0, k0=k0)
     ref = orc.attention_ref(q, k, v, h, kv, d, 0.0884, 0.0, mode, window, q0, k0)
     check(orc, got, ref)
+
+
+@pytest.mark.parametrize("mode,window,softcap,q0,k0,n_q,n_kv", [
+    (2, 512, 0.0, 0, 0, 1200, 1200),       # sliding layer, one chunk
+    (0, -1, 0.0, 0, 0, 700, 700),          # full layer
+    (2, 512, 0.0, 1024, 512, 176, 688),    # sliding layer, a later query chunk (keys from q0 - window)
+    (3, 100, 30.0, 0, 0, 333, 333),        # causal window with a softcap
+])
+def test_head_dim_256_gemma_layers(rk, orc, mode, window, softcap, q0, k0, n_q, n_kv):
+    """EmbeddingGemma's attention: 3 query heads on 1 kv head of 256 values
+    (src/gemma/embeddinggemma/model.rs:165-230 calls attention_window and
+    attention_window_block with its sliding window). Head dims above 128 run
+    32-key tiles and two 128-row Oᵀ chunks per query tile."""
+    note(f"d=256 gemma mode={mode} window={window} softcap={softcap} q0={q0} k0={k0} n_q={n_q} n_kv={n_kv}")
+    r = np.random.default_rng(n_q + n_kv + mode)
+    h, kv, d = 3, 1, 256
+    q = r.standard_normal((n_q, h * d)).astype(np.float16)
+    k = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    v = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    got = attn_dev(rk, q, k, v, h, kv, d, 1.0 / 16, softcap=softcap, mode=mode, window=window, q0=q0, k0=k0)
+    rows = _slices(n_q, 48)
+    check_rows(orc, got, q, k, v, h, kv, d, 1.0 / 16, rows, softcap=softcap, mode=mode, window=window,
+               q0=q0, k0=k0)
 
 
 def test_softcap(rk, orc):
