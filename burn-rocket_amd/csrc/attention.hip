@@ -22,7 +22,9 @@
 // takes fewer rounds of one workgroup per CU (launch_attn below). Head dim
 // 256 walks 32-key tiles and splits Oᵀ into two 128-row chunks, one per
 // workgroup (both form the same QKᵀ and P), so that the four K/Vᵀ buffers fit
-// in LDS and the Oᵀ accumulators in registers.
+// in LDS and the Oᵀ accumulators in registers. A launch with at most half as
+// many query tiles as CUs splits each tile's key tiles between two workgroups
+// whose softmax states meet in a workspace (KSPLIT, at the end of the kernel).
 //
 // Per wave and 64-key tile (v_mfma_f32_16x16x32_f16 throughout):
 //   Sᵀ = K·Qᵀ   A = K rows from LDS, B = Q fragments held in VGPRs; a lane
@@ -184,7 +186,7 @@ struct AttnGeom {
 
 }  // namespace
 
-template <int D, bool SOFTCAP, int NWG, int TK = BK>
+template <int D, bool SOFTCAP, int NWG, int TK = BK, bool KSPLIT = false>
 __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel(AttnArgs a, int G,
                                                                                 int BQ,
                                                                                 int n_qtiles) {
@@ -214,8 +216,12 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = (int)((unsigned)wave / NWG), wq = (int)((unsigned)wave % NWG);
   const int KV = a.n_kv_heads;
-  const int dch = (int)(blockIdx.x % NCH);  // Oᵀ row chunk
-  const int wgq = (int)(blockIdx.x / NCH);
+  // KSPLIT: workgroups 2t and 2t+1 take the first and the second half of the
+  // key tiles of query tile t.
+  const int ks = KSPLIT ? (int)(blockIdx.x & 1) : 0;
+  const int bid = KSPLIT ? (int)(blockIdx.x >> 1) : (int)blockIdx.x;
+  const int dch = bid % NCH;  // Oᵀ row chunk
+  const int wgq = bid / NCH;
   const int kvh = wgq % KV;
   const int qt = n_qtiles - 1 - wgq / KV;  // longest causal tiles first
   const int l16 = lane & 15, lg = lane >> 4;
@@ -298,7 +304,14 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     const TileKeys tkeys = tile_keys<TK>(a, qt, BQ);
     const bool degenerate = tkeys.degenerate;
     const int full_lo = tkeys.full_lo, full_hi = tkeys.full_hi;
-    const int kt_begin = tkeys.kt_begin, kt_end = tkeys.kt_end;
+    int kt_begin = tkeys.kt_begin, kt_end = tkeys.kt_end;
+    if constexpr (KSPLIT) {
+      const int kt_mid = kt_begin + (kt_end - kt_begin + 1) / 2;
+      if (ks == 0)
+        kt_end = kt_mid;
+      else
+        kt_begin = kt_mid;
+    }
     const float masked_x = degenerate ? MASKED_SCORE * LOG2E : -INFINITY;
     // Visible keys of each of this lane's queries as a relative key interval
     // [klo, khi] (every mask mode is an interval), clipped to [0, n_kv).
@@ -576,6 +589,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
           for (int e = 0; e < 4; ++e) p[(4 + (db * 2 + qb) * 4 + e) * 64] = o[db][qb][e];
     }
     BARRIER();
+    float m_all[2] = {0.f, 0.f}, l_all[2] = {0.f, 0.f};  // KSPLIT: the merged state of this key half
     if (grp == 0) {
       const float *p = xch + lane;
 #pragma unroll
@@ -586,6 +600,16 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
         const float a0 = __builtin_amdgcn_exp2f(m_run[qb] - mu);
         const float a1 = __builtin_amdgcn_exp2f(m1 - mu);
         const float l = lt[qb] * a0 + l1 * a1;
+        if constexpr (KSPLIT) {
+          m_all[qb] = m;
+          l_all[qb] = l;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              o[db][qb][e] = o[db][qb][e] * a0 + p[(4 + (db * 2 + qb) * 4 + e) * 64] * a1;
+          continue;
+        }
         const float inv = l > 0.f ? 1.0f / l : 0.f;
         if (rok[qb]) {
           f16 *orow = (f16 *)a.out + (int64_t)qi[qb] * a.o_tok_stride + (int64_t)hq[qb] * a.o_head_stride;
@@ -598,6 +622,76 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
               for (int e = 0; e < 4; ++e) {
                 const float o1 = p[(4 + (db * 2 + qb) * 4 + e) * 64];
                 h[e] = (f16)((o[db][qb][e] * a0 + o1 * a1) * inv);
+              }
+              *(half4 *)(orow + d0) = h;
+            }
+          }
+        }
+      }
+    }
+    if constexpr (KSPLIT) {
+      // Each half writes its state (m, l, unnormalised Oᵀ) to its slot, and
+      // the second half to arrive merges the two, in split order whichever it
+      // is, and stores O. Nothing waits on the other workgroup. The slots are
+      // written and read with 16-byte device-coherent (sc1) accesses, so no
+      // L2-wide write-back or invalidate is needed (those cost more than the
+      // split gained). Slot of a half: [wave wq][j][lane] 16-byte entries,
+      // j = 0 the (m, l) pairs of the two query blocks, j = 1 + 2·db + qb the
+      // Oᵀ block (db, qb).
+      constexpr int NJ = 1 + 2 * NDB;
+      constexpr int SLOT_BYTES = NWG * NJ * 64 * 16;
+      constexpr int SC1 = 16;  // cache policy bit: device scope
+      const rsrc_t rp = make_rsrc(a.part + (size_t)bid * 2 * (SLOT_BYTES / 4), 2 * SLOT_BYTES);
+      const uint32_t lane_off = (uint32_t)((wq * NJ * 64 + lane) * 16);
+      const uint32_t mine = lane_off + (uint32_t)(ks * SLOT_BYTES);
+      const uint32_t other = lane_off + (uint32_t)((ks ^ 1) * SLOT_BYTES);
+      if (grp == 0) {
+        const floatx4 ml = {m_all[0], l_all[0], m_all[1], l_all[1]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, ml), rp, mine, 0, SC1);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, o[db][qb]), rp,
+                                                   mine + (uint32_t)((1 + 2 * db + qb) * 1024), 0, SC1);
+        WAIT_VMCNT(0);  // the state is stored before the arrival count
+      }
+      BARRIER();  // every read of the exchange area is done: its first word is free
+      unsigned *flag = (unsigned *)smem;
+      if (threadIdx.x == 0) {
+        const unsigned prev = atomicAdd(a.cnt + bid, 1u);
+        if (prev != 0) atomicExch(a.cnt + bid, 0u);  // both halves are in: reset for the next launch
+        *flag = prev;
+        WAIT_LGKMCNT0();
+      }
+      BARRIER();
+      if (*flag == 0 || grp != 0) return;
+      const floatx4 mlo = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, other, 0, SC1));
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float mo = mlo[2 * qb], lo = mlo[2 * qb + 1];
+        const float m0 = ks == 0 ? m_all[qb] : mo, m1 = ks == 0 ? mo : m_all[qb];
+        const float l0 = ks == 0 ? l_all[qb] : lo, l1 = ks == 0 ? lo : l_all[qb];
+        const float m = fmaxf(m0, m1);
+        const float mu = (m == -INFINITY) ? 0.f : m;
+        const float a0 = __builtin_amdgcn_exp2f(m0 - mu);
+        const float a1 = __builtin_amdgcn_exp2f(m1 - mu);
+        const float l = l0 * a0 + l1 * a1;
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        if (rok[qb]) {
+          f16 *orow = (f16 *)a.out + (int64_t)qi[qb] * a.o_tok_stride + (int64_t)hq[qb] * a.o_head_stride;
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const int d0 = dch * DVC + db * 16 + 4 * lg;
+            if (d0 < D) {
+              const floatx4 oo = __builtin_bit_cast(
+                  floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                               rp, other + (uint32_t)((1 + 2 * db + qb) * 1024), 0, SC1));
+              half4 h;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float o0 = ks == 0 ? o[db][qb][e] : oo[e], o1 = ks == 0 ? oo[e] : o[db][qb][e];
+                h[e] = (f16)((o0 * a0 + o1 * a1) * inv);
               }
               *(half4 *)(orow + d0) = h;
             }
@@ -641,14 +735,14 @@ hipError_t rk_launch_v_transpose_strided(const void *v, int64_t tok_stride, int6
   return hipGetLastError();
 }
 
-template <int D, int NWG, int TK = BK>
+template <int D, int NWG, int TK = BK, bool KSPLIT = false>
 static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
   const int G = a.n_head / a.n_kv_heads;
   const int BQ = 32 * NWG / G;
   const int n_qtiles = (a.n_q + BQ - 1) / BQ;
-  const int grid = n_qtiles * a.n_kv_heads * AttnGeom<D, TK>::NCH;
-  auto kern0 = attn_fa_kernel<D, false, NWG, TK>;
-  auto kern1 = attn_fa_kernel<D, true, NWG, TK>;
+  const int grid = n_qtiles * a.n_kv_heads * AttnGeom<D, TK>::NCH * (KSPLIT ? 2 : 1);
+  auto kern0 = attn_fa_kernel<D, false, NWG, TK, KSPLIT>;
+  auto kern1 = attn_fa_kernel<D, true, NWG, TK, KSPLIT>;
   constexpr int smem = AttnGeom<D, TK>::SMEM;
   static bool attr_set = false;
   if (!attr_set) {
@@ -675,12 +769,19 @@ static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
 // queries in fewer rounds (vision S=2394, 16 heads: 304 tiles of 128 rows =
 // 2 rounds, 208 tiles of 192 rows = 1). Head dims up to 80 fit 3 waves per
 // SIMD in registers.
+//
+// A grid that fills at most half of the CUs (few query heads, short
+// sequences) leaves the rest idle for the whole launch: given the workspace,
+// such a launch splits each query tile's key tiles between two workgroups.
 template <int D>
 static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
+  const bool split = a.part != nullptr && a.cnt != nullptr && rk_attn_split_tiles(a) > 0;
   // Head dims above 128: 32-key tiles and 128-row Oᵀ chunks (LDS).
   if constexpr (D > 128) {
+    if (split) return launch_attn_nwg<D, 4, 32, true>(a, st);
     return launch_attn_nwg<D, 4, 32>(a, st);
   } else {
+  if (split) return launch_attn_nwg<D, 4, BK, true>(a, st);
   if constexpr (D <= 80) {
     // RK_ATTN_ROWS = 128 or 192 forces the tile height (any mask).
     const int G = a.n_head / a.n_kv_heads;
@@ -696,6 +797,27 @@ static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
   }
   return launch_attn_nwg<D, 4>(a, st);
   }
+}
+
+long rk_attn_split_floats(int head_dim) {
+  const int dv = rk_attn_dv_pad(head_dim);
+  const int ndb = (dv <= 128 ? dv : 128) / 16;
+  return 4L * 64 * (4 + 8 * ndb);  // four waves of 64 lanes (the exchange layout)
+}
+
+// RK_ATTN_SPLIT: 0 (default) splits grids of at most half the CUs, 1 never
+// splits, 2 splits every launch that has the workspace.
+long rk_attn_split_tiles(const AttnArgs &a) {
+  const int knob = rk_knob("RK_ATTN_SPLIT", 0);
+  if (knob == 1 || a.n_kv_heads <= 0 || a.n_head % a.n_kv_heads) return 0;
+  const int G = a.n_head / a.n_kv_heads;
+  if (G < 1 || G > ROWS) return 0;
+  const int dv = rk_attn_dv_pad(a.head_dim);
+  const long nch = dv <= 128 ? 1 : dv / 128;
+  const int BQ = ROWS / G;
+  const long tiles = (long)((a.n_q + BQ - 1) / BQ) * a.n_kv_heads * nch;
+  const long cus = a.num_cus > 0 ? a.num_cus : 256;
+  return (knob == 2 || 2 * tiles <= cus) ? tiles : 0;
 }
 
 hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st) {

@@ -161,7 +161,9 @@ int fence_point(DevBuf &b, const char *op) {
 }
 
 // Grow-only named device scratch, ordered after its last use on any stream.
-int scratch(CallScope &c, const char *name, size_t bytes, void **out) {
+// *fresh (when given) tells whether this call allocated it.
+int scratch(CallScope &c, const char *name, size_t bytes, void **out, bool *fresh = nullptr) {
+  if (fresh) *fresh = false;
   DevBuf &b = g_eng->scratch[name];
   if (!b.ev) HIP_TRY(hipEventCreateWithFlags(&b.ev, hipEventDisableTiming), "scratch");
   if (b.bytes < bytes) {
@@ -177,6 +179,7 @@ int scratch(CallScope &c, const char *name, size_t bytes, void **out) {
     const size_t want = std::max<size_t>(bytes, 256);
     HIP_TRY(hipMalloc(&b.p, want), "scratch");
     b.bytes = want;
+    if (fresh) *fresh = true;
   } else if ((b.recorded || b.pending) && b.ev_stream != c.st) {
     RK_TRY(fence_point(b, "scratch"));
     HIP_TRY(hipStreamWaitEvent(c.st, b.ev, 0), "scratch");
@@ -959,10 +962,12 @@ int attn_check(int64_t n_q, int64_t n_kv, int n_head, int n_kv_heads, int head_d
   return RK_OK;
 }
 
+// cs: the call's scope, which provides the key-split workspace; null (the
+// no-allocation entry) launches without a key split.
 int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_q, int64_t n_kv,
              int64_t n_kv_pad, int n_head, int n_kv_heads, int head_dim, float scale, float softcap,
              int mode, int64_t window, int64_t q0, int64_t k0, bool head_major, hipStream_t st,
-             const char *op, int64_t q_ts = 0, int64_t k_ts = 0, int64_t o_ts = 0) {
+             const char *op, CallScope *cs, int64_t q_ts = 0, int64_t k_ts = 0, int64_t o_ts = 0) {
   // K and Vᵀ of one kv head are addressed with 32-bit byte offsets.
   const int64_t k_tok = head_major ? head_dim : (k_ts ? k_ts : (int64_t)n_kv_heads * head_dim);
   if (((n_kv - 1) * k_tok + head_dim) * 2 >= ((int64_t)1 << 31) ||
@@ -1001,6 +1006,21 @@ int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_
   a.q0 = q0;
   a.k0 = k0;
   a.num_cus = g_eng->num_cus;
+  const long split = cs ? rk_attn_split_tiles(a) : 0;
+  if (split > 0) {
+    // Partial states (two per split tile) and arrival counters. The counters
+    // start at zero and every launch leaves them at zero.
+    // A new counter buffer is zeroed whole: a later launch with more query
+    // tiles uses counters past this one's.
+    void *part, *cnt;
+    bool fresh = false;
+    const size_t cnt_bytes = std::max<size_t>((size_t)split * 4, 256);
+    RK_TRY(scratch(*cs, "attn_part", (size_t)split * 2 * rk_attn_split_floats(head_dim) * 4, &part));
+    RK_TRY(scratch(*cs, "attn_cnt", cnt_bytes, &cnt, &fresh));
+    if (fresh) HIP_TRY(hipMemsetAsync(cnt, 0, cnt_bytes, st), op);
+    a.part = (float *)part;
+    a.cnt = (unsigned *)cnt;
+  }
   HIP_TRY(rk_launch_attention(a, st), op);
   return RK_OK;
 }
@@ -1024,7 +1044,7 @@ int attn_dev_impl(CallScope &cs, const void *q, const void *k, const void *v, in
           op);
   if (tm) tm->mark(1);
   return attn_run(q, k, vt, out, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale, softcap,
-                  mode, window, q0, k0, false, cs.st, op, q_ts, k_ts, o_ts);
+                  mode, window, q0, k0, false, cs.st, op, &cs, q_ts, k_ts, o_ts);
 }
 }  // namespace
 
@@ -1089,7 +1109,7 @@ extern "C" int rk_attention_dev_noalloc(const void *q, const void *k, const void
                                 (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, st),
           op);
   RK_TRY(attn_run(q, k, vt, out, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale, softcap,
-                  mode, window, q0, k0, false, st, op));
+                  mode, window, q0, k0, false, st, op, nullptr));
   g_eng->calls++;
   return RK_OK;
 }
@@ -1188,7 +1208,7 @@ extern "C" int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv
           op);
   tm.mark(1);
   RK_TRY(attn_run(q16, k16, vt, o16, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, D, scale, softcap,
-                  mode, window, q0, k0, true, st, op));
+                  mode, window, q0, k0, true, st, op, &cs));
   tm.mark(2);
   // out [H][n_q][dv]: the first dv columns of each output row.
   HIP_TRY(hipMemcpy2DAsync(out, (size_t)dv * 2, o16, (size_t)D * 2, (size_t)dv * 2,
@@ -1809,7 +1829,7 @@ extern "C" int rk_attention_qkv_dev(void *qkv, int64_t s, int64_t row_stride, in
                                  (int)n_kv_pad, dvp), name);
   RK_TRY(attn_run(qkv, (const uint16_t *)qkv + (int64_t)n_head * head_dim, vt, out, s, s, n_kv_pad,
                   n_head, n_kv_heads, head_dim, scale, softcap, mode, window, q0, k0, false, st,
-                  name, row_stride, row_stride, out_stride));
+                  name, &cs, row_stride, row_stride, out_stride));
   g_eng->calls++;
   return RK_OK;
 }

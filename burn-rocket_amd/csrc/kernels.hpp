@@ -154,6 +154,11 @@ struct AttnArgs {
   int mask_mode;
   int64_t window, q0, k0;
   int num_cus;
+  // Key-split workspace (both null: no split). part: per split query tile, two
+  // partial softmax states (rk_attn_split_floats values each); cnt: one
+  // arrival counter per split query tile, zero between launches.
+  float *part;
+  unsigned *cnt;
 };
 // V [n_kv, tok stride] (kv head g at column g·D) → Vt [KV][Dv_pad][n_kv_pad].
 hipError_t rk_launch_v_transpose(const void *v, int64_t v_tok_stride, int64_t v_head_stride,
@@ -162,6 +167,11 @@ hipError_t rk_launch_v_transpose(const void *v, int64_t v_tok_stride, int64_t v_
 int rk_attn_dv_pad(int head_dim);
 int rk_attn_kv_tile();
 hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st);
+// Query tiles whose keys a launch with this shape splits between two
+// workgroups when given the workspace (0: no split), and the floats of one
+// half's partial state.
+long rk_attn_split_tiles(const AttnArgs &a);
+long rk_attn_split_floats(int head_dim);
 
 // MoE helpers.
 struct MoeTile {

@@ -143,6 +143,35 @@ def test_mask_modes_and_block_offsets(rk, orc, mode, window, n_q, n_kv, q0, k0):
     check(orc, got, ref)
 
 
+@pytest.mark.parametrize("split", ["1", "2"])
+@pytest.mark.parametrize("d,h,kv,mode,window,softcap,n_q,n_kv,q0,k0", [
+    (128, 8, 2, 1, -1, 0.0, 300, 300, 0, 0),     # causal: halves of unequal length per tile
+    (64, 4, 4, 0, -1, 0.0, 200, 64, 0, 0),       # one key tile: the second half walks none
+    (72, 16, 16, 0, -1, 0.0, 150, 150, 0, 0),    # padded head dim (row sums from the ones row of Vᵀ)
+    (256, 3, 1, 2, 100, 0.0, 260, 260, 0, 0),    # two Oᵀ chunks per query tile, band
+    (128, 8, 2, 1, -1, 0.0, 40, 70, 10, 30),     # emptied rows sweep every key in both halves
+    (96, 6, 3, 3, 40, 15.0, 180, 180, 0, 0),     # causal window with a softcap
+    (112, 8, 8, 2, 5, 0.0, 30, 40, 100, 0),      # every row emptied
+])
+def test_key_split(rk, orc, monkeypatch, split, d, h, kv, mode, window, softcap, n_q, n_kv, q0, k0):
+    """RK_ATTN_SPLIT=2 splits every launch's key tiles between two workgroups
+    (the second to finish merges the two partial softmax states, in split
+    order); 1 never splits. Both against the oracle, and each bit-identical
+    from one call to the next."""
+    note(f"key split={split} d={d} h={h} kv={kv} mode={mode} w={window} cap={softcap} "
+         f"n_q={n_q} n_kv={n_kv} q0={q0} k0={k0}")
+    monkeypatch.setenv("RK_ATTN_SPLIT", split)
+    r = np.random.default_rng(d + h * 3 + n_q + n_kv)
+    q = r.standard_normal((n_q, h * d)).astype(np.float16)
+    k = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    v = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+    args = dict(softcap=softcap, mode=mode, window=window, q0=q0, k0=k0)
+    got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, **args)
+    again = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, **args)
+    assert (got == again).all()
+    check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, softcap, mode, window, q0, k0))
+
+
 @pytest.mark.parametrize("mode,window,softcap,q0,k0,n_q,n_kv", [
     (2, 512, 0.0, 0, 0, 1200, 1200),       # sliding layer, one chunk
     (0, -1, 0.0, 0, 0, 700, 700),          # full layer
@@ -244,7 +273,8 @@ def test_attention_rejects_bad_shapes(rk):
 
 
 def test_attention_is_deterministic(rk, orc):
-    # Same inputs, same bits: the kernel has no atomics or order-dependent sums.
+    # Same inputs, same bits: every sum has a fixed order (a split query tile's
+    # two halves are merged in split order, whichever finishes second).
     c = synth.MOE
     s, h, kv, d = c["s"], c["attn_heads"], c["attn_kv"], c["attn_d"]
     note(f"determinism S={s} H={h} KV={kv}")

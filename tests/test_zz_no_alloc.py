@@ -24,10 +24,14 @@ def _call(rk, name, bufs, s, h, kv, d, mode, out):
     return out.download((s, h * d), np.uint16).view(np.float16).astype(np.float32)
 
 
-def test_noalloc_attention_equals_rk_attention_dev(rk, orc):
+def test_noalloc_attention_equals_rk_attention_dev(rk, orc, monkeypatch):
     # Two calls in a row, the second smaller: the causal Qwen3 shape, then a
     # bidirectional 72-wide one. The static array keeps the first call's Vᵀ;
-    # the second call must not see any of it.
+    # the second call must not see any of it. The no-allocation entry never
+    # splits a query tile's keys between workgroups (that takes a workspace),
+    # so it equals rk_attention_dev bit for bit with the split off
+    # (RK_ATTN_SPLIT=1), and within the parity gate with the default, which
+    # splits the small second grid.
     rk.clear_scratch()
     for i, (s, h, kv, d, mode) in enumerate(((3633, 16, 8, 128, 1), (700, 8, 2, 72, 0))):
         note(f"noalloc attention S={s} H={h} KV={kv} D={d} mode={mode}")
@@ -40,8 +44,12 @@ def test_noalloc_attention_equals_rk_attention_dev(rk, orc):
         held = rk.mem_stats().scratch_bytes
         got = _call(rk, "rk_attention_dev_noalloc", bufs, s, h, kv, d, mode, out)
         assert rk.mem_stats().scratch_bytes == held  # no library scratch taken
+        monkeypatch.setenv("RK_ATTN_SPLIT", "1")
         want = _call(rk, "rk_attention_dev", bufs, s, h, kv, d, mode, rk.DeviceBuffer(s * h * d * 2))
         assert (got == want).all()  # the same kernels on the same operands
+        monkeypatch.delenv("RK_ATTN_SPLIT")
+        dflt = _call(rk, "rk_attention_dev", bufs, s, h, kv, d, mode, rk.DeviceBuffer(s * h * d * 2))
+        assert orc.cosine(got, dflt) >= COS_MIN and orc.max_rel(got, dflt) <= REL_MAX
         for a, b in ((0, 40), (s // 2, s // 2 + 40), (s - 40, s)):
             ref = orc.attention_ref(q[a:b], k, v, h, kv, d, d ** -0.5, 0.0, mode, -1, a, 0)
             assert orc.cosine(got[a:b], ref) >= COS_MIN and orc.max_rel(got[a:b], ref) <= REL_MAX
