@@ -666,7 +666,16 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       }
       BARRIER();
       if (*flag == 0 || grp != 0) return;
+      // Every load of the other state is issued before the first use (the
+      // loads go to memory; one at a time they cost a latency each).
       const floatx4 mlo = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, other, 0, SC1));
+      floatx4 ot[NDB][2];
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          ot[db][qb] = __builtin_bit_cast(
+              floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, other + (uint32_t)((1 + 2 * db + qb) * 1024), 0, SC1));
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const float mo = mlo[2 * qb], lo = mlo[2 * qb + 1];
@@ -684,9 +693,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
           for (int db = 0; db < NDB; ++db) {
             const int d0 = dch * DVC + db * 16 + 4 * lg;
             if (d0 < D) {
-              const floatx4 oo = __builtin_bit_cast(
-                  floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                               rp, other + (uint32_t)((1 + 2 * db + qb) * 1024), 0, SC1));
+              const floatx4 oo = ot[db][qb];
               half4 h;
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
