@@ -256,7 +256,11 @@ int rk_attention(const float *q, const float *k, const float *v, int64_t n_q,
                  float scale, float softcap, int mask_mode, int64_t window,
                  int64_t q0, int64_t k0, float *out);
 
-/* The same on fp16 device buffers in the token-major layout. */
+/* The same on fp16 device buffers in the token-major layout. Library scratch
+ * holds V transposed and, when the launch has at most half as many query
+ * tiles as the GPU has CUs, the partial softmax states of query tiles whose
+ * keys are split between two workgroups (merged in a fixed order: results are
+ * the same from call to call). */
 int rk_attention_dev(const void *q, const void *k, const void *v, int64_t n_q,
                      int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
                      float scale, float softcap, int mask_mode, int64_t window,
@@ -270,8 +274,10 @@ int rk_attention_dev(const void *q, const void *k, const void *v, int64_t n_q,
  * round_up(n_kv, 64) · 2 bytes with dv_pad = head_dim rounded up to 16, is
  * larger return RK_E_RANGE. All calls on one GPU share that array and each
  * call rewrites it: calls whose work overlaps on the device (different streams
- * with no ordering between them) race and give wrong results. Otherwise the
- * same arguments and results as rk_attention_dev. */
+ * with no ordering between them) race and give wrong results. It never
+ * splits a query tile's keys (that needs a workspace); otherwise the same
+ * arguments and results as rk_attention_dev (bit for bit when that split is
+ * off, RK_ATTN_SPLIT=1). */
 #define RK_NOALLOC_SCRATCH_BYTES (32u << 20)
 int rk_attention_dev_noalloc(const void *q, const void *k, const void *v, int64_t n_q,
                              int64_t n_kv, int n_head, int n_kv_heads, int head_dim, float scale,
