@@ -24,7 +24,8 @@
 // workgroup (both form the same QKᵀ and P), so that the four K/Vᵀ buffers fit
 // in LDS and the Oᵀ accumulators in registers. A launch with at most half as
 // many query tiles as CUs splits each tile's key tiles between two workgroups
-// whose softmax states meet in a workspace (KSPLIT, at the end of the kernel).
+// whose softmax states meet in a workspace (KSPLIT, at the end of the kernel);
+// a causal launch of one round splits its longest tiles only.
 //
 // Per wave and 64-key tile (v_mfma_f32_16x16x32_f16 throughout):
 //   Sᵀ = K·Qᵀ   A = K rows from LDS, B = Q fragments held in VGPRs; a lane
@@ -216,10 +217,13 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = (int)((unsigned)wave / NWG), wq = (int)((unsigned)wave % NWG);
   const int KV = a.n_kv_heads;
-  // KSPLIT: workgroups 2t and 2t+1 take the first and the second half of the
-  // key tiles of query tile t.
-  const int ks = KSPLIT ? (int)(blockIdx.x & 1) : 0;
-  const int bid = KSPLIT ? (int)(blockIdx.x >> 1) : (int)blockIdx.x;
+  // KSPLIT: for t < n_split, workgroups 2t and 2t+1 take the first and the
+  // second half of the key tiles of query tile t (ks 0, 1); the workgroups
+  // after them take the other tiles whole (ks -1).
+  const int n_split = KSPLIT ? a.n_split : 0;
+  const bool split_wg = KSPLIT && (int)blockIdx.x < 2 * n_split;
+  const int ks = split_wg ? (int)(blockIdx.x & 1) : -1;
+  const int bid = split_wg ? (int)(blockIdx.x >> 1) : (int)blockIdx.x - n_split;
   const int dch = bid % NCH;  // Oᵀ row chunk
   const int wgq = bid / NCH;
   const int kvh = wgq % KV;
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     const bool degenerate = tkeys.degenerate;
     const int full_lo = tkeys.full_lo, full_hi = tkeys.full_hi;
     int kt_begin = tkeys.kt_begin, kt_end = tkeys.kt_end;
-    if constexpr (KSPLIT) {
+    if (split_wg) {
       const int kt_mid = kt_begin + (kt_end - kt_begin + 1) / 2;
       if (ks == 0)
         kt_end = kt_mid;
@@ -600,7 +604,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
         const float a0 = __builtin_amdgcn_exp2f(m_run[qb] - mu);
         const float a1 = __builtin_amdgcn_exp2f(m1 - mu);
         const float l = lt[qb] * a0 + l1 * a1;
-        if constexpr (KSPLIT) {
+        if (split_wg) {
           m_all[qb] = m;
           l_all[qb] = l;
 #pragma unroll
@@ -629,7 +633,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
         }
       }
     }
-    if constexpr (KSPLIT) {
+    if (split_wg) {
       // Each half writes its state (m, l, unnormalised Oᵀ) to its slot, and
       // the second half to arrive merges the two, in split order whichever it
       // is, and stores O. Nothing waits on the other workgroup. The slots are
@@ -747,7 +751,7 @@ static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
   const int G = a.n_head / a.n_kv_heads;
   const int BQ = 32 * NWG / G;
   const int n_qtiles = (a.n_q + BQ - 1) / BQ;
-  const int grid = n_qtiles * a.n_kv_heads * AttnGeom<D, TK>::NCH * (KSPLIT ? 2 : 1);
+  const int grid = n_qtiles * a.n_kv_heads * AttnGeom<D, TK>::NCH + (KSPLIT ? a.n_split : 0);
   auto kern0 = attn_fa_kernel<D, false, NWG, TK, KSPLIT>;
   auto kern1 = attn_fa_kernel<D, true, NWG, TK, KSPLIT>;
   constexpr int smem = AttnGeom<D, TK>::SMEM;
@@ -782,7 +786,7 @@ static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
 // such a launch splits each query tile's key tiles between two workgroups.
 template <int D>
 static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
-  const bool split = a.part != nullptr && a.cnt != nullptr && rk_attn_split_tiles(a) > 0;
+  const bool split = a.part != nullptr && a.cnt != nullptr && a.n_split > 0;
   // Head dims above 128: 32-key tiles and 128-row Oᵀ chunks (LDS).
   if constexpr (D > 128) {
     if (split) return launch_attn_nwg<D, 4, 32, true>(a, st);
@@ -824,7 +828,13 @@ long rk_attn_split_tiles(const AttnArgs &a) {
   const int BQ = ROWS / G;
   const long tiles = (long)((a.n_q + BQ - 1) / BQ) * a.n_kv_heads * nch;
   const long cus = a.num_cus > 0 ? a.num_cus : 256;
-  return (knob == 2 || 2 * tiles <= cus) ? tiles : 0;
+  if (knob == 2 || 2 * tiles <= cus) return tiles;
+  // One round under a causal mask: the longest tiles set the time.
+  const bool causal = a.mask_mode == RK_MASK_CAUSAL || a.mask_mode == RK_MASK_CAUSAL_WINDOW;
+  const int forced = rk_knob("RK_ATTN_SPLIT_TILES", -1);
+  if (causal && forced >= 0) return std::min<long>(tiles, forced);
+  if (causal && tiles <= cus) return std::min(tiles, (cus - tiles) / 2 + tiles / 8);
+  return 0;
 }
 
 hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st) {

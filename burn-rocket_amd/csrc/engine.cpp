@@ -1020,6 +1020,7 @@ int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_
     if (fresh) HIP_TRY(hipMemsetAsync(cnt, 0, cnt_bytes, st), op);
     a.part = (float *)part;
     a.cnt = (unsigned *)cnt;
+    a.n_split = (int)split;
   }
   HIP_TRY(rk_launch_attention(a, st), op);
   return RK_OK;

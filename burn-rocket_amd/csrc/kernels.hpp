@@ -159,6 +159,7 @@ struct AttnArgs {
   // arrival counter per split query tile, zero between launches.
   float *part;
   unsigned *cnt;
+  int n_split;  // query tiles split (the first ones in dispatch order, the longest)
 };
 // V [n_kv, tok stride] (kv head g at column g·D) → Vt [KV][Dv_pad][n_kv_pad].
 hipError_t rk_launch_v_transpose(const void *v, int64_t v_tok_stride, int64_t v_head_stride,
@@ -168,7 +169,8 @@ int rk_attn_dv_pad(int head_dim);
 int rk_attn_kv_tile();
 hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st);
 // Query tiles whose keys a launch with this shape splits between two
-// workgroups when given the workspace (0: no split), and the floats of one
+// workgroups when given the workspace (0: no split; the longest tiles come
+// first in dispatch order, so they are the ones split), and the floats of one
 // half's partial state.
 long rk_attn_split_tiles(const AttnArgs &a);
 long rk_attn_split_floats(int head_dim);

@@ -172,6 +172,26 @@ def test_key_split(rk, orc, monkeypatch, split, d, h, kv, mode, window, softcap,
     check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, softcap, mode, window, q0, k0))
 
 
+@pytest.mark.parametrize("forced", ["", "7", "200"])
+@pytest.mark.parametrize("mode,window", [(1, -1), (3, 300)])
+def test_key_split_of_the_longest_causal_tiles(rk, orc, monkeypatch, forced, mode, window):
+    """A causal grid of one round splits only its longest query tiles (the first
+    n_split in dispatch order) and runs the rest whole in the same launch; the
+    default count and forced ones (RK_ATTN_SPLIT_TILES), odd included."""
+    note(f"partial key split mode={mode} window={window} forced={forced or 'default'}")
+    monkeypatch.setenv("RK_ATTN_SPLIT_TILES", forced)
+    r = np.random.default_rng(1000 + mode)
+    n, h, kv, d = 1000, 32, 16, 64  # 16 query tiles of 64 × 16 kv heads = 256 tiles
+    q = r.standard_normal((n, h * d)).astype(np.float16)
+    k = r.standard_normal((n, kv * d)).astype(np.float16)
+    v = r.standard_normal((n, kv * d)).astype(np.float16)
+    got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=mode, window=window)
+    again = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=mode, window=window)
+    assert (got == again).all()
+    check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(n, 40) + [(600, 640), (960, 1000)], mode=mode,
+               window=window, ref64=False)
+
+
 @pytest.mark.parametrize("mode,window,softcap,q0,k0,n_q,n_kv", [
     (2, 512, 0.0, 0, 0, 1200, 1200),       # sliding layer, one chunk
     (0, -1, 0.0, 0, 0, 700, 700),          # full layer
