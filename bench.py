@@ -149,7 +149,7 @@ def traffic_probe(layers, launches):
 def probe_all(launches):
     """A few launches of every workload's kernels (for rocprofv3 --pmc runs,
     which serialise and count each dispatch): the W8A8 pair (per-token and
-    group-32 activations), the fp16 GEMMs, the three attentions and the MoE
+    group-32 activations), the fp16 GEMMs, the four attentions and the MoE
     experts."""
     layers = setup_w8a8()
     lib = rk.lib()
@@ -176,6 +176,7 @@ def probe_all(launches):
                                          (synth.VISION["s"], 16, 16, 72, False, synth.SEEDS["vision"][6:9]),
                                          (synth.MOE["s"], 32, 4, 128, True, synth.SEEDS["moe"][6:9])):
         time_attention(s, h, kv, d, causal, seeds, launches)
+    extra_gemma_attention(launches)
     extra_moe(launches)
     rk.synchronize()
     log(f"probe-all: {launches} launches of each workload")
