@@ -250,9 +250,12 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       const int d = 8 * (c - K_INS) + (lane >> 3);
       const int lch = (lane & 7) ^ (d & 7);
       return (uint32_t)d * vrow_b + (uint32_t)(lch * 16);
-    } else {  // 16 Vᵀ rows of 4 chunks, chunk c of row d at c ^ ((d >> 2) & 3)
+    } else {  // 16 Vᵀ rows of 4 chunks, chunk c of row d at c ^ ((d >> 1) & 3): the
+              // 64-byte rows pair up in 128 bytes, and eight consecutive rows
+              // then cover the 128 bytes a fragment read serves at once
+              // (d >> 2 left rows d and d + 2 on the same banks)
       const int d = 16 * (c - K_INS) + (lane >> 2);
-      const int lch = (lane & 3) ^ ((d >> 2) & 3);
+      const int lch = (lane & 3) ^ ((d >> 1) & 3);
       return (uint32_t)d * vrow_b + (uint32_t)(lch * 16);
     }
   };
@@ -285,7 +288,7 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
 #pragma unroll
   for (int c2 = 0; c2 < NC2; ++c2)
     v_off[c2] = TK == 64 ? (uint32_t)(K_BYTES + l16 * 128 + (((4 * c2 + lg) ^ (l16 & 7)) << 4))
-                         : (uint32_t)(K_BYTES + l16 * 64 + ((lg ^ ((l16 >> 2) & 3)) << 4));
+                         : (uint32_t)(K_BYTES + l16 * 64 + ((lg ^ ((l16 >> 1) & 3)) << 4));
 
   const float C = SOFTCAP ? LOG2E : a.scale * LOG2E;
   {
