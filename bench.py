@@ -731,6 +731,9 @@ def main():
                                 oracle, synth.GQA_CAUSAL["s"], synth.GQA_CAUSAL["n_head"], synth.GQA_CAUSAL["n_kv"],
                                 synth.GQA_CAUSAL["d"], True, synth.SEEDS["gqa"], budget, 256, 32)),
                             ("vision_layer_2394", lambda: cpu_vision(oracle, budget)),
+                            ("gemma_attention_d256_2587", lambda: _cpu_attention(
+                                oracle, synth.GEMMA_TEXT["s"], synth.GEMMA_TEXT["n_head"], synth.GEMMA_TEXT["n_kv"],
+                                synth.GEMMA_TEXT["d"], False, synth.SEEDS["gemma"], budget, 256, 32)),
                             ("moe_30b_a3b_1024", lambda: cpu_moe(oracle, _MOE_STATE, budget))):
                 log(f"CPU baseline: {key}")
                 extras[key]["cpu_baseline"] = fn()
