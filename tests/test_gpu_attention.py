@@ -215,6 +215,24 @@ def test_head_dim_256_gemma_layers(rk, orc, mode, window, softcap, q0, k0, n_q, 
                q0=q0, k0=k0)
 
 
+@pytest.mark.parametrize("mode,window", [(0, -1), (2, 512)])
+def test_gemma_attention_at_the_bench_size(rk, orc, mode, window):
+    """EmbeddingGemma's attention at the measured size (2587 tokens, 3 query heads
+    on 1 kv head of 256, full and 512-key sliding layers; key split on by
+    default at this grid), on row slices from the start, middle and end, and
+    bit-identical from one call to the next."""
+    c = synth.GEMMA_TEXT
+    s, h, kv, d = c["s"], c["n_head"], c["n_kv"], c["d"]
+    note(f"gemma bench size S={s} mode={mode} window={window}")
+    seeds = synth.SEEDS["gemma"]
+    q = synth.normal_f16(seeds[0], (s, h * d))
+    k = synth.normal_f16(seeds[1], (s, kv * d))
+    v = synth.normal_f16(seeds[2], (s, kv * d))
+    got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=mode, window=window)
+    assert (got == attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=mode, window=window)).all()
+    check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(s, 48), mode=mode, window=window)
+
+
 def test_softcap(rk, orc):
     note("softcap 20")
     r = np.random.default_rng(99)
