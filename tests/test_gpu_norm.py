@@ -517,7 +517,7 @@ def test_qk_norm_rope_head_counts(rk, orc, hq, hk, s):
 
 
 @pytest.mark.parametrize("s,hq,hk,d,mode", [(203, 4, 2, 128, 1), (150, 3, 3, 72, 0), (64, 8, 1, 64, 1),
-                                            (1, 2, 1, 128, 1)])
+                                            (1, 2, 1, 128, 1), (300, 3, 1, 256, 0), (300, 3, 1, 256, 1)])
 def test_attention_qkv_equals_prologue_then_strided_attention(rk, orc, s, hq, hk, d, mode):
     note(f"rk_attention_qkv_dev S={s} {hq}/{hk} d={d} mode={mode}")
     width = (hq + 2 * hk) * d + 8
