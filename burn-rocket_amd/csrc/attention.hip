@@ -786,7 +786,9 @@ static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
 //
 // A grid that fills at most half of the CUs (few query heads, short
 // sequences) leaves the rest idle for the whole launch: given the workspace,
-// such a launch splits each query tile's key tiles between two workgroups.
+// such a launch splits each query tile's key tiles between two workgroups. A
+// causal grid of one round splits its first a.n_split tiles, the longest
+// (rk_attn_split_tiles).
 template <int D>
 static hipError_t launch_attn(const AttnArgs &a, hipStream_t st) {
   const bool split = a.part != nullptr && a.cnt != nullptr && a.n_split > 0;
