@@ -209,6 +209,9 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
   constexpr int CPW = (K_INS + V_INS + NWG - 1) / NWG;  // copies per wave of a group
   // Reads ahead: fewer with 3 waves per SIMD, whose register budget is 168.
   constexpr int LAW = NWG == 4 ? LA : 3;
+  // (at most the fragments a slot reads: head dim 32 has four per product)
+  constexpr int NF_ = NC2 * NDB, NR_ = NKB * (NQC + (TAIL16 ? 1 : 0));
+  constexpr int LAWV = LAW < NF_ ? LAW : NF_, LAWK = LAW < NR_ ? LAW : NR_;
   static_assert(Gm::SMEM <= 160 * 1024, "LDS");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -399,13 +402,13 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
         }
         vprev = vcur;
       });
-      // Each fragment read LAW reads ahead of its four MFMAs.
-      __builtin_amdgcn_sched_group_barrier(0x100, LAW, 0);
-      static_for<NF - LAW>([&](auto) {
+      // Each fragment read LAWV reads ahead of its four MFMAs.
+      __builtin_amdgcn_sched_group_barrier(0x100, LAWV, 0);
+      static_for<NF - LAWV>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       });
-      __builtin_amdgcn_sched_group_barrier(0x008, 4 * LAW, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * LAWV, 0);
     }
     // P of tile j-1 dies here, before S of tile j is produced (keeps the two
     // register sets from overlapping).
@@ -436,14 +439,14 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
             sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x16f16(kfr, qt16[qb], sacc[kb][qb], 0, 0, 0);
         }
       }
-      // Each fragment read LAW reads ahead of its two MFMAs.
+      // Each fragment read LAWK reads ahead of its two MFMAs.
       constexpr int NR = NKB * (NQC + (TAIL16 ? 1 : 0));
-      __builtin_amdgcn_sched_group_barrier(0x100, LAW, 0);
-      static_for<NR - LAW>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x100, LAWK, 0);
+      static_for<NR - LAWK>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       });
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * LAW, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * LAWK, 0);
     }
     };
     // VALU slot j: online softmax of tile j. Scores stay in the raw domain s
@@ -846,6 +849,10 @@ hipError_t rk_launch_attention(const AttnArgs &a, hipStream_t st) {
   const int G = a.n_head / a.n_kv_heads;
   if (G < 1 || G > ROWS || a.n_head % a.n_kv_heads) return hipErrorInvalidValue;
   switch (a.head_dim) {
+    case 32:
+      return launch_attn<32>(a, st);
+    case 48:
+      return launch_attn<48>(a, st);
     case 64:
       return launch_attn<64>(a, st);
     case 72:

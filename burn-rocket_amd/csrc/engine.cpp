@@ -949,10 +949,10 @@ int attn_check(int64_t n_q, int64_t n_kv, int n_head, int n_kv_heads, int head_d
     return fail(RK_E_SHAPE, op, "n_head must be a positive multiple of n_kv_heads");
   if (n_head / n_kv_heads > 128) return fail(RK_E_SHAPE, op, "GQA group above 128");
   switch (head_dim) {
-    case 64: case 72: case 80: case 96: case 112: case 128: case 256: break;
+    case 32: case 48: case 64: case 72: case 80: case 96: case 112: case 128: case 256: break;
     default:
       return fail(RK_E_UNSUPPORTED, op, "head_dim " + std::to_string(head_dim) +
-                                            " (supported: 64, 72, 80, 96, 112, 128, 256)");
+                                            " (supported: 32, 48, 64, 72, 80, 96, 112, 128, 256)");
   }
   if (*mode < RK_MASK_NONE || *mode > RK_MASK_CAUSAL_WINDOW)
     return fail(RK_E_SHAPE, op, "unknown mask mode");

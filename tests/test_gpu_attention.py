@@ -87,7 +87,7 @@ def test_config5_gqa_32_4_full(rk, orc):
     check_rows(orc, got, q, k, v, h, kv, d, d ** -0.5, _slices(s, 64), mode=1)
 
 
-@pytest.mark.parametrize("d", [64, 72, 80, 96, 112, 128, 256])
+@pytest.mark.parametrize("d", [32, 48, 64, 72, 80, 96, 112, 128, 256])
 @pytest.mark.parametrize("h,kv", [(4, 4), (8, 2), (16, 2), (6, 3)])
 def test_head_dims_and_groups(rk, orc, d, h, kv):
     note(f"attention d={d} h={h} kv={kv}")
@@ -101,7 +101,7 @@ def test_head_dims_and_groups(rk, orc, d, h, kv):
         check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, mode=mode))
 
 
-@pytest.mark.parametrize("d", [64, 72, 80])
+@pytest.mark.parametrize("d", [32, 48, 64, 72, 80])
 @pytest.mark.parametrize("h,kv", [(4, 4), (8, 2), (6, 3), (16, 16)])
 def test_192_row_tiles(rk, orc, d, h, kv, monkeypatch):
     """Head dims up to 80 also run on 192-row query tiles (6 waves per key
