@@ -1162,12 +1162,20 @@ extern "C" int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv
   const char *op = "rk_flash_attn_f16";
   RK_TRY(ensure(op));
   if (head_dim <= 0 || dv <= 0) return fail(RK_E_SHAPE, op, "head_dim and dv must be positive");
-  // The kernel runs one width D = max(head_dim, dv) for q, k and v: zero
-  // columns added to q and k leave every score unchanged, zero rows added to
-  // Vᵀ only add zero output columns, so the first dv output columns are the
-  // attention of the given operands (the reference pads Clef's 72-wide heads
-  // to head_dim 96 / dv 80 the same way, src/clef/vision/npu.rs:211-230).
-  const int D = std::max(head_dim, dv);
+  // The kernel runs one width D for q, k and v, the smallest kernel width at
+  // least max(head_dim, dv): zero columns added to q and k leave every score
+  // unchanged, zero rows added to Vᵀ only add zero output columns, so the
+  // first dv output columns are the attention of the given operands (the
+  // reference pads Clef's 72-wide heads to head_dim 96 / dv 80 the same way,
+  // src/clef/vision/npu.rs:211-230). Its own contract, head_dim % 32 and
+  // dv % 16 with no upper bound (attn/mod.rs:1443), is met here up to 256.
+  int D = 0;
+  for (int w : {32, 48, 64, 72, 80, 96, 112, 128, 256})
+    if (D == 0 && std::max(head_dim, dv) <= w) D = w;
+  if (D == 0)
+    return fail(RK_E_UNSUPPORTED, op,
+                "head_dim " + std::to_string(head_dim) + " / dv " + std::to_string(dv) +
+                    " above the widest kernel (256)");
   int mode = mask_mode;
   RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, D, &mode, window, op));
   hipStream_t st = g_eng->stream;

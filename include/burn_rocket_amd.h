@@ -300,8 +300,10 @@ int rk_attention_strided_dev(const void *q, int64_t q_stride, const void *k, int
  * [head_dim], v transposed [n_kv_heads][dv][n_kv], out [n_head][n_q][dv].
  * head_dim (the q·k width) and dv (the v width) are independent, as in the
  * reference's padded calls (Clef's 72-wide vision heads as head_dim 96,
- * dv 80: src/clef/vision/npu.rs:211-230); max(head_dim, dv) must be one of
- * the kernel widths 32, 48, 64, 72, 80, 96, 112, 128, 256. The reference's optional
+ * dv 80: src/clef/vision/npu.rs:211-230); max(head_dim, dv) is zero-padded
+ * to the next kernel width (32, 48, 64, 72, 80, 96, 112, 128, 256), so the
+ * reference's contract head_dim % 32, dv % 16 (attn/mod.rs:1443) holds up to
+ * 256; wider heads return RK_E_UNSUPPORTED. The reference's optional
  * additive mask tensor is replaced by mask_mode / window / q0 / k0. */
 int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv,
                       int n_head, int n_kv_heads, float scale, float softcap,

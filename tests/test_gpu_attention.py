@@ -303,6 +303,34 @@ def test_flash_attn_clef_padded_layout(rk, orc, mode):
     check(orc, o2[:, :, :d].transpose(1, 0, 2).reshape(s, h * d).astype(np.float32), got)
 
 
+@pytest.mark.parametrize("hd,dv", [(32, 16), (64, 48), (96, 112), (160, 144), (192, 192), (224, 64)])
+def test_flash_attn_head_dims_of_the_reference_contract(rk, orc, hd, dv):
+    """`check_flash` accepts any head_dim % 32 and dv % 16 (attn/mod.rs:1443):
+    widths between the kernel's run on the next kernel width, zero-padded.
+    Checked against the oracle on operands zero-padded to a common width
+    (zero q/k columns leave the scores, zero V columns give zero outputs)."""
+    s, h, kv = 150, 4, 2
+    note(f"flash_attn head_dim {hd} dv {dv}")
+    r = np.random.default_rng(hd * 7 + dv)
+    w = max(hd, dv)
+    q = np.zeros((h, s, w), np.float16)
+    k = np.zeros((kv, s, w), np.float16)
+    v = np.zeros((kv, s, w), np.float16)
+    q[:, :, :hd] = r.standard_normal((h, s, hd))
+    k[:, :, :hd] = r.standard_normal((kv, s, hd))
+    v[:, :, :dv] = r.standard_normal((kv, s, dv))
+    vt = np.ascontiguousarray(v[:, :, :dv].transpose(0, 2, 1))  # [kv][dv][s]
+    for mode in (0, 1):
+        o = rk.flash_attn_f16(np.ascontiguousarray(q[:, :, :hd]), np.ascontiguousarray(k[:, :, :hd]), vt, s, s,
+                              hd, h, kv, hd ** -0.5, 0.0, mode, dv=dv)
+        assert o.shape == (h, s, dv)
+        got = o.transpose(1, 0, 2).reshape(s, h * dv).astype(np.float32)
+        tok = lambda x: x.transpose(1, 0, 2).reshape(s, -1)  # [heads][s][w] → [s, heads·w]
+        ref = orc.attention_ref(tok(q), tok(k), tok(v), h, kv, w, hd ** -0.5, 0.0, mode)
+        ref = ref.reshape(s, h, w)[:, :, :dv].reshape(s, h * dv)
+        check(orc, got, ref)
+
+
 def test_attention_rejects_bad_shapes(rk):
     note("attention errors")
     lib = rk.lib()
