@@ -941,8 +941,9 @@ hipError_t rk_launch_v_transpose_strided(const void *v, int64_t tok_stride, int6
                                          int n_kv_heads, int head_dim, int dv_pad, void *vt,
                                          hipStream_t st);
 namespace {
+// padded: also head dims 160, 192 and 224, which attn_dev_impl runs zero-padded.
 int attn_check(int64_t n_q, int64_t n_kv, int n_head, int n_kv_heads, int head_dim, int *mode,
-               int64_t window, const char *op) {
+               int64_t window, const char *op, bool padded = false) {
   if (n_q <= 0 || n_kv <= 0) return fail(RK_E_SHAPE, op, "empty query or key axis");
   if (n_q > INT32_MAX || n_kv > INT32_MAX) return fail(RK_E_SHAPE, op, "sequence too long");
   if (n_head <= 0 || n_kv_heads <= 0 || n_head % n_kv_heads != 0)
@@ -950,6 +951,9 @@ int attn_check(int64_t n_q, int64_t n_kv, int n_head, int n_kv_heads, int head_d
   if (n_head / n_kv_heads > 128) return fail(RK_E_SHAPE, op, "GQA group above 128");
   switch (head_dim) {
     case 32: case 48: case 64: case 72: case 80: case 96: case 112: case 128: case 256: break;
+    case 160: case 192: case 224:
+      if (padded) break;
+      [[fallthrough]];
     default:
       return fail(RK_E_UNSUPPORTED, op, "head_dim " + std::to_string(head_dim) +
                                             " (supported: 32, 48, 64, 72, 80, 96, 112, 128, 256)");
@@ -1033,6 +1037,38 @@ int attn_dev_impl(CallScope &cs, const void *q, const void *k, const void *v, in
                   float softcap, int mode, int64_t window, int64_t q0, int64_t k0, void *out,
                   const char *op, int64_t q_ts = 0, int64_t k_ts = 0, int64_t v_ts = 0,
                   int64_t o_ts = 0, HostTimer *tm = nullptr) {
+  // Head dims of the reference's contract (head_dim % 32, attn/mod.rs:1443)
+  // between the kernel widths (160, 192, 224) run zero-padded to 256 on
+  // packed token-major operands: zero q/k columns leave the scores, zero V
+  // columns only give output columns that are not copied back.
+  const int pad_w = head_dim > 128 && head_dim < 256 && head_dim % 32 == 0 ? 256 : 0;
+  if (pad_w) {
+    if ((q_ts && q_ts != (int64_t)n_head * head_dim) || (k_ts && k_ts != (int64_t)n_kv_heads * head_dim) ||
+        (v_ts && v_ts != (int64_t)n_kv_heads * head_dim) || (o_ts && o_ts != (int64_t)n_head * head_dim))
+      return fail(RK_E_UNSUPPORTED, op, "head_dim " + std::to_string(head_dim) + " with token strides");
+    RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, pad_w, &mode, window, op));
+    const size_t hd = (size_t)head_dim * 2, w = (size_t)pad_w * 2;
+    void *qp, *kp, *vp, *op_;
+    RK_TRY(scratch(cs, "attn_pad_q", (size_t)n_q * n_head * w, &qp));
+    RK_TRY(scratch(cs, "attn_pad_k", (size_t)n_kv * n_kv_heads * w, &kp));
+    RK_TRY(scratch(cs, "attn_pad_v", (size_t)n_kv * n_kv_heads * w, &vp));
+    RK_TRY(scratch(cs, "attn_pad_o", (size_t)n_q * n_head * w, &op_));
+    const struct {
+      const void *src;
+      void *dst;
+      size_t rows;
+    } in[3] = {{q, qp, (size_t)n_q * n_head}, {k, kp, (size_t)n_kv * n_kv_heads},
+               {v, vp, (size_t)n_kv * n_kv_heads}};
+    for (const auto &t : in) {
+      HIP_TRY(hipMemsetAsync(t.dst, 0, t.rows * w, cs.st), op);
+      HIP_TRY(hipMemcpy2DAsync(t.dst, w, t.src, hd, hd, t.rows, hipMemcpyDeviceToDevice, cs.st), op);
+    }
+    RK_TRY(attn_dev_impl(cs, qp, kp, vp, n_q, n_kv, n_head, n_kv_heads, pad_w, scale, softcap, mode,
+                         window, q0, k0, op_, op, 0, 0, 0, 0, tm));
+    HIP_TRY(hipMemcpy2DAsync(out, hd, op_, w, hd, (size_t)n_q * n_head, hipMemcpyDeviceToDevice, cs.st),
+            op);
+    return RK_OK;
+  }
   RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, op));
   const int dvp = rk_attn_dv_pad(head_dim);
   const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
@@ -1122,7 +1158,7 @@ extern "C" int rk_attention(const float *q, const float *k, const float *v, int6
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_attention"));
   int mode = mask_mode;
-  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, "rk_attention"));
+  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, "rk_attention", true));
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
   HostTimer tm(st);

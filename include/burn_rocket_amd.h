@@ -250,7 +250,10 @@ int rk_matmul_i8_partials_dev(rk_weight_id id, const int8_t *a, int64_t m,
  * 0), f32 online softmax over the visible keys, fp16 operands, fp16 result
  * widened to f32. A query row with no visible key averages V uniformly over
  * the n_kv keys (flash_attn_ref, attn/oneshot.rs:118-127). window < 0 turns
- * the window modes into NONE / CAUSAL (ext.rs:99-126). */
+ * the window modes into NONE / CAUSAL (ext.rs:99-126). head_dim: 32, 48, 64,
+ * 72, 80, 96, 112, 128 or 256, and 160, 192, 224 (run zero-padded to 256, on
+ * packed rows; the reference's contract is head_dim % 32, attn/mod.rs:1443);
+ * others return RK_E_UNSUPPORTED. */
 int rk_attention(const float *q, const float *k, const float *v, int64_t n_q,
                  int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
                  float scale, float softcap, int mask_mode, int64_t window,

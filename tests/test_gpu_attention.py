@@ -331,6 +331,34 @@ def test_flash_attn_head_dims_of_the_reference_contract(rk, orc, hd, dv):
         check(orc, got, ref)
 
 
+@pytest.mark.parametrize("d", [160, 192, 224])
+def test_token_major_head_dims_run_padded(rk, orc, d):
+    """rk_attention_dev and rk_attention take the head dims of the reference's
+    contract between the kernel widths (head_dim % 32 above 128) and run them
+    zero-padded to 256; the no-allocation entry and token strides wider than
+    the packed rows refuse them."""
+    note(f"token-major head dim {d} (padded to 256)")
+    r = np.random.default_rng(d)
+    n, h, kv = 130, 4, 2
+    q = r.standard_normal((n, h * d)).astype(np.float16)
+    k = r.standard_normal((n, kv * d)).astype(np.float16)
+    v = r.standard_normal((n, kv * d)).astype(np.float16)
+    for mode in (0, 1):
+        got = attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=mode)
+        check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, 0.0, mode))
+    host = rk.attention(q[None].astype(np.float32), k[None].astype(np.float32), v[None].astype(np.float32), h, kv, d,
+                        d ** -0.5, is_causal=True)
+    check(orc, np.asarray(host, np.float32).reshape(n, h * d), orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, 0.0, 1))
+    lib = rk.lib()
+    bufs = [rk.DeviceBuffer.from_array(np.ascontiguousarray(a).view(np.uint16)) for a in (q, k, v)]
+    out = rk.DeviceBuffer(n * h * d * 2)
+    assert lib.rk_attention_dev_noalloc(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, n, n, h, kv, d, 0.1, 0.0, 0, -1, 0, 0,
+                                        out.ptr, None) == rk.RK_E_UNSUPPORTED
+    wide = rk.DeviceBuffer(n * (h * d + 8) * 2)
+    assert lib.rk_attention_strided_dev(wide.ptr, h * d + 8, bufs[1].ptr, kv * d, bufs[2].ptr, kv * d, n, n, h, kv,
+                                        d, 0.1, 0.0, 0, -1, 0, 0, out.ptr, h * d, None) == rk.RK_E_UNSUPPORTED
+
+
 def test_attention_rejects_bad_shapes(rk):
     note("attention errors")
     lib = rk.lib()
