@@ -68,8 +68,10 @@ SIGNATURES = {
     "rk_pack_moe_q8_0": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
     "rk_pack_moe_f32": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
     "rk_moe_experts_dev": (_i, [_u64, _p, _i64, _i, _p, _p, _p, _p]),
+    "rk_moe_experts_acc_dev": (_i, [_u64, _p, _i64, _i, _p, _p, _p, _p]),
     "rk_moe_plan_create": (_i, [_u64, _i64, _i, _p, _p, _p]),
     "rk_moe_experts_planned_dev": (_i, [_u64, _p, _p, _p, _p]),
+    "rk_moe_experts_planned_acc_dev": (_i, [_u64, _p, _p, _p, _p]),
     "rk_moe_plan_destroy": (_i, [_p]),
     "rk_moe_gate_up_dev": (_i, [_u64, _p, _p, _p, _p]),
     "rk_device_alloc": (_i, [_sz, _p]),

@@ -1501,11 +1501,11 @@ int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const f
 }
 
 int moe_run(CallScope &cs, const Weight &w, const MoePlan &plan, const float *x, float *y,
-            float *act_out = nullptr) {
+            float *act_out = nullptr, bool accumulate = false) {
   hipStream_t st = cs.st;
   const int64_t H = w.hidden, I = w.inter, S = plan.s, R = std::max<int64_t>(plan.rows, 1);
   const int64_t KBh = H / 32, KBi = I / 32;  // 32-value activation groups per row
-  void *xq, *xs, *act, *aq, *as, *yb;
+  void *xq, *xs, *act, *aq, *as, *yb, *cnt;
   RK_TRY(scratch(cs, "moe_xq", (size_t)S * H, &xq));
   RK_TRY(scratch(cs, "moe_xs", (size_t)S * KBh * 4, &xs));
   if (act_out)
@@ -1515,24 +1515,37 @@ int moe_run(CallScope &cs, const Weight &w, const MoePlan &plan, const float *x,
   RK_TRY(scratch(cs, "moe_aq", (size_t)R * I, &aq));
   RK_TRY(scratch(cs, "moe_as", (size_t)R * KBi * 4, &as));
   RK_TRY(scratch(cs, "moe_yb", (size_t)R * H * 4, &yb));
+  // One arrival counter per (token, 128-column slice) for the combine in the
+  // down launch. Each launch leaves them at zero; a new buffer is zeroed once.
+  const size_t cnt_bytes = (size_t)S * ((H + 127) / 128) * 4;
+  bool fresh = false;
+  RK_TRY(scratch(cs, "moe_cnt", cnt_bytes, &cnt, &fresh));
   const char *op = "rk_moe_experts_dev";
+  if (fresh) HIP_TRY(hipMemsetAsync(cnt, 0, std::max<size_t>(cnt_bytes, 256), st), op);
   // x and the silu·up rows are quantized per row per 32-value group, as the
   // reference's expert workers do (engine.rs:1005-1006, 1034-1035).
   HIP_TRY(rk_launch_quantize_rows(x, S, H, 32, (int8_t *)xq, (float *)xs, st), op);
   HIP_TRY(rk_launch_moe_gemm_gu(plan.tile_rows, (const int8_t *)xq, (const float *)xs, (int)KBh, plan.tok, S,
                                 plan.tiles, plan.n_tiles, w.gu_codes, w.gu_scales,
                                 moe_gu_code_stride(w), 2 * I * w.gu_ws_stride, w.gu_ws_stride,
-                                (int)(2 * I), (int)H, (float *)act, g_eng->num_cus, st),
+                                (int)(2 * I), (int)H, (float *)act, st),
           op);
   if (!y) return RK_OK;  // stage 1 only
   HIP_TRY(rk_launch_quantize_rows((const float *)act, plan.rows, I, 32, (int8_t *)aq, (float *)as, st),
           op);
+  MoeCombine cmb;
+  cmb.tok = plan.tok;
+  cmb.slot = plan.slot;
+  cmb.cnt = (unsigned *)cnt;
+  cmb.y = y;
+  cmb.n_tok = (int)S;
+  cmb.top_k = plan.top_k;
+  cmb.accumulate = accumulate ? 1 : 0;
   HIP_TRY(rk_launch_moe_gemm_down(plan.tile_rows, (const int8_t *)aq, (const float *)as, (int)KBi, plan.rows,
                                   plan.tiles, plan.n_tiles, w.dn_codes, w.dn_scales,
                                   moe_dn_code_stride(w), H * w.dn_ws_stride, w.dn_ws_stride, (int)H,
-                                  (int)I, plan.roww, (float *)yb, g_eng->num_cus, st),
+                                  (int)I, plan.roww, (float *)yb, cmb, st),
           op);
-  HIP_TRY(rk_launch_moe_combine((const float *)yb, plan.slot, S, plan.top_k, H, y, st), op);
   return RK_OK;
 }
 
@@ -1557,6 +1570,49 @@ int moe_check(uint64_t id, int64_t s, int top_k, Weight **w, const char *op) {
   // quantized silu·up rows [s·top_k, inter]) with 32-bit byte offsets.
   if (s * (*w)->hidden >= ((int64_t)1 << 31) || s * top_k * (*w)->inter >= ((int64_t)1 << 31))
     return fail(RK_E_SHAPE, op, "s·hidden and s·top_k·inter must stay below 2^31");
+  // The combine reads the per-slot f32 rows [s·top_k, hidden] the same way.
+  if (s * top_k * (*w)->hidden * 4 >= ((int64_t)1 << 31))
+    return fail(RK_E_SHAPE, op, "s·top_k·hidden f32 values must stay below 2^31 bytes");
+  return RK_OK;
+}
+}  // namespace
+
+namespace {
+int moe_experts(rk_weight_id id, const float *x, int64_t s, int top_k, const uint32_t *ids,
+                const float *wts, float *y, rk_stream stream, bool accumulate, const char *op) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure(op));
+  Weight *w;
+  RK_TRY(moe_check(id, s, top_k, &w, op));
+  if (!x || !y || !ids || !wts) return fail(RK_E_SHAPE, op, "null buffer");
+  hipStream_t st = pick(stream);
+  CallScope cs(st);
+  MoePlan *plan = new MoePlan();
+  int rc = moe_plan(*w, s, top_k, ids, wts, plan, st);
+  if (rc == RK_OK) rc = moe_run(cs, *w, *plan, x, y, nullptr, accumulate);
+  // The plan's lists must outlive the kernels that read them.
+  hipError_t e = hipStreamSynchronize(st);
+  plan_free(plan);
+  if (rc != RK_OK) return rc;
+  HIP_TRY(e, op);
+  g_eng->calls++;
+  return RK_OK;
+}
+
+int moe_experts_planned(rk_weight_id id, const void *plan, const float *x, float *y, rk_stream stream,
+                        bool accumulate, const char *op) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure(op));
+  const MoePlan *p = (const MoePlan *)plan;
+  if (!p) return fail(RK_E_SHAPE, op, "null plan");
+  if (!x || !y) return fail(RK_E_SHAPE, op, "null buffer");
+  Weight *w;
+  RK_TRY(moe_check(id, p->s, p->top_k, &w, op));
+  if (p->weight != id) return fail(RK_E_SHAPE, op, "plan was made for another expert stack");
+  CallScope cs(pick(stream));
+  RK_TRY(moe_run(cs, *w, *p, x, y, nullptr, accumulate));
+  RK_TRY(plan_mark_used(*p, cs.st));
+  g_eng->calls++;
   return RK_OK;
 }
 }  // namespace
@@ -1564,22 +1620,13 @@ int moe_check(uint64_t id, int64_t s, int top_k, Weight **w, const char *op) {
 extern "C" int rk_moe_experts_dev(rk_weight_id id, const float *x, int64_t s, int top_k,
                                   const uint32_t *ids, const float *wts, float *y,
                                   rk_stream stream) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  RK_TRY(ensure("rk_moe_experts_dev"));
-  Weight *w;
-  RK_TRY(moe_check(id, s, top_k, &w, "rk_moe_experts_dev"));
-  hipStream_t st = pick(stream);
-  CallScope cs(st);
-  MoePlan *plan = new MoePlan();
-  int rc = moe_plan(*w, s, top_k, ids, wts, plan, st);
-  if (rc == RK_OK) rc = moe_run(cs, *w, *plan, x, y);
-  // The plan's lists must outlive the kernels that read them.
-  hipError_t e = hipStreamSynchronize(st);
-  plan_free(plan);
-  if (rc != RK_OK) return rc;
-  HIP_TRY(e, "rk_moe_experts_dev");
-  g_eng->calls++;
-  return RK_OK;
+  return moe_experts(id, x, s, top_k, ids, wts, y, stream, false, "rk_moe_experts_dev");
+}
+
+extern "C" int rk_moe_experts_acc_dev(rk_weight_id id, const float *x, int64_t s, int top_k,
+                                      const uint32_t *ids, const float *wts, float *y,
+                                      rk_stream stream) {
+  return moe_experts(id, x, s, top_k, ids, wts, y, stream, true, "rk_moe_experts_acc_dev");
 }
 
 extern "C" int rk_moe_plan_create(rk_weight_id id, int64_t s, int top_k, const uint32_t *ids,
@@ -1601,19 +1648,12 @@ extern "C" int rk_moe_plan_create(rk_weight_id id, int64_t s, int top_k, const u
 
 extern "C" int rk_moe_experts_planned_dev(rk_weight_id id, const void *plan, const float *x,
                                           float *y, rk_stream stream) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  RK_TRY(ensure("rk_moe_experts_planned_dev"));
-  const MoePlan *p = (const MoePlan *)plan;
-  if (!p) return fail(RK_E_SHAPE, "rk_moe_experts_planned_dev", "null plan");
-  Weight *w;
-  RK_TRY(moe_check(id, p->s, p->top_k, &w, "rk_moe_experts_planned_dev"));
-  if (p->weight != id)
-    return fail(RK_E_SHAPE, "rk_moe_experts_planned_dev", "plan was made for another expert stack");
-  CallScope cs(pick(stream));
-  RK_TRY(moe_run(cs, *w, *p, x, y));
-  RK_TRY(plan_mark_used(*p, cs.st));
-  g_eng->calls++;
-  return RK_OK;
+  return moe_experts_planned(id, plan, x, y, stream, false, "rk_moe_experts_planned_dev");
+}
+
+extern "C" int rk_moe_experts_planned_acc_dev(rk_weight_id id, const void *plan, const float *x,
+                                              float *y, rk_stream stream) {
+  return moe_experts_planned(id, plan, x, y, stream, true, "rk_moe_experts_planned_acc_dev");
 }
 
 extern "C" int rk_moe_gate_up_dev(rk_weight_id id, const void *plan, const float *x, float *act,

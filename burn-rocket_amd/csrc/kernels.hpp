@@ -190,15 +190,27 @@ int rk_moe_tile_rows();
 hipError_t rk_launch_moe_gemm_gu(int tile_rows, const int8_t *xq, const float *xs, int xs_stride,
                                  const int32_t *tok, int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
                                  const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
-                                 int ws_stride, int N, int K, float *act, int num_cus,
-                                 hipStream_t st);
+                                 int ws_stride, int N, int K, float *act, hipStream_t st);
+// The combine fused into the down launch (src/clef/engine.rs:317-338): y[t]
+// (+)= the token's yb rows in ascending expert id, summed by the workgroup
+// whose rows complete the token's top_k for its column slice. cnt holds one
+// counter per (token, slice of 128 or 256 columns), zero before the launch and
+// zero again after it; yb (bucket rows × N f32) must stay below 2^31 bytes.
+struct MoeCombine {
+  const int32_t *tok = nullptr;   // [rows] token of each bucket row
+  const int32_t *slot = nullptr;  // [s, top_k] bucket rows of a token, ascending expert id
+  unsigned *cnt = nullptr;        // [s, ceil(N / 128)] arrival counters
+  float *y = nullptr;             // [s, N]
+  int n_tok = 0;                  // s: rows of y
+  int top_k = 0;
+  int accumulate = 0;             // 1: y += the sum (onto the residual); 0: y = the sum
+  int n_tiles = 0;                // set by the launcher
+};
 hipError_t rk_launch_moe_gemm_down(int tile_rows, const int8_t *aq, const float *as, int as_stride, int64_t rows,
                                    const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
                                    int64_t w_stride_e, int64_t ws_stride_e, int ws_stride,
-                                   int N, int K, const float *row_w, float *yb, int num_cus,
+                                   int N, int K, const float *row_w, float *yb, const MoeCombine &cmb,
                                    hipStream_t st);
-hipError_t rk_launch_moe_combine(const float *yb, const int32_t *slot_rows, int64_t s, int top_k,
-                                 int64_t h, float *y, hipStream_t st);
 
 // The static device scratch of rk_attention_dev_noalloc (noalloc.hip):
 // rk_noalloc_setup looks up the array's address on `device`, which must be

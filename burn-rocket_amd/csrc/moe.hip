@@ -47,7 +47,14 @@
 //            through ds_bpermute and the epilogue writes
 //            act = silu(g) · u, silu(v) = v / (1 + e^-v) (src/clef/model.rs:
 //            491-493) with e^-v rounded once from f64 (exp_rn).
-//   down:    yb[row] = acc · router weight of the row (engine.rs:649-650).
+//   down:    yb[row] = acc · router weight of the row (engine.rs:649-650),
+//            then the combine (engine.rs:317-338) in the same launch: every
+//            workgroup counts its rows in on a per-(token, column slice)
+//            arrival counter, and the workgroup whose arrival completes a
+//            token's top_k rows sums them in ascending expert id into y
+//            (onto y's old value in accumulate mode). No workgroup waits on
+//            another, and the sum's order does not depend on which one
+//            arrives last, so y is the same from call to call.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -63,10 +70,11 @@ template <int BM> constexpr int moe_s_stage() { return 4 * BM * 4; }
 template <int BM> constexpr int moe_slot() { return moe_a_stage<BM>() + moe_s_stage<BM>(); }
 
 // LDS: the (PD+1)-slot ring of token-row stages with their scales, then the
-// router weight of each tile row.
+// router weight of each tile row, and for the combine the tokens the
+// workgroup completes, their slot rows and their count.
 template <int PD, int BM>
 constexpr int moe_smem() {
-  return (PD + 1) * moe_slot<BM>() + BM * 4;
+  return (PD + 1) * moe_slot<BM>() + BM * 4 + BM * 4 + BM * 8 * 4 + 16;
 }
 }  // namespace
 
@@ -85,7 +93,8 @@ __device__ __forceinline__ void moe_body(
     const int8_t *__restrict__ A, const float *__restrict__ AS, int as_stride,
     const int32_t *__restrict__ tok, int64_t a_rows, const MoeTile &tile,
     const int8_t *__restrict__ We, const float *__restrict__ WSe, int ws_stride, int N, int K,
-    int n0, const float *__restrict__ row_w, float *__restrict__ out, int out_ld, uint8_t *smem) {
+    int n0, const float *__restrict__ row_w, float *__restrict__ out, int out_ld, const MoeCombine &cmb,
+    uint8_t *smem) {
   constexpr int ROWB = MOE_ROWB, NSLOT = PD + 1;
   constexpr int MOE_A_STAGE = moe_a_stage<BM>(), MOE_SLOT = moe_slot<BM>();
   constexpr int QA = BM / 8;     // 8-row copies of token rows per stage
@@ -324,6 +333,8 @@ __device__ __forceinline__ void moe_body(
   // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of each 32-row
   // block, column lane%32 of the wave's 32 columns.
   const int col = n0 + wave * 32 + fcol;
+  constexpr int SC1 = 16;  // cache policy bit: device scope
+  const rsrc_t ryb = make_rsrc(out + (int64_t)tile.row0 * out_ld, (int64_t)tile.rows * out_ld * 4);
 #pragma unroll
   for (int i = 0; i < NRB; ++i) {
     if constexpr (GU) {
@@ -348,11 +359,114 @@ __device__ __forceinline__ void moe_body(
         }
       }
     } else {
+      // yb rows with device-coherent (sc1) stores: the workgroup that
+      // completes a token may run on another XCD, whose L2 does not see this
+      // one's.
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = i * 32 + (r >> 2) * 8 + fh * 4 + (r & 3);
         if (row < tile.rows && col < N)
-          out[(int64_t)(tile.row0 + row) * out_ld + col] = facc[i][r] * s_rw[row];
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(facc[i][r] * s_rw[row]), ryb,
+                                                (uint32_t)((row * out_ld + col) * 4), 0, SC1);
+      }
+    }
+  }
+  if constexpr (!GU) {
+    // Combine (engine.rs:317-338). Once every wave's rows are stored, each
+    // row of the tile counts itself in on its token's counter for this
+    // column slice; the row whose count completes the token's top_k rows
+    // belongs to the workgroup that sums them. It resets the counter, so
+    // every launch leaves the counters at zero.
+    WAIT_VMCNT(0);
+    int *s_tok = (int *)(smem + NSLOT * MOE_SLOT + BM * 4);  // [BM] tokens this workgroup completes
+    int *s_sl = s_tok + BM;                                  // [BM][8] their slot rows (top_k <= 8)
+    int *s_n = s_sl + BM * 8;
+    if (threadIdx.x == 0) *s_n = 0;
+    __syncthreads();
+    const int n_cs = (N + 32 * NW - 1) / (32 * NW), cs = n0 / (32 * NW);
+    const int top_k = cmb.top_k;
+    const bool staged = top_k <= 8;
+    for (int row = threadIdx.x; row < tile.rows; row += NW * 64) {
+      const int t = cmb.tok[tile.row0 + row];
+      unsigned *c = cmb.cnt + (int64_t)t * n_cs + cs;
+      if (atomicAdd(c, 1u) == (unsigned)top_k - 1) {
+        atomicExch(c, 0u);
+        const int idx = atomicAdd(s_n, 1);
+        s_tok[idx] = t;
+        if (staged)
+          for (int j = 0; j < top_k; ++j) s_sl[idx * 8 + j] = cmb.slot[(int64_t)t * top_k + j];
+      }
+    }
+    __syncthreads();
+    // y[t] (+)= Σ_j yb[slot j of t] over the token's rows in ascending
+    // expert id: 4 columns per thread, 8·NW threads per row, U rows per
+    // thread at a time with every row load issued before the first add (the
+    // completing workgroups are the last ones to run, so their loads are
+    // the launch's tail).
+    constexpr int TPR = 8 * NW, NT = NW * 64, RPI = NT / TPR, U = 4;
+    const int n_last = *s_n;
+    const int c = n0 + 4 * ((int)threadIdx.x % TPR);
+    const int sub = (int)threadIdx.x / TPR;
+    const rsrc_t rall = make_rsrc(out, a_rows * out_ld * 4);
+    if (c < N) {
+      if (staged) {
+        // Loads past the token's top_k or past the last row read zeros
+        // (offsets outside the buffer) rather than sitting under a branch,
+        // which would serialise them.
+        const rsrc_t ry = make_rsrc(cmb.y, (int64_t)cmb.n_tok * N * 4);
+        for (int i0 = 0; i0 < n_last; i0 += U * RPI) {
+          floatx4 v[U][8], y0[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int idx = i0 + u * RPI + sub;
+            const bool ok = idx < n_last;
+            const int ic = ok ? idx : 0;
+            const intx4 sa = *(const intx4 *)(s_sl + ic * 8), sb = *(const intx4 *)(s_sl + ic * 8 + 4);
+            const int tk = s_tok[ic];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int sv = j < 4 ? sa[j & 3] : sb[j & 3];
+              const uint32_t off = (ok && j < top_k) ? (uint32_t)((sv * out_ld + c) * 4) : OOB_OFFSET;
+              v[u][j] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rall, off, 0, SC1));
+            }
+            const uint32_t yoff = (ok && cmb.accumulate) ? (uint32_t)((tk * N + c) * 4) : OOB_OFFSET;
+            y0[u] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ry, yoff, 0, 0));
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            floatx4 acc = y0[u];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (j < top_k)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = acc[e] + v[u][j][e];
+            const int idx = i0 + u * RPI + sub;
+            if (idx < n_last) *(floatx4 *)(cmb.y + (int64_t)s_tok[idx] * N + c) = acc;
+          }
+        }
+      } else {
+        for (int idx = sub; idx < n_last; idx += RPI) {
+          const int t = s_tok[idx];
+          const int32_t *sl = cmb.slot + (int64_t)t * top_k;
+          float *yr = cmb.y + (int64_t)t * N + c;
+          floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+          if (cmb.accumulate) acc = *(const floatx4 *)yr;
+          for (int j0 = 0; j0 < top_k; j0 += 8) {
+            const int nj = min(8, top_k - j0);
+            floatx4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (j < nj)
+                v[j] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rall, (uint32_t)((sl[j0 + j] * out_ld + c) * 4), 0, SC1));
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (j < nj)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = acc[e] + v[j][e];
+          }
+          *(floatx4 *)yr = acc;
+        }
       }
     }
   }
@@ -364,11 +478,23 @@ __global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
     const int32_t *__restrict__ tok, int64_t a_rows, const MoeTile *__restrict__ tiles, int n_col_tiles,
     const int8_t *__restrict__ W, const float *__restrict__ WS, int64_t w_stride_e,
     int64_t ws_stride_e, int ws_stride, int N, int K, const float *__restrict__ row_w,
-    float *__restrict__ out, int out_ld) {
+    float *__restrict__ out, int out_ld, MoeCombine cmb) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  // Consecutive logical indices (the column slices of one tile) share an XCD
-  // and so the tile's token rows in that XCD's L2.
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  // The column slices of one tile run on one XCD and share the tile's token
+  // rows in its L2. gate|up: consecutive tiles on one XCD. down: tile t on
+  // XCD t mod 8 (the dispatcher hands workgroup b to XCD b mod 8), so the
+  // last tiles, whose workgroups complete most tokens and run the combine's
+  // reads, are spread over all XCDs; the grid is padded to whole rounds of 8
+  // tiles and the padding workgroups exit at once.
+  int L;
+  if constexpr (GU) {
+    L = xcd_remap(blockIdx.x, gridDim.x);
+  } else {
+    const int j = blockIdx.x / 8;
+    const int t = blockIdx.x % 8 + 8 * (j / n_col_tiles);
+    if (t >= cmb.n_tiles) return;
+    L = t * n_col_tiles + j % n_col_tiles;
+  }
   const MoeTile tile = tiles[L / n_col_tiles];
   const int n0 = (L % n_col_tiles) * 32 * NW;
   const int8_t *We = W + (int64_t)tile.expert * w_stride_e;
@@ -380,7 +506,7 @@ __global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
     constexpr int NRB = decltype(u_c)::value + 1;
     if (nrb == NRB || (NRB == BM / 32 && nrb > NRB))
       moe_body<GU, NW, PD, BM, NRB>(A, AS, as_stride, tok, a_rows, tile, We, WSe, ws_stride, N, K, n0,
-                                    row_w, out, out_ld, smem);
+                                    row_w, out, out_ld, cmb, smem);
   });
 }
 
@@ -389,7 +515,8 @@ static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, int as_stride
                                  int64_t a_rows, const MoeTile *tiles, int n_tiles,
                                  const int8_t *w, const float *ws, int64_t w_stride_e,
                                  int64_t ws_stride_e, int ws_stride, int N, int K,
-                                 const float *row_w, float *out, int out_ld, hipStream_t st) {
+                                 const float *row_w, float *out, int out_ld, const MoeCombine &cmb,
+                                 hipStream_t st) {
   constexpr int smem = moe_smem<PD, BM>();
   static_assert(smem <= 160 * 1024, "LDS per workgroup");
   auto kern = moe_q8_kernel<GU, NW, PD, BM>;
@@ -401,9 +528,12 @@ static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, int as_stride
     attr_set = true;
   }
   const int n_col = (N + 32 * NW - 1) / (32 * NW);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(n_tiles * n_col)), dim3(NW * 64), smem, st, A, AS, as_stride,
+  const int grid = GU ? n_tiles * n_col : (n_tiles + 7) / 8 * 8 * n_col;
+  MoeCombine c = cmb;
+  c.n_tiles = n_tiles;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * 64), smem, st, A, AS, as_stride,
                      tok, a_rows, tiles, n_col, w, ws, w_stride_e, ws_stride_e, ws_stride, N, K,
-                     row_w, out, out_ld);
+                     row_w, out, out_ld, c);
   return hipGetLastError();
 }
 
@@ -424,10 +554,11 @@ static hipError_t launch_moe(int tile_rows, const int8_t *A, const float *AS, in
                              int64_t a_rows,
                              const MoeTile *tiles, int n_tiles, const int8_t *w, const float *ws,
                              int64_t w_stride_e, int64_t ws_stride_e, int ws_stride, int N,
-                             int K, const float *row_w, float *out, int out_ld, hipStream_t st) {
+                             int K, const float *row_w, float *out, int out_ld, const MoeCombine &cmb,
+                             hipStream_t st) {
   if (n_tiles == 0) return hipSuccess;
 #define RK_MOE_ARGS A, AS, as_stride, tok, a_rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e, ws_stride, N, K, \
-                    row_w, out, out_ld, st
+                    row_w, out, out_ld, cmb, st
   if (tile_rows == 64) {
     switch (rk_knob("RK_MOE_TILE", 0)) {
       case 2: return launch_moe_cfg<GU, 4, 2, 64>(RK_MOE_ARGS);
@@ -449,47 +580,17 @@ static hipError_t launch_moe(int tile_rows, const int8_t *A, const float *AS, in
 hipError_t rk_launch_moe_gemm_gu(int tile_rows, const int8_t *xq, const float *xs, int xs_stride,
                                  const int32_t *tok, int64_t s, const MoeTile *tiles, int n_tiles, const int8_t *w,
                                  const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
-                                 int ws_stride, int N, int K, float *act, int num_cus,
-                                 hipStream_t st) {
-  (void)num_cus;
+                                 int ws_stride, int N, int K, float *act, hipStream_t st) {
   return launch_moe<true>(tile_rows, xq, xs, xs_stride, tok, s, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
-                          ws_stride, N, K, nullptr, act, N / 2, st);
+                          ws_stride, N, K, nullptr, act, N / 2, MoeCombine{}, st);
 }
 
 hipError_t rk_launch_moe_gemm_down(int tile_rows, const int8_t *aq, const float *as, int as_stride, int64_t rows,
                                    const MoeTile *tiles, int n_tiles, const int8_t *w,
                                    const float *ws, int64_t w_stride_e, int64_t ws_stride_e,
                                    int ws_stride, int N, int K, const float *row_w, float *yb,
-                                   int num_cus, hipStream_t st) {
-  (void)num_cus;
+                                   const MoeCombine &cmb, hipStream_t st) {
   return launch_moe<false>(tile_rows, aq, as, as_stride, nullptr, rows, tiles, n_tiles, w, ws, w_stride_e, ws_stride_e,
-                           ws_stride, N, K, row_w, yb, N, st);
+                           ws_stride, N, K, row_w, yb, N, cmb, st);
 }
 
-// y[t] = Σ_j yb[slot_rows[t, j]] with the slots of a token already sorted by
-// ascending expert id (the deterministic order of combine, engine.rs:317-338).
-__global__ void moe_combine_kernel(const float *__restrict__ yb,
-                                   const int32_t *__restrict__ slot_rows, int top_k, int64_t h,
-                                   float *__restrict__ y) {
-  const int64_t t = blockIdx.y;
-  const int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
-  if (c >= h) return;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < top_k; ++j) {
-    const int64_t row = slot_rows[t * top_k + j];
-    const floatx4 v = *(const floatx4 *)(yb + row * h + c);
-    acc[0] += v[0];
-    acc[1] += v[1];
-    acc[2] += v[2];
-    acc[3] += v[3];
-  }
-  *(floatx4 *)(y + t * h + c) = acc;
-}
-
-hipError_t rk_launch_moe_combine(const float *yb, const int32_t *slot_rows, int64_t s, int top_k,
-                                 int64_t h, float *y, hipStream_t st) {
-  if (s == 0) return hipSuccess;
-  dim3 grid((unsigned)((h / 4 + 255) / 256), (unsigned)s);
-  hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, st, yb, slot_rows, top_k, h, y);
-  return hipGetLastError();
-}

@@ -162,11 +162,18 @@ unsafe extern "C" {
         id: WeightId, x: *const f32, s: i64, top_k: c_int, ids: *const u32, wts: *const f32,
         y: *mut f32, stream: Stream
     ) -> c_int;
+    pub fn rk_moe_experts_acc_dev(
+        id: WeightId, x: *const f32, s: i64, top_k: c_int, ids: *const u32, wts: *const f32,
+        y: *mut f32, stream: Stream
+    ) -> c_int;
     pub fn rk_moe_plan_create(
         id: WeightId, s: i64, top_k: c_int, ids: *const u32, wts: *const f32,
         plan: *mut *mut c_void
     ) -> c_int;
     pub fn rk_moe_experts_planned_dev(
+        id: WeightId, plan: *const c_void, x: *const f32, y: *mut f32, stream: Stream
+    ) -> c_int;
+    pub fn rk_moe_experts_planned_acc_dev(
         id: WeightId, plan: *const c_void, x: *const f32, y: *mut f32, stream: Stream
     ) -> c_int;
     pub fn rk_moe_plan_destroy(plan: *mut c_void) -> c_int;

@@ -350,11 +350,23 @@ int rk_pack_moe_f32(const float *gate, const float *up, const float *down,
  * product is Σ_b (a_s[m,b]·w_s[n,b])·P_b over the Q8_0 blocks b with exact
  * int32 P_b, accumulated in f32. silu(v) = v / (1 + e^-v) (src/clef/model.rs:
  * 491-493). ids/wts are host arrays (bucketing runs on the host,
- * engine.rs:284-313); y f32 [s, hidden] is overwritten. RK_E_SHAPE when
- * s·hidden or s·top_k·inter reaches 2^31. */
+ * engine.rs:284-313); y f32 [s, hidden] is overwritten with the sum. The
+ * combine runs inside the down-projection launch: the workgroup that
+ * completes a token's top_k rows (an arrival count per token and column
+ * slice) sums them in ascending expert id, so y does not depend on the
+ * order the workgroups finish in. RK_E_SHAPE when s·hidden or
+ * s·top_k·inter reaches 2^31, or s·top_k·hidden·4 bytes reaches 2^31. */
 int rk_moe_experts_dev(rk_weight_id id, const float *x, int64_t s, int top_k,
                        const uint32_t *ids, const float *wts, float *y,
                        rk_stream stream);
+/* The same, accumulating onto y: y[t] = ((y[t] + out_e0) + out_e1) + …
+ * with e0 < e1 < … the token's experts, the reference's combine onto the
+ * residual it already holds (`let mut y = hid; … *a += b`, src/clef/model.rs:
+ * 606-614; combine, src/clef/engine.rs:317-338). x and y may be the same
+ * buffer (x is read before y is written). */
+int rk_moe_experts_acc_dev(rk_weight_id id, const float *x, int64_t s, int top_k,
+                           const uint32_t *ids, const float *wts, float *y,
+                           rk_stream stream);
 
 /* The same split in two: bucket once (host), keep the per-expert row lists,
  * tiles and combine order on the device, then run the expert FFN for any x
@@ -364,6 +376,8 @@ int rk_moe_plan_create(rk_weight_id id, int64_t s, int top_k,
                        const uint32_t *ids, const float *wts, void **plan);
 int rk_moe_experts_planned_dev(rk_weight_id id, const void *plan,
                                const float *x, float *y, rk_stream stream);
+int rk_moe_experts_planned_acc_dev(rk_weight_id id, const void *plan,
+                                   const float *x, float *y, rk_stream stream);
 int rk_moe_plan_destroy(void *plan);
 /* First stage alone, for exactness checks: act f32 [rows, inter] =
  * silu(gate·x)·(up·x) for every bucket row, rows ordered by expert id and,

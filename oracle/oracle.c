@@ -525,11 +525,13 @@ void orc_clef_silu_mul(const float *g, const float *u, float *out, int64_t n) {
  * src/clef/engine.rs:317-338). A token's row is quantized the same way in
  * every expert it is routed to, so quantizing x once per token is the same.
  * Weights: gate/up codes [E][I][H] with scales [E][I][H/32], down codes
- * [E][H][I] with scales [E][H][I/32]. y [s][H]. */
+ * [E][H][I] with scales [E][H][I/32]. y [s][H]: overwritten with the sum, or,
+ * with accumulate, holding the residual the expert outputs are added onto
+ * (`let mut y = hid; … *a += b`, src/clef/model.rs:606-614). */
 void orc_moe_experts(const float *x, int64_t s, int64_t H, int64_t I, int E, int top_k,
                      const uint32_t *ids, const float *wts, const int8_t *gq, const float *gs,
                      const int8_t *uq, const float *us, const int8_t *dq, const float *ds,
-                     float *y, int threads) {
+                     float *y, int accumulate, int threads) {
   int8_t *xq = (int8_t *)malloc((size_t)s * H);
   float *xs = (float *)malloc(sizeof(float) * (size_t)s * (H / 32));
   orc_quantize_rows(x, s, H, 32, xq, xs, threads);
@@ -572,7 +574,8 @@ void orc_moe_experts(const float *x, int64_t s, int64_t H, int64_t I, int E, int
         order[b] = order[b - 1];
         order[b - 1] = tmp;
       }
-    for (int64_t c = 0; c < H; ++c) y[t * H + c] = 0.f;
+    if (!accumulate)
+      for (int64_t c = 0; c < H; ++c) y[t * H + c] = 0.f;
     for (int j = 0; j < top_k; ++j) {
       const float *yr = yslot + (t * top_k + order[j]) * H;
       for (int64_t c = 0; c < H; ++c) y[t * H + c] += yr[c];

@@ -35,7 +35,7 @@ _SIG = {
     "orc_attention_ref": (None, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _i]),
     "orc_attention_flex": (None, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _i]),
     "orc_route": (None, [_p, _i64, _i, _i, _i, _p, _p]),
-    "orc_moe_experts": (None, [_p, _i64, _i64, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i]),
+    "orc_moe_experts": (None, [_p, _i64, _i64, _i64, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i]),
     "orc_gelu_tanh": (_f, [_f]),
     "orc_gelu_mul": (None, [_p, _p, _p, _i64]),
     "orc_silu_mul": (None, [_p, _p, _p, _i64]),
@@ -237,20 +237,22 @@ def route(logits, top_k, norm_topk=True):
     return ids, wts
 
 
-def moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds, threads=None):
+def moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds, threads=None, y0=None):
     """W8A8 expert FFN + combine, activations (x and silu·up) quantized per row
     per 32-value group as the reference's expert workers do. gq/uq [E,I,H]
-    int8, gs/us [E,I,H/32] f32, dq [E,H,I] int8, ds [E,H,I/32] f32 → y [s,H]."""
+    int8, gs/us [E,I,H/32] f32, dq [E,H,I] int8, ds [E,H,I/32] f32 → y [s,H].
+    With y0 (the residual [s,H]) the expert outputs are added onto it in
+    ascending expert id, as the reference's layer does (model.rs:606-614)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     s, H = x.shape
     E, I = gq.shape[0], gq.shape[1]
     top_k = ids.shape[1]
-    y = np.empty((s, H), dtype=np.float32)
+    y = np.empty((s, H), dtype=np.float32) if y0 is None else np.array(y0, dtype=np.float32, copy=True)
     arrs = [np.ascontiguousarray(a, dtype=t) for a, t in
             ((ids, np.uint32), (wts, np.float32), (gq, np.int8), (gs, np.float32), (uq, np.int8),
              (us, np.float32), (dq, np.int8), (ds, np.float32))]
     lib().orc_moe_experts(_ptr(x), s, H, I, E, top_k, *[_ptr(a) for a in arrs], _ptr(y),
-                          threads or threads_default())
+                          int(y0 is not None), threads or threads_default())
     return y
 
 

@@ -83,6 +83,20 @@ def run(rk, wid, x, ids, wts):
     return act, y
 
 
+def run_acc(rk, wid, x, ids, wts, resid):
+    """y = resid with the expert rows added in ascending expert id (the one-shot
+    accumulating entry)."""
+    lib = rk.lib()
+    S, H = x.shape
+    ids = np.ascontiguousarray(ids, np.uint32)
+    wts = np.ascontiguousarray(wts, np.float32)
+    dx, dy = rk.DeviceBuffer.from_array(x), rk.DeviceBuffer.from_array(np.ascontiguousarray(resid, np.float32))
+    assert lib.rk_moe_experts_acc_dev(int(wid), dx.ptr, S, ids.shape[1], ids.ctypes.data, wts.ctypes.data,
+                                      dy.ptr, None) == 0, lib.rk_last_error()
+    rk.synchronize()
+    return dy.download((S, H), np.float32)
+
+
 _INTER = {}
 
 
@@ -104,15 +118,16 @@ def oracle_stage1(orc, x, ex, e_rows, t_rows):
     return act
 
 
-def oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S):
-    """Down projection of the given act rows (quantized per 32-group), router weight, combine."""
+def oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S, y0=None):
+    """Down projection of the given act rows (quantized per 32-group), router weight,
+    combine (onto y0, the residual, when given: src/clef/model.rs:606-614)."""
     H = ex["dq"].shape[1]
     aq, a_s = orc.quantize_rows(act, 32)
     yb = np.empty((len(e_rows), H), np.float32)
     for e in np.unique(e_rows):
         sel = np.nonzero(e_rows == e)[0]
         yb[sel] = orc.emu_matmul_gw(aq[sel], a_s[sel], 32, ex["dq"][e], ex["ds"][e], 32) * w_rows[sel][:, None]
-    y = np.zeros((S, H), np.float32)
+    y = np.zeros((S, H), np.float32) if y0 is None else np.array(y0, np.float32, copy=True)
     for row in range(len(e_rows)):  # bucket rows are expert-ascending: the combine order
         y[t_rows[row]] += yb[row]
     return y
@@ -147,6 +162,14 @@ def check_pipeline(rk, orc, S, H, I, E, ids, wts, seed):
     # end to end against the full oracle pipeline
     y_ref = orc.moe_experts(x, ids, wts, ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"])
     assert orc.cosine(y, y_ref) >= COS_MIN and orc.max_rel(y, y_ref) <= REL_MAX
+    # accumulating onto a residual: the same expert rows added onto it in
+    # ascending expert id, the reference's summation order
+    resid = synth.normal_f32(seed + 20_000, (S, H), 0.5)
+    y_acc = run_acc(rk, wid, x, ids, wts, resid)
+    y_acc_ref2 = oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S, y0=resid)
+    assert np.abs(y_acc - y_acc_ref2).max() <= 2e-5 * np.abs(y_acc_ref2).max()
+    y_acc_ref = orc.moe_experts(x, ids, wts, ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"], y0=resid)
+    assert orc.cosine(y_acc, y_acc_ref) >= COS_MIN and orc.max_rel(y_acc, y_acc_ref) <= REL_MAX
     return y
 
 
@@ -226,6 +249,97 @@ def test_moe_config5_full_size(rk, orc):
     assert orc.cosine(y[toks], y_ref) >= COS_MIN and orc.max_rel(y[toks], y_ref) <= REL_MAX
 
 
+
+def test_moe_config5_benched_stack(rk, orc):
+    # The stack the benchmark times: N(0, 0.02²) weights from the benchmark's
+    # seeds, quantized to Q8_0 on the device by rk_pack_moe_f32; x and the
+    # router logits from the same seeds; 1024 tokens, top-8 of 128 experts.
+    # 64 tokens spread over the sequence are checked end to end, overwriting
+    # and accumulating onto a residual, and stage 1 of their bucket rows
+    # within f32 rounding.
+    c = synth.MOE
+    S, H, I, E, K = c["s"], c["hidden"], c["inter"], c["experts"], c["top_k"]
+    seeds = synth.SEEDS["moe"]
+    note(f"MoE benched stack S={S} H={H} I={I} E={E} top{K}: generating weights")
+    gate = synth.normal_f32(seeds[2], (E, I, H), 0.02)
+    up = synth.normal_f32(seeds[3], (E, I, H), 0.02)
+    down = synth.normal_f32(seeds[4], (E, H, I), 0.02)
+    wid = rk.pack_moe_f32(gate, up, down)
+    _INTER[int(wid)] = I
+    ex = {}
+    for name, w in (("g", gate), ("u", up), ("d", down)):
+        q, d = orc.q8_0_quantize(w.reshape(-1, w.shape[-1]))
+        ex[name + "q"] = q.reshape(w.shape)
+        ex[name + "s"] = d.view(np.float16).astype(np.float32).reshape(w.shape[:-1] + (w.shape[-1] // 32,))
+    del gate, up, down
+    x = synth.normal_f32(seeds[0], (S, H))
+    ids, wts = rk.moe_route(synth.normal_f32(seeds[1], (S, E)), K)
+    note("MoE benched stack: running")
+    act, y = run(rk, wid, x, ids, wts)
+    e_rows, t_rows, s_rows = bucket_order(ids)
+    toks = np.linspace(0, S - 1, 64).round().astype(np.int64)
+    assert len(np.unique(ids[toks])) > 100
+    rows = np.nonzero(np.isin(t_rows, toks))[0]
+    act_ref = oracle_stage1(orc, x, ex, e_rows[rows], t_rows[rows])
+    check_stage1(act[rows], act_ref)
+    args = (ex["gq"], ex["gs"], ex["uq"], ex["us"], ex["dq"], ex["ds"])
+    y_ref = orc.moe_experts(x[toks], ids[toks], wts[toks], *args)
+    note(f"MoE benched stack: cosine {orc.cosine(y[toks], y_ref):.7f} max-rel {orc.max_rel(y[toks], y_ref):.2e}")
+    assert orc.cosine(y[toks], y_ref) >= COS_MIN and orc.max_rel(y[toks], y_ref) <= REL_MAX
+    resid = synth.normal_f32(seeds[0] + 1, (S, H))
+    y_acc = run_acc(rk, wid, x, ids, wts, resid)
+    y_acc_ref = orc.moe_experts(x[toks], ids[toks], wts[toks], *args, y0=resid[toks])
+    assert orc.cosine(y_acc[toks], y_acc_ref) >= COS_MIN and orc.max_rel(y_acc[toks], y_acc_ref) <= REL_MAX
+
+
+def test_moe_accumulate_planned_twice_and_onto_zeros(rk, orc):
+    # The planned accumulating entry adds onto whatever y holds: twice in a row
+    # gives ((r + Σ) + Σ) in expert order; onto zeros it is the overwriting
+    # entry bit for bit; repeated overwriting calls are bit-identical (the
+    # combine's order does not depend on which workgroup finishes last).
+    S, H, I, E, K = 300, 256, 128, 8, 8
+    ex = make_experts(orc, 1500, E, H, I)
+    wid = rk.pack_moe_q8_0(*ex["blocks"], E, H, I)
+    _INTER[int(wid)] = I
+    r = np.random.default_rng(77)
+    x = r.standard_normal((S, H)).astype(np.float32)
+    ids, wts = rk.moe_route(r.standard_normal((S, E)).astype(np.float32), K)
+    ids, wts = np.ascontiguousarray(ids), np.ascontiguousarray(wts)
+    act, y = run(rk, wid, x, ids, wts)
+    lib = rk.lib()
+    plan = ctypes.c_void_p()
+    assert lib.rk_moe_plan_create(int(wid), S, K, ids.ctypes.data, wts.ctypes.data, ctypes.byref(plan)) == 0
+    dx = rk.DeviceBuffer.from_array(x)
+    resid = r.standard_normal((S, H)).astype(np.float32)
+    dy = rk.DeviceBuffer.from_array(resid)
+    for _ in range(2):
+        assert lib.rk_moe_experts_planned_acc_dev(int(wid), plan, dx.ptr, dy.ptr, None) == 0, lib.rk_last_error()
+    dz = rk.DeviceBuffer.from_array(np.zeros((S, H), np.float32))
+    assert lib.rk_moe_experts_planned_acc_dev(int(wid), plan, dx.ptr, dz.ptr, None) == 0
+    outs = []
+    for _ in range(3):
+        d = rk.DeviceBuffer(S * H * 4)
+        assert lib.rk_moe_experts_planned_dev(int(wid), plan, dx.ptr, d.ptr, None) == 0
+        outs.append(d)
+    rk.synchronize()
+    assert lib.rk_moe_plan_destroy(plan) == 0
+    for d in outs:
+        assert (d.download((S, H), np.float32) == y).all()
+    assert (dz.download((S, H), np.float32) == y).all()
+    e_rows, t_rows, s_rows = bucket_order(ids)
+    w_rows = wts[t_rows, s_rows]
+    once = oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S, y0=resid)
+    twice = oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S, y0=once)
+    got = dy.download((S, H), np.float32)
+    assert np.abs(got - twice).max() <= 2e-5 * np.abs(twice).max()
+    # x and y may be one buffer: x is quantized before y is written
+    dxy = rk.DeviceBuffer.from_array(x)
+    assert lib.rk_moe_experts_acc_dev(int(wid), dxy.ptr, S, K, ids.ctypes.data, wts.ctypes.data, dxy.ptr,
+                                      None) == 0
+    rk.synchronize()
+    xy = oracle_stage2(orc, act, ex, e_rows, t_rows, w_rows, S, y0=x)
+    assert np.abs(dxy.download((S, H), np.float32) - xy).max() <= 2e-5 * np.abs(xy).max()
+
 def test_pack_moe_f32_equals_pack_from_blocks(rk, orc):
     # The device Q8_0 quantizer gives the stack the GGUF blocks give.
     note("pack_moe_f32 vs pack_moe_q8_0")
@@ -245,9 +359,9 @@ def test_pack_moe_f32_equals_pack_from_blocks(rk, orc):
     assert (a1 == a2).all() and (y1 == y2).all()
 
 
-# Every workgroup shape of the expert kernels: tiles of ≤128 rows (RK_MOE_ROWS
-# 128; RK_MOE_TILE 0-3: 4 or 8 waves, 2-4 stages ahead) and of ≤64 rows (the
-# default; RK_MOE_TILE 0, 2, 3, 4: 4, 2, 3, 5 stages ahead); tiles of 1..4 row
+# Every workgroup shape of the expert kernels: tiles of ≤128 rows (the default,
+# RK_MOE_ROWS 128; RK_MOE_TILE 0-3: 4 or 8 waves, 2-4 stages ahead) and of ≤64
+# rows (RK_MOE_TILE 0, 2, 3, 4: 4, 2, 3, 5 stages ahead); tiles of 1..4 row
 # blocks, several tiles per expert, and a gate|up width (2·inter = 128) below
 # one 256-column slice.
 @pytest.mark.parametrize("rows,tile", [(128, 0), (128, 1), (128, 2), (128, 3), (64, 0), (64, 2), (64, 3),

@@ -455,6 +455,34 @@ def test_moe_experts_is_the_composition_of_the_pinned_primitives(orc):
     assert (y == want).all()
 
 
+
+def test_moe_experts_accumulates_onto_the_residual_in_expert_order(orc):
+    # The reference's layer starts from the residual and adds each expert's
+    # rows in ascending expert id (`let mut y = hid; … *a += b`,
+    # src/clef/model.rs:606-614): y = ((hid + out_e0) + out_e1) + … . Each
+    # slot's output alone comes from a top-1 call (0 + out = out exactly);
+    # composing them onto hid in numpy in expert order must give the same
+    # bits (a sum formed first and then added to hid rounds differently).
+    r = _rng(24)
+    s, H, I, E, K = 11, 64, 64, 6, 3
+    x = r.standard_normal((s, H)).astype(np.float32)
+    hid = (r.standard_normal((s, H)) * 3).astype(np.float32)
+    ids, wts = orc.route(r.standard_normal((s, E)).astype(np.float32), K)
+    (gq, gs), (uq, us), (dq, ds) = (_moe_q8(orc, (r.standard_normal(shp) * 0.1).astype(np.float32))
+                                    for shp in ((E, I, H), (E, I, H), (E, H, I)))
+    y = orc.moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds, y0=hid)
+    want = hid.copy()
+    for j in np.argsort(ids, axis=1, kind="stable").T:
+        sel = (np.arange(s), j)
+        one = orc.moe_experts(x, ids[sel][:, None], wts[sel][:, None], gq, gs, uq, us, dq, ds)
+        want = want + one
+    assert (y == want).all()
+    summed_first = hid + orc.moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds)
+    assert (y != summed_first).any()
+    # onto zeros, the accumulating form is the overwriting one
+    z = orc.moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds, y0=np.zeros((s, H), np.float32))
+    assert (z == orc.moe_experts(x, ids, wts, gq, gs, uq, us, dq, ds)).all()
+
 def test_clef_silu_mul_formula(orc):
     # src/clef/model.rs:491-493: silu(v) = v / (1 + e^-v), then ·u, in f32;
     # against the same expression in f64 (within f32 rounding), its limits,
