@@ -224,21 +224,30 @@ __device__ __forceinline__ void moe_body(
       // The reference's rounding sequence, acc + fl(fl(a_s·w_s)·P): gate|up
       // results feed the next quantizer, where a one-ulp difference could move
       // an int8 code, so they are computed exactly as the reference does.
+      // Written as four passes over the 16 elements, so that no step waits on
+      // the one before it for the same element.
 #pragma clang fp contract(off)
+      float pf[16], sc[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int bits = ires[P][r];  // element to a scalar before the bit cast
-        const float pf = __int_as_float(bits) - MOE_BIAS;  // P, exact
-        const float sc = as[r] * d;
-        facc[I][r] = facc[I][r] + sc * pf;
+        pf[r] = __int_as_float(bits) - MOE_BIAS;  // P, exact
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] = as[r] * d;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pf[r] = sc[r] * pf[r];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) facc[I][r] = facc[I][r] + pf[r];
     } else {
+      float y[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int bits = ires[P][r];
-        const float y = __builtin_fmaf(__int_as_float(bits), d, c);
-        facc[I][r] = __builtin_fmaf(y, as[r], facc[I][r]);
+        y[r] = __builtin_fmaf(__int_as_float(bits), d, c);
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) facc[I][r] = __builtin_fmaf(y[r], as[r], facc[I][r]);
     }
   };
 
