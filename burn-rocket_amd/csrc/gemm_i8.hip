@@ -468,6 +468,10 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
 
   intx4 af[2][TM], bf[2][TN];
   float dsc[2][TN];
+  // The column's 4 weight scales of a stage, read with one 16-byte LDS read
+  // at the stage's first block (4-byte reads at a 16-byte lane stride would
+  // conflict on the banks).
+  floatx4 wsq[TN];
   auto load_frags = [&](auto buf_c, auto slot_c, auto b_c) {
     constexpr int buf = decltype(buf_c)::value, slot = decltype(slot_c)::value,
                   b = decltype(b_c)::value;
@@ -477,7 +481,10 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       bf[buf][j] = *(const intx4 *)(base + b_off[b] + j * 32 * ROWB);
-      if constexpr (SCALED) dsc[buf][j] = *(const float *)(base + s_off + j * 32 * 16 + b * 4);
+      if constexpr (SCALED) {
+        if constexpr (b == 0) wsq[j] = *(const floatx4 *)(base + s_off + j * 32 * 16);
+        dsc[buf][j] = wsq[j][b];
+      }
     }
   };
 
