@@ -408,6 +408,32 @@ def extra_w8a8_forms(layers, iters):
     return out
 
 
+def extra_host_path(layers, steps):
+    """The W8A8 pair through the host-buffer entry (`rk_matmul`: f32 activations
+    from and f32 outputs to ordinary pageable host arrays, quantized per 32-group
+    on the GPU, as an unchanged Flex caller's `matmul` reaches it, ext.rs:1505-1554),
+    PCIe included: the rate a caller that keeps its tensors in host memory sees."""
+    xs = [np.ascontiguousarray(L["dx"].download((L["m"], L["k"]), np.float32)) for L in layers]
+    ys = [np.empty((L["m"], L["n"]), np.float32) for L in layers]
+    lib = rk.lib()
+
+    def step():
+        for L, x, y in zip(layers, xs, ys):
+            call(lib.rk_matmul(int(L["wid"]), x.ctypes.data, L["m"], L["k"], y.ctypes.data), "rk_matmul")
+
+    for _ in range(3):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]
+    ops = 2 * 2.0 * m * h * i
+    moved = sum(x.nbytes + y.nbytes for x, y in zip(xs, ys))
+    return {"ms": ms, "tops": ops / ms / 1e9, "pcie_gbps": moved / ms / 1e6, "bytes_per_step": moved,
+            "what": "rk_matmul on the up and down Q8_0 weights, host f32 in and out (group-32 activations)"}
+
+
 def extra_glue(iters):
     """The HBM-bound ops around the GEMMs at the Qwen3-0.6B layer shape (S=3633, hidden 1024,
     MLP 3072, 16 q / 8 kv heads of 128): bytes are one read of each input and one write of
@@ -714,7 +740,8 @@ def main():
                         ("vision_layer_2394", lambda: extra_vision(50)),
                         ("gemma_attention_d256_2587", lambda: extra_gemma_attention(50)),
                         ("moe_30b_a3b_1024", lambda: extra_moe(20)),
-                        ("glue_qwen3_3633", lambda: extra_glue(50))):
+                        ("glue_qwen3_3633", lambda: extra_glue(50)),
+                        ("host_path_w8a8_pair_3633", lambda: extra_host_path(layers, 10))):
             log(f"extra {key}")
             extras[key] = fn()
 

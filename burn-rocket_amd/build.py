@@ -18,7 +18,7 @@ BUILD = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libburn_rocket_amd.so")
 SOURCES = ["gemm_f16.hip", "gemm_i8.hip", "misc.hip", "norm.hip", "attention.hip", "moe.hip", "noalloc.hip",
-           "engine.cpp"]
+           "engine.cpp", "stage.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

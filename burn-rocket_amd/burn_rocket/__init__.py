@@ -41,6 +41,7 @@ SIGNATURES = {
     "rk_mem_stats": (_i, [_p]),
     "rk_trim_scratch_to": (_i, [_u64]),
     "rk_clear_scratch": (_i, []),
+    "rk_trim_scratch": (_i, []),
     "rk_pack": (_i, [_p, _i64, _i64, _p]),
     "rk_pack_f16": (_i, [_p, _i64, _i64, _p]),
     "rk_pack_seg": (_i, [_p, _p, _i, _i64, _p]),
@@ -53,6 +54,9 @@ SIGNATURES = {
     "rk_weight_info": (_i, [_u64, _p, _p, _p, _p]),
     "rk_matmul": (_i, [_u64, _p, _i64, _i64, _p]),
     "rk_matmul_f16_dev": (_i, [_u64, _p, _i64, _i64, _p, _p]),
+    "rk_matmul_f16": (_i, [_u64, _p, _i64, _i64, _p]),
+    "rk_matmul_i8_gw": (_i, [_u64, _p, _p, _p, _i64, _i64, _p]),
+    "rk_matmul_i8": (_i, [_u64, _p, _i64, _i64, _p]),
     "rk_pack_f16_glu": (_i, [_p, _p, _i64, _i64, _p]),
     "rk_matmul_f16_glu_dev": (_i, [_u64, _p, _i64, _i64, _i, _p, _i, _p]),
     "rk_quantize_rows_dev": (_i, [_p, _i64, _i64, _i64, _p, _p, _p]),
@@ -64,6 +68,7 @@ SIGNATURES = {
     "rk_attention_dev": (_i, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p]),
     "rk_attention_dev_noalloc": (_i, [_p, _p, _p, _i64, _i64, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p]),
     "rk_flash_attn_f16": (_i, [_i64, _i64, _i, _i, _i, _i, _f, _f, _i, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "rk_flash_attn_f16_masked": (_i, [_i64, _i64, _i, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p]),
     "rk_moe_route": (_i, [_p, _i64, _i, _i, _i, _p, _p]),
     "rk_pack_moe_q8_0": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
     "rk_pack_moe_f32": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
@@ -227,19 +232,23 @@ def pack_i8(w, group):
 
 
 def pack_i8_codes(codes, scales, group):
+    """Pre-quantized group-wise weight; scales None keeps the codes alone
+    (`I8Context::pack_weight_gw`: the scales come with each matmul_gw)."""
     codes = np.ascontiguousarray(codes, dtype=np.int8)
-    scales = _f32(scales)
+    scales = None if scales is None else _f32(scales)
     n, k = codes.shape
     out = ctypes.c_uint64()
-    _check(_lib.rk_pack_i8_codes(_ptr(codes), _ptr(scales), n, k, group, ctypes.byref(out)),
+    _check(_lib.rk_pack_i8_codes(_ptr(codes), None if scales is None else _ptr(scales), n, k, group,
+                                 ctypes.byref(out)),
            "rocket_i8_weights_pack_gw", 0, k, n)
     return WeightId(out.value)
 
 
-def rewrite_i8(wid, codes, scales):
+def rewrite_i8(wid, codes, scales=None):
     codes = np.ascontiguousarray(codes, dtype=np.int8)
-    scales = _f32(scales)
-    _check(_lib.rk_rewrite_i8(int(wid), _ptr(codes), _ptr(scales)), "rocket_i8_rewrite_gw")
+    scales = None if scales is None else _f32(scales)
+    _check(_lib.rk_rewrite_i8(int(wid), _ptr(codes), None if scales is None else _ptr(scales)),
+           "rocket_i8_rewrite_gw")
 
 
 def pack_q8_0(blocks, n, k):
@@ -535,8 +544,11 @@ class Stats(ctypes.Structure):
 
 
 class MemStats(ctypes.Structure):
+    """`rk_mem_stats_t`: resident weights, device scratch (all / attention),
+    page-locked staging bytes (`MemStats`, lib.rs:44-84)."""
     _fields_ = [("weights_bytes", ctypes.c_uint64), ("scratch_bytes", ctypes.c_uint64),
-                ("n_weights", ctypes.c_uint64)]
+                ("n_weights", ctypes.c_uint64), ("attention_bytes", ctypes.c_uint64),
+                ("host_bytes", ctypes.c_uint64), ("n_scratch", ctypes.c_uint64)]
 
 
 def stats():
@@ -561,6 +573,202 @@ def trim_scratch_to(budget):
 
 def clear_scratch():
     _check(_lib.rk_clear_scratch(), "clear_scratch")
+
+
+def trim_scratch():
+    """`burn_rocket::trim_scratch` (ext.rs:254-265): scratch unused since the
+    previous trim is freed; the just-used set stays."""
+    _check(_lib.rk_trim_scratch(), "trim_scratch")
+
+
+def _shape_error(op, what):
+    raise RocketError(op, RK_E_SHAPE, f"{op} failed: unsupported shape (rc=-1): {what}")
+
+
+def _u16(a):
+    return np.ascontiguousarray(a, dtype=np.float16).view(np.uint16)
+
+
+class RocketWeight:
+    """A resident fp16 weight of a `RocketCtx` (`RocketWeight`, lib.rs:268-270)."""
+
+    def __init__(self, wid, m, k, n):
+        self.id, self.m, self.k, self.n = WeightId(wid), m, k, n
+
+    def bytes(self):
+        return self.n * self.k * 2
+
+
+class RocketCtx:
+    """`burn_rocket::RocketCtx` (lib.rs:203-266): resident fp16 weights and
+    `C[M, N] = A[M, K]·B[N, K]ᵀ` on host fp16 buffers. `nthreads` (the NPU
+    worker count) has no counterpart; scratch belongs to the one engine."""
+
+    def __init__(self, nthreads=1):
+        init(0)
+
+    def pack_weight(self, m, k, n, b):
+        b = _u16(b)
+        if b.size != n * k:
+            _shape_error("rocket_weights_pack", "b must be [N, K]")
+        out = ctypes.c_uint64()
+        _check(_lib.rk_pack_f16(_ptr(b), n, k, ctypes.byref(out)), "rocket_weights_pack", m, k, n)
+        return RocketWeight(out.value, m, k, n)
+
+    def pack_weight_seg(self, m, k, parts):
+        parts = [np.ascontiguousarray(p, dtype=np.float16).ravel() for p in parts]
+        if any(p.size % k for p in parts):
+            _shape_error("rocket_weights_pack_seg", "every part must be [n_i, K]")
+        return self.pack_weight(m, k, sum(p.size // k for p in parts), np.concatenate(parts))
+
+    def matmul_prepacked(self, m, k, n, a, c, w):
+        """Fills the fp16 array `c` [M·N] in place."""
+        a = _u16(a)
+        if k != w.k or n != w.n or a.size != m * k or c.size != m * n or c.dtype != np.float16:
+            _shape_error("rocket_matmul_fp16", "A [M, K], C [M, N] fp16 and the weight's K, N")
+        out = np.empty(m * n, dtype=np.uint16)
+        _check(_lib.rk_matmul_f16(int(w.id), _ptr(a), m, k, _ptr(out)), "rocket_matmul_fp16", m, k, n)
+        c.reshape(-1)[:] = out.view(np.float16)
+
+    def trim_scratch(self):
+        trim_scratch()
+
+    def trim_to_budget(self, budget):
+        trim_scratch_to(budget)
+
+    def scratch_bytes(self):
+        ms = mem_stats()
+        return ms.scratch_bytes - ms.attention_bytes + ms.host_bytes
+
+    def clear_scratch(self):
+        clear_scratch()
+
+
+class RocketFaCtx:
+    """`burn_rocket::RocketFaCtx` (lib.rs:285-330): head-major fp16 masked GQA
+    attention, q [H][T][head_dim], k [KV][Nk][head_dim], v [KV][dv][Nk],
+    out [H][T][dv], optional additive fp16 mask [T][Nk] of 0 / -inf."""
+
+    def __init__(self, nthreads=1):
+        init(0)
+
+    def flash_attn(self, n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, q, k, v, mask, out):
+        q16, k16, v16 = _u16(q), _u16(k), _u16(v)
+        if (q16.size != n_head * n_tokens * head_dim or k16.size != n_kv_heads * n_kv * head_dim
+                or v16.size != n_kv_heads * dv * n_kv or out.size != n_head * n_tokens * dv
+                or out.dtype != np.float16):
+            _shape_error("rocket_flash_attn_fp16_ctx", "q, k, v or out do not match the shapes")
+        m16 = None
+        if mask is not None:
+            m16 = _u16(mask)
+            if m16.size != n_tokens * n_kv:
+                _shape_error("rocket_flash_attn_fp16_ctx", "mask must be [n_tokens, n_kv]")
+        o = np.empty(n_head * n_tokens * dv, dtype=np.uint16)
+        _check(_lib.rk_flash_attn_f16_masked(n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, float(scale),
+                                             float(softcap), None if m16 is None else _ptr(m16), _ptr(q16),
+                                             _ptr(k16), _ptr(v16), _ptr(o)),
+               "rocket_flash_attn_fp16_ctx", n_tokens, n_kv, head_dim)
+        out.reshape(-1)[:] = o.view(np.float16)
+
+    def mem_stats(self):
+        ms = mem_stats()
+        return {"bo_bytes": ms.attention_bytes, "host_bytes": 0}
+
+    def trim_scratch(self):
+        trim_scratch()
+
+    def clear_scratch(self):
+        clear_scratch()
+
+
+class I8Weight:
+    """A resident int8 weight of an `I8Context` (int8.rs:112-136): codes only;
+    group 0 is the per-channel layout."""
+
+    def __init__(self, wid, m, k, n, group):
+        self.id, self.m, self.k, self.n, self.group = WeightId(wid), m, k, n, group
+
+    def shape(self):
+        return self.m, self.k, self.n, self.group
+
+    def bytes(self):
+        return self.n * self.k
+
+
+class I8Context:
+    """`rocket_npu::matmul::I8Context` (int8.rs:236-676) as Clef's expert
+    workers use it (src/clef/engine_npu.rs:75-207): resident int8 codes whose
+    scales come with each call, exact int32 products and the group-wise
+    scaled product on host buffers. The worker count and core base of the NPU
+    have no counterpart."""
+
+    def __init__(self, nthreads=1, core_base=0):
+        init(0)
+
+    @classmethod
+    def new_at(cls, nthreads, core_base):
+        return cls(nthreads, core_base)
+
+    def _pack(self, m, k, n, b, group, op):
+        b = np.ascontiguousarray(b, dtype=np.int8)
+        if b.size != n * k:
+            _shape_error(op, "b must be [N, K] int8")
+        out = ctypes.c_uint64()
+        _check(_lib.rk_pack_i8_codes(_ptr(b), None, n, k, group if group else k, ctypes.byref(out)), op, m, k, n)
+        return I8Weight(out.value, m, k, n, group)
+
+    def pack_weight(self, m, k, n, b):
+        return self._pack(m, k, n, b, 0, "rocket_i8_weights_pack")
+
+    def pack_weight_gw(self, m, k, n, b, group):
+        if group == 0:
+            _shape_error("int8/pack/group", "group-wise weight needs group > 0")
+        return self._pack(m, k, n, b, group, "rocket_i8_weights_pack_gw")
+
+    def rewrite_weight(self, w, b):
+        b = np.ascontiguousarray(b, dtype=np.int8)
+        if b.size != w.n * w.k:
+            _shape_error("int8/rewrite", "b must be [N, K] int8")
+        _check(_lib.rk_rewrite_i8(int(w.id), _ptr(b), None), "int8/rewrite")
+
+    def rewrite_weight_gw(self, w, b):
+        if w.group == 0:
+            _shape_error("int8/rewrite/group", "the weight is per-channel")
+        self.rewrite_weight(w, b)
+
+    def matmul(self, m, k, n, a, c, w):
+        """Raw int32 product into `c` [M·N] (int32)."""
+        a = np.ascontiguousarray(a, dtype=np.int8)
+        if k != w.k or n != w.n or w.group != 0:
+            _shape_error("int8/matmul/shape", "per-channel weight of this K, N")
+        if a.size != m * k or c.size != m * n or c.dtype != np.int32:
+            _shape_error("int8/matmul/buffers", "a [M, K] int8, c [M, N] int32")
+        out = np.empty(m * n, dtype=np.int32)
+        _check(_lib.rk_matmul_i8(int(w.id), _ptr(a), m, k, _ptr(out)), "rocket_matmul_int8_prepacked", m, k, n)
+        c.reshape(-1)[:] = out
+
+    def matmul_gw(self, m, k, n, a, a_scale, b_scale, cf, w):
+        """`cf[m, n] = Σ_g a_scale[m,g]·b_scale[n,g]·(A_g·B_gᵀ)` into `cf` (f32)."""
+        a = np.ascontiguousarray(a, dtype=np.int8)
+        if k != w.k or n != w.n or w.group == 0:
+            _shape_error("int8/matmul/shape", "group-wise weight of this K, N")
+        if a.size != m * k or cf.size != m * n or cf.dtype != np.float32:
+            _shape_error("int8/matmul/buffers", "a [M, K] int8, cf [M, N] f32")
+        ng = k // w.group
+        a_scale, b_scale = _f32(a_scale), _f32(b_scale)
+        if a_scale.size != m * ng or b_scale.size != n * ng:
+            _shape_error("int8/matmul/scales", "a_scale [M, K/group], b_scale [N, K/group]")
+        out = np.empty(m * n, dtype=np.float32)
+        _check(_lib.rk_matmul_i8_gw(int(w.id), _ptr(a), _ptr(a_scale), _ptr(b_scale), m, k, _ptr(out)),
+               "rocket_matmul_int8_prepacked_gw", m, k, n)
+        cf.reshape(-1)[:] = out
+
+    def scratch_bytes(self):
+        ms = mem_stats()
+        return ms.scratch_bytes - ms.attention_bytes + ms.host_bytes
+
+    def clear_scratch(self):
+        clear_scratch()
 
 
 # ------------------------------------------------------------- device buffers

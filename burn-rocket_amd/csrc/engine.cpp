@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -20,6 +21,7 @@
 
 #include "../../include/burn_rocket_amd.h"
 #include "kernels.hpp"
+#include "stage.hpp"
 
 static inline int64_t round_up_i(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
 
@@ -80,6 +82,7 @@ struct DevBuf {
   hipStream_t ev_stream = nullptr;  // stream of the last call that used the buffer
   bool recorded = false;            // ev marks the end of that call's work
   bool pending = false;             // that call ran on a library stream; ev not recorded yet
+  uint64_t epoch = 0;               // Engine::epoch at its last use
 };
 
 struct Weight {
@@ -111,7 +114,8 @@ struct Engine {
   std::unordered_map<std::string, DevBuf> scratch;
   double convert_s = 0, device_s = 0;
   uint64_t calls = 0;
-  hipEvent_t tev[4] = {};  // HostTimer marks
+  rkstage::HostStage stage;  // page-locked staging of the host-buffer entries
+  uint64_t epoch = 0;        // rk_trim_scratch: scratch not used since the last trim goes
 };
 
 std::mutex g_mu;
@@ -185,28 +189,52 @@ int scratch(CallScope &c, const char *name, size_t bytes, void **out, bool *fres
     HIP_TRY(hipStreamWaitEvent(c.st, b.ev, 0), "scratch");
   }
   if (std::find(c.used.begin(), c.used.end(), &b) == c.used.end()) c.used.push_back(&b);
+  b.epoch = g_eng->epoch;
   *out = b.p;
   return RK_OK;
 }
 
-// Conversion / device time of a host-buffer entry point, from four events on
-// its stream: [0, 1) uploads and conversions in, [1, 2) the kernels of the op,
-// [2, 3) conversions out and downloads (the split of `T_CONVERT_US` /
-// `T_NPU_US`, ext.rs:165-200). finish() runs after the stream has synchronized.
-struct HostTimer {
-  hipStream_t st;
-  explicit HostTimer(hipStream_t s) : st(s) {}
-  void mark(int i) { (void)hipEventRecord(g_eng->tev[i], st); }
-  void finish() {
-    float t[3] = {0.f, 0.f, 0.f};
-    for (int i = 0; i < 3; ++i)
-      if (hipEventElapsedTime(&t[i], g_eng->tev[i], g_eng->tev[i + 1]) != hipSuccess) t[i] = 0.f;
-    g_eng->convert_s += 1e-3 * (t[0] + t[2]);
-    g_eng->device_s += 1e-3 * t[1];
-  }
-};
-
 hipStream_t pick(rk_stream s) { return s ? (hipStream_t)s : g_eng->stream; }
+
+// A host-buffer op through the page-locked staging (stage.hpp): `ins` go up,
+// compute(r0, r1) enqueues the kernels of rows [r0, r1) on cs.st and returns
+// an RK status, `outs` come down; row-sliced transfers move chunk by chunk so
+// that uploads, kernels and downloads overlap. The op's kernel time (events
+// around each chunk's kernels) is device_s; the rest of its wall time
+// (copies and waits not hidden behind kernels) is convert_s.
+int staged(CallScope &cs, const std::vector<rkstage::Xfer> &ins,
+           const std::vector<rkstage::Xfer> &outs, int64_t rows, int64_t chunk_rows,
+           const std::function<int(int64_t, int64_t)> &compute, const char *op) {
+  HIP_TRY(g_eng->stage.setup(g_eng->device), op);
+  const auto t0 = Clock::now();
+  int crc = RK_OK;
+  bool ok = true;
+  float kms = 0.f;
+  const hipError_t e = g_eng->stage.run(
+      cs.st, ins, outs, rows, chunk_rows,
+      [&](int64_t r0, int64_t r1) {
+        crc = compute(r0, r1);
+        return crc == RK_OK;
+      },
+      &ok, &kms);
+  if (e != hipSuccess) return hip_fail(e, op);
+  if (!ok) return crc;
+  const double wall = secs(t0, Clock::now());
+  g_eng->device_s += 1e-3 * kms;
+  g_eng->convert_s += std::max(0.0, wall - 1e-3 * kms);
+  return RK_OK;
+}
+
+// Rows per staged chunk: about 8 MiB of the larger of a row's input and
+// output bytes, at most HostStage::kMaxChunks chunks, a multiple of 16 rows
+// (so every chunk's device offsets keep 64-byte alignment).
+int64_t stage_chunk_rows(int64_t rows, size_t in_row, size_t out_row) {
+  const size_t per = std::max<size_t>({in_row, out_row, (size_t)1});
+  int64_t c = std::max<int64_t>(1, (int64_t)(((size_t)8 << 20) / per));
+  c = std::max<int64_t>(c, (rows + rkstage::HostStage::kMaxChunks - 1) / rkstage::HostStage::kMaxChunks);
+  c = round_up_i(c, 16);
+  return std::min<int64_t>(c, std::max<int64_t>(rows, 1));
+}
 
 Weight *find(uint64_t id) {
   auto it = g_eng->weights.find(id);
@@ -291,7 +319,6 @@ extern "C" int rk_init(int device) {
   e->device = device;
   e->num_cus = prop.multiProcessorCount;
   hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
-  for (int i = 0; i < 4 && err == hipSuccess; ++i) err = hipEventCreate(&e->tev[i]);
   if (err != hipSuccess) {
     delete e;
     return hip_fail(err, "rk_init");
@@ -326,11 +353,31 @@ extern "C" int rk_mem_stats(rk_mem_stats_t *out) {
   RK_TRY(ensure("rk_mem_stats"));
   out->weights_bytes = 0;
   out->scratch_bytes = 0;
+  out->attention_bytes = 0;
   out->n_weights = g_eng->weights.size();
+  out->n_scratch = g_eng->scratch.size();
   for (auto &kv : g_eng->weights) out->weights_bytes += kv.second.bytes;
-  for (auto &kv : g_eng->scratch) out->scratch_bytes += kv.second.bytes;
+  for (auto &kv : g_eng->scratch) {
+    out->scratch_bytes += kv.second.bytes;
+    if (kv.first.rfind("at", 0) == 0 || kv.first.rfind("fa_", 0) == 0)
+      out->attention_bytes += kv.second.bytes;
+  }
+  out->host_bytes = g_eng->stage.pinned_bytes();
   return RK_OK;
 }
+
+namespace {
+// Frees one named scratch buffer once its last use has completed.
+int free_scratch(const std::string &name, const char *op) {
+  DevBuf &b = g_eng->scratch[name];
+  RK_TRY(fence_point(b, op));
+  if (b.recorded) HIP_TRY(hipEventSynchronize(b.ev), op);
+  HIP_TRY(hipFree(b.p), op);
+  if (b.ev) (void)hipEventDestroy(b.ev);
+  g_eng->scratch.erase(name);
+  return RK_OK;
+}
+}  // namespace
 
 extern "C" int rk_trim_scratch_to(uint64_t budget) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -345,14 +392,25 @@ extern "C" int rk_trim_scratch_to(uint64_t budget) {
   std::sort(order.rbegin(), order.rend());
   for (auto &o : order) {
     if (total <= budget) break;
-    DevBuf &b = g_eng->scratch[o.second];
-    RK_TRY(fence_point(b, "rk_trim_scratch_to"));
-    if (b.recorded) HIP_TRY(hipEventSynchronize(b.ev), "rk_trim_scratch_to");
-    HIP_TRY(hipFree(b.p), "rk_trim_scratch_to");
-    if (b.ev) (void)hipEventDestroy(b.ev);
-    total -= b.bytes;
-    g_eng->scratch.erase(o.second);
+    RK_TRY(free_scratch(o.second, "rk_trim_scratch_to"));
+    total -= o.first;
   }
+  // A zero budget also returns the page-locked staging slots.
+  if (budget == 0) HIP_TRY(g_eng->stage.release(), "rk_trim_scratch_to");
+  return RK_OK;
+}
+
+extern "C" int rk_trim_scratch(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  RK_TRY(ensure("rk_trim_scratch"));
+  // Scratch no call has used since the previous rk_trim_scratch goes; what
+  // the calls in between used stays (the reference keeps the just-used shape
+  // set, ext.rs:254-265).
+  std::vector<std::string> old;
+  for (auto &kv : g_eng->scratch)
+    if (kv.second.epoch < g_eng->epoch) old.push_back(kv.first);
+  for (auto &name : old) RK_TRY(free_scratch(name, "rk_trim_scratch"));
+  g_eng->epoch++;
   return RK_OK;
 }
 
@@ -430,11 +488,14 @@ int pack_i8_host(const int8_t *codes, const std::vector<float> &block_scales, in
   return RK_OK;
 }
 
+// Per-group scales [n, K/group] repeated over each group's 32-value blocks;
+// null scales (codes packed alone, I8Context::pack_weight_gw) give zeros.
 std::vector<float> expand_group_scales(const float *scales, int64_t n, int64_t k, int64_t group) {
   const int64_t kb = k / 32, ng = k / group, gb = group / 32;
-  std::vector<float> blk((size_t)n * kb);
-  for (int64_t r = 0; r < n; ++r)
-    for (int64_t b = 0; b < kb; ++b) blk[r * kb + b] = scales[r * ng + b / gb];
+  std::vector<float> blk((size_t)n * kb, 0.f);
+  if (scales)
+    for (int64_t r = 0; r < n; ++r)
+      for (int64_t b = 0; b < kb; ++b) blk[r * kb + b] = scales[r * ng + b / gb];
   return blk;
 }
 }  // namespace
@@ -482,9 +543,11 @@ extern "C" int rk_rewrite_i8(rk_weight_id id, const int8_t *codes, const float *
   RK_TRY(ensure("rk_rewrite_i8"));
   Weight *w = find(id);
   if (!w || w->kind != RK_WEIGHT_I8)
-    return fail(RK_E_RANGE, "rk_rewrite_i8", "id is not a resident int8 weight");
+    return fail(RK_E_SHAPE, "rk_rewrite_i8", "id is not a resident int8 weight");
   HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_rewrite_i8");
   HIP_TRY(hipMemcpy(w->codes, codes, (size_t)w->n * w->k, hipMemcpyHostToDevice), "rk_rewrite_i8");
+  // Null scales: the codes alone (I8Context::rewrite_weight_gw, int8.rs:482-526).
+  if (!scales) return RK_OK;
   std::vector<float> blk = expand_group_scales(scales, w->n, w->k, w->group);
   const int64_t kb = w->k / 32;
   std::vector<float> pad((size_t)w->n * w->ws_stride, 0.f);
@@ -662,7 +725,7 @@ extern "C" int rk_pack_qat(const int8_t *codes, const float *w_scale, int64_t n,
   RK_TRY(ensure("rk_pack_qat"));
   if (n <= 0 || k <= 0 || k % 32 != 0)
     return fail(RK_E_SHAPE, "rk_pack_qat", "the int8 path needs K % 32 == 0");
-  if (!(in_scale >= 0.f)) return fail(RK_E_RANGE, "rk_pack_qat", "input scale must not be negative");
+  if (!(in_scale >= 0.f)) return fail(RK_E_SHAPE, "rk_pack_qat", "input scale must not be negative");
   Weight w;
   w.kind = RK_WEIGHT_QAT;
   w.n = n;
@@ -684,7 +747,7 @@ extern "C" int rk_weight_info(rk_weight_id id, int *kind, int64_t *n, int64_t *k
   std::lock_guard<std::mutex> lk(g_mu);
   RK_TRY(ensure("rk_weight_info"));
   Weight *w = find(id);
-  if (!w) return fail(RK_E_RANGE, "rk_weight_info", "weight id is not packed");
+  if (!w) return fail(RK_E_SHAPE, "rk_weight_info", "weight id is not packed");
   *kind = w->moe ? 0 : w->kind;
   *n = w->n;
   *k = w->k;
@@ -720,7 +783,7 @@ int launch_i8(const Weight &w, const int8_t *a, const float *as, int as_stride, 
 }
 
 int check_m(int64_t m, int64_t k, const Weight *w, const char *op) {
-  if (!w) return fail(RK_E_RANGE, op, "weight id is not packed");
+  if (!w) return fail(RK_E_SHAPE, op, "weight id is not packed");
   if (m <= 0) return fail(RK_E_SHAPE, op, "M must be positive");
   if (m > INT32_MAX) return fail(RK_E_SHAPE, op, "M too large");
   if (k != w->k)
@@ -740,54 +803,163 @@ extern "C" int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, 
     return fail(RK_E_UNSUPPORTED, "rk_matmul", "gate|up weight: use rk_matmul_w8a8_glu_dev");
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
-  HostTimer tm(st);
   const int64_t n = w->n;
-  void *x32, *y32;
-  RK_TRY(scratch(cs, "mm_x32", (size_t)m * k * 4, &x32));
-  RK_TRY(scratch(cs, "mm_y32", (size_t)m * n * 4, &y32));
-  tm.mark(0);
-  HIP_TRY(hipMemcpyAsync(x32, x, (size_t)m * k * 4, hipMemcpyHostToDevice, st), "rk_matmul");
+  float *x32, *y32;
+  RK_TRY(scratch(cs, "mm_x32", (size_t)m * k * 4, (void **)&x32));
+  RK_TRY(scratch(cs, "mm_y32", (size_t)m * n * 4, (void **)&y32));
+  // Row chunks of x go up, are converted or quantized and multiplied, and
+  // their rows of y come down while the next chunk is in flight.
+  std::function<int(int64_t, int64_t)> compute;
   if (w->kind == RK_WEIGHT_F16) {
-    void *a16, *c16;
-    RK_TRY(scratch(cs, "mm_a16", (size_t)m * k * 2, &a16));
-    RK_TRY(scratch(cs, "mm_c16", (size_t)m * n * 2, &c16));
-    HIP_TRY(rk_launch_f32_to_f16((const float *)x32, a16, m * k, st), "rk_matmul");
-    tm.mark(1);
-    HIP_TRY(rk_launch_gemm_f16(a16, w->codes, c16, (int)m, (int)n, (int)k, g_eng->num_cus, st),
-            "rk_matmul_fp16");
-    tm.mark(2);
-    HIP_TRY(rk_launch_f16_to_f32(c16, (float *)y32, m * n, st), "rk_matmul");
+    uint16_t *a16, *c16;
+    RK_TRY(scratch(cs, "mm_a16", (size_t)m * k * 2, (void **)&a16));
+    RK_TRY(scratch(cs, "mm_c16", (size_t)m * n * 2, (void **)&c16));
+    compute = [=](int64_t r0, int64_t r1) {
+      const int64_t rows = r1 - r0;
+      HIP_TRY(rk_launch_f32_to_f16(x32 + r0 * k, a16 + r0 * k, rows * k, st), "rk_matmul");
+      HIP_TRY(rk_launch_gemm_f16(a16 + r0 * k, w->codes, c16 + r0 * n, (int)rows, (int)n, (int)k,
+                                 g_eng->num_cus, st),
+              "rk_matmul_fp16");
+      HIP_TRY(rk_launch_f16_to_f32(c16 + r0 * n, y32 + r0 * n, rows * n, st), "rk_matmul");
+      return RK_OK;
+    };
   } else if (w->kind == RK_WEIGHT_I8) {
-    void *q, *s;
+    int8_t *q;
+    float *s;
     const int64_t ng = k / w->group;
-    RK_TRY(scratch(cs, "mm_q", (size_t)m * k, &q));
-    RK_TRY(scratch(cs, "mm_s", (size_t)m * ng * 4, &s));
-    HIP_TRY(rk_launch_quantize_rows((const float *)x32, m, k, w->group, (int8_t *)q, (float *)s, st),
-            "rk_matmul");
-    tm.mark(1);
-    RK_TRY(launch_i8(*w, (const int8_t *)q, (const float *)s, (int)ng, (int)(w->group / 32),
-                     I8_PER_GROUP, false, m, y32, st, "rk_matmul_int8_gw"));
-    tm.mark(2);
+    RK_TRY(scratch(cs, "mm_q", (size_t)m * k, (void **)&q));
+    RK_TRY(scratch(cs, "mm_s", (size_t)m * ng * 4, (void **)&s));
+    compute = [=](int64_t r0, int64_t r1) {
+      HIP_TRY(rk_launch_quantize_rows(x32 + r0 * k, r1 - r0, k, w->group, q + r0 * k, s + r0 * ng, st),
+              "rk_matmul");
+      return launch_i8(*w, q + r0 * k, s + r0 * ng, (int)ng, (int)(w->group / 32), I8_PER_GROUP, false,
+                       r1 - r0, y32 + r0 * n, st, "rk_matmul_int8_gw");
+    };
   } else {  // QAT
-    void *q, *rs, *acc;
-    RK_TRY(scratch(cs, "mm_q", (size_t)m * k, &q));
-    RK_TRY(scratch(cs, "mm_rs", (size_t)m * 4, &rs));
-    RK_TRY(scratch(cs, "mm_acc", (size_t)m * n * 4, &acc));
-    HIP_TRY(rk_launch_quantize_static((const float *)x32, m, k, w->in_scale, (int8_t *)q,
-                                      (float *)rs, st),
-            "rk_matmul");
-    tm.mark(1);
-    RK_TRY(launch_i8(*w, (const int8_t *)q, nullptr, 0, 1, I8_RAW, false, m, acc, st,
-                     "rk_matmul_int8_qat"));
-    HIP_TRY(rk_launch_qat_epilogue((const int32_t *)acc, (const float *)rs, w->scales, m, n,
-                                   w->out_scale, (float *)y32, st),
-            "rk_matmul");
-    tm.mark(2);
+    int8_t *q;
+    float *rs;
+    int32_t *acc;
+    RK_TRY(scratch(cs, "mm_q", (size_t)m * k, (void **)&q));
+    RK_TRY(scratch(cs, "mm_rs", (size_t)m * 4, (void **)&rs));
+    RK_TRY(scratch(cs, "mm_acc", (size_t)m * n * 4, (void **)&acc));
+    compute = [=](int64_t r0, int64_t r1) {
+      const int64_t rows = r1 - r0;
+      HIP_TRY(rk_launch_quantize_static(x32 + r0 * k, rows, k, w->in_scale, q + r0 * k, rs + r0, st),
+              "rk_matmul");
+      RK_TRY(launch_i8(*w, q + r0 * k, nullptr, 0, 1, I8_RAW, false, rows, acc + r0 * n, st,
+                       "rk_matmul_int8_qat"));
+      HIP_TRY(rk_launch_qat_epilogue(acc + r0 * n, rs + r0, w->scales, rows, n, w->out_scale,
+                                     y32 + r0 * n, st),
+              "rk_matmul");
+      return RK_OK;
+    };
   }
-  HIP_TRY(hipMemcpyAsync(y, y32, (size_t)m * n * 4, hipMemcpyDeviceToHost, st), "rk_matmul");
-  tm.mark(3);
-  HIP_TRY(hipStreamSynchronize(st), "rk_matmul");
-  tm.finish();
+  RK_TRY(staged(cs, {{x, nullptr, x32, (size_t)k * 4, 0}}, {{nullptr, y, y32, (size_t)n * 4, 0}}, m,
+                stage_chunk_rows(m, (size_t)k * 4, (size_t)n * 4), compute, "rk_matmul"));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+// RocketCtx::matmul_prepacked (crates/burn-rocket/src/lib.rs:244-254) on host
+// fp16 buffers.
+extern "C" int rk_matmul_f16(rk_weight_id id, const uint16_t *a, int64_t m, int64_t k, uint16_t *c) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_matmul_f16";
+  RK_TRY(ensure(op));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, op));
+  if (w->kind != RK_WEIGHT_F16 || w->moe || w->glu_n > 0)
+    return fail(RK_E_UNSUPPORTED, op, "weight is not a plain fp16 weight");
+  if (!a || !c) return fail(RK_E_SHAPE, op, "null buffer");
+  hipStream_t st = g_eng->stream;
+  CallScope cs(st);
+  const int64_t n = w->n;
+  uint16_t *a16, *c16;
+  RK_TRY(scratch(cs, "mm_a16", (size_t)m * k * 2, (void **)&a16));
+  RK_TRY(scratch(cs, "mm_c16", (size_t)m * n * 2, (void **)&c16));
+  auto compute = [&](int64_t r0, int64_t r1) {
+    HIP_TRY(rk_launch_gemm_f16(a16 + r0 * k, w->codes, c16 + r0 * n, (int)(r1 - r0), (int)n, (int)k,
+                               g_eng->num_cus, st),
+            "rocket_matmul_fp16");
+    return RK_OK;
+  };
+  RK_TRY(staged(cs, {{a, nullptr, a16, (size_t)k * 2, 0}}, {{nullptr, c, c16, (size_t)n * 2, 0}}, m,
+                stage_chunk_rows(m, (size_t)k * 2, (size_t)n * 2), compute, op));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+// I8Context::matmul_gw (crates/rocket-npu/src/matmul/int8.rs:644-676) on host
+// buffers, as Clef's gw_matmul calls it (src/clef/engine_npu.rs:75-110).
+extern "C" int rk_matmul_i8_gw(rk_weight_id id, const int8_t *a, const float *a_scale,
+                               const float *b_scale, int64_t m, int64_t k, float *cf) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_matmul_i8_gw";
+  RK_TRY(ensure(op));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, op));
+  if (w->kind != RK_WEIGHT_I8 || w->moe || w->glu_n > 0)
+    return fail(RK_E_UNSUPPORTED, op, "weight is not a group-wise int8 weight");
+  if (!a || !a_scale || !cf) return fail(RK_E_SHAPE, op, "null buffer");
+  hipStream_t st = g_eng->stream;
+  CallScope cs(st);
+  const int64_t n = w->n, ng = k / w->group;
+  int8_t *q;
+  float *s, *y32, *ws = w->scales;
+  RK_TRY(scratch(cs, "mm_q", (size_t)m * k, (void **)&q));
+  RK_TRY(scratch(cs, "mm_s", (size_t)m * ng * 4, (void **)&s));
+  RK_TRY(scratch(cs, "mm_y32", (size_t)m * n * 4, (void **)&y32));
+  // This call's weight scales [N, K/group], widened to the resident layout
+  // (one f32 per 32-value block, rows padded to ws_stride) and uploaded with
+  // the first chunk.
+  std::vector<float> wpad;
+  if (b_scale) {
+    RK_TRY(scratch(cs, "mm_ws", (size_t)n * w->ws_stride * 4, (void **)&ws));
+    const std::vector<float> blk = expand_group_scales(b_scale, n, k, w->group);
+    const int64_t kb = k / 32;
+    wpad.assign((size_t)n * w->ws_stride, 0.f);
+    for (int64_t r = 0; r < n; ++r)
+      std::memcpy(&wpad[(size_t)r * w->ws_stride], &blk[(size_t)r * kb], sizeof(float) * kb);
+  }
+  Weight wv = *w;
+  wv.scales = ws;
+  // The fold is the reference's (a_s·w_s)·P per group (int8.rs:663-667) for
+  // any scale values (no fp16-scale fold order).
+  wv.ws_f16 = false;
+  std::vector<rkstage::Xfer> ins = {{a, nullptr, q, (size_t)k, 0}, {a_scale, nullptr, s, (size_t)ng * 4, 0}};
+  if (b_scale) ins.push_back({wpad.data(), nullptr, ws, 0, wpad.size() * 4});
+  auto compute = [&](int64_t r0, int64_t r1) {
+    return launch_i8(wv, q + r0 * k, s + r0 * ng, (int)ng, (int)(w->group / 32), I8_PER_GROUP, false,
+                     r1 - r0, y32 + r0 * n, st, "rk_matmul_int8_gw");
+  };
+  RK_TRY(staged(cs, ins, {{nullptr, cf, y32, (size_t)n * 4, 0}}, m,
+                stage_chunk_rows(m, (size_t)k, (size_t)n * 4), compute, op));
+  g_eng->calls++;
+  return RK_OK;
+}
+
+// I8Context::matmul (int8.rs:606-640): raw int32 on host buffers.
+extern "C" int rk_matmul_i8(rk_weight_id id, const int8_t *a, int64_t m, int64_t k, int32_t *c) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_matmul_i8";
+  RK_TRY(ensure(op));
+  Weight *w = find(id);
+  RK_TRY(check_m(m, k, w, op));
+  if ((w->kind != RK_WEIGHT_I8 && w->kind != RK_WEIGHT_QAT) || w->moe || w->glu_n > 0)
+    return fail(RK_E_UNSUPPORTED, op, "weight is not int8");
+  if (!a || !c) return fail(RK_E_SHAPE, op, "null buffer");
+  hipStream_t st = g_eng->stream;
+  CallScope cs(st);
+  const int64_t n = w->n;
+  int8_t *q;
+  int32_t *acc;
+  RK_TRY(scratch(cs, "mm_q", (size_t)m * k, (void **)&q));
+  RK_TRY(scratch(cs, "mm_acc", (size_t)m * n * 4, (void **)&acc));
+  auto compute = [&](int64_t r0, int64_t r1) {
+    return launch_i8(*w, q + r0 * k, nullptr, 0, 1, I8_RAW, false, r1 - r0, acc + r0 * n, st, op);
+  };
+  RK_TRY(staged(cs, {{a, nullptr, q, (size_t)k, 0}}, {{nullptr, c, acc, (size_t)n * 4, 0}}, m,
+                stage_chunk_rows(m, (size_t)k, (size_t)n * 4), compute, op));
   g_eng->calls++;
   return RK_OK;
 }
@@ -1030,13 +1202,12 @@ int attn_run(const void *q, const void *k, const void *vt, void *out, int64_t n_
   return RK_OK;
 }
 
-// Token-major attention on device buffers: Vᵀ into scratch, then the kernel
-// (tm, when given, is marked between the two: the Vᵀ rewrite is layout work).
+// Token-major attention on device buffers: Vᵀ into scratch, then the kernel.
 int attn_dev_impl(CallScope &cs, const void *q, const void *k, const void *v, int64_t n_q,
                   int64_t n_kv, int n_head, int n_kv_heads, int head_dim, float scale,
                   float softcap, int mode, int64_t window, int64_t q0, int64_t k0, void *out,
                   const char *op, int64_t q_ts = 0, int64_t k_ts = 0, int64_t v_ts = 0,
-                  int64_t o_ts = 0, HostTimer *tm = nullptr) {
+                  int64_t o_ts = 0) {
   // Head dims of the reference's contract (head_dim % 32, attn/mod.rs:1443)
   // between the kernel widths (160, 192, 224) run zero-padded to 256 on
   // packed token-major operands: zero q/k columns leave the scores, zero V
@@ -1064,7 +1235,7 @@ int attn_dev_impl(CallScope &cs, const void *q, const void *k, const void *v, in
       HIP_TRY(hipMemcpy2DAsync(t.dst, w, t.src, hd, hd, t.rows, hipMemcpyDeviceToDevice, cs.st), op);
     }
     RK_TRY(attn_dev_impl(cs, qp, kp, vp, n_q, n_kv, n_head, n_kv_heads, pad_w, scale, softcap, mode,
-                         window, q0, k0, op_, op, 0, 0, 0, 0, tm));
+                         window, q0, k0, op_, op));
     HIP_TRY(hipMemcpy2DAsync(out, hd, op_, w, hd, (size_t)n_q * n_head, hipMemcpyDeviceToDevice, cs.st),
             op);
     return RK_OK;
@@ -1079,7 +1250,6 @@ int attn_dev_impl(CallScope &cs, const void *q, const void *k, const void *v, in
   HIP_TRY(rk_launch_v_transpose(v, v_ts ? v_ts : (int64_t)n_kv_heads * head_dim, head_dim,
                                 (int)n_kv, (int)n_kv_pad, n_kv_heads, head_dim, dvp, vt, cs.st),
           op);
-  if (tm) tm->mark(1);
   return attn_run(q, k, vt, out, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, head_dim, scale, softcap,
                   mode, window, q0, k0, false, cs.st, op, &cs, q_ts, k_ts, o_ts);
 }
@@ -1134,7 +1304,7 @@ extern "C" int rk_attention_dev_noalloc(const void *q, const void *k, const void
   const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
   const int64_t need = (int64_t)n_kv_heads * dvp * n_kv_pad * 2;
   if (need > (int64_t)RK_NOALLOC_SCRATCH_BYTES)
-    return fail(RK_E_RANGE, op,
+    return fail(RK_E_NOMEM, op,
                 "V transposed needs " + std::to_string(need) + " bytes, above the " +
                     std::to_string(RK_NOALLOC_SCRATCH_BYTES) + "-byte static scratch");
   void *vt = rk_noalloc_scratch(g_eng->device);
@@ -1151,51 +1321,65 @@ extern "C" int rk_attention_dev_noalloc(const void *q, const void *k, const void
   return RK_OK;
 }
 
+namespace {
+// RK_E_RANGE after a host-buffer attention whose q or k held a value that
+// fp16 cannot represent: the reference converts them to fp16 the same way
+// and answers Status::Range when a score leaves fp16's range
+// (attn/softmax.rs:462-475, attn/mod.rs:1044-1046). The scores themselves are
+// f32 here and cannot saturate.
+int range_flag(const int *flag, const char *op) {
+  int h = 0;
+  HIP_TRY(hipMemcpy(&h, flag, 4, hipMemcpyDeviceToHost), op);
+  if (h) return fail(RK_E_RANGE, op, "q or k holds a value outside the fp16 range");
+  return RK_OK;
+}
+}  // namespace
+
 extern "C" int rk_attention(const float *q, const float *k, const float *v, int64_t n_q,
                             int64_t n_kv, int n_head, int n_kv_heads, int head_dim, float scale,
                             float softcap, int mask_mode, int64_t window, int64_t q0, int64_t k0,
                             float *out) {
   std::lock_guard<std::mutex> lk(g_mu);
-  RK_TRY(ensure("rk_attention"));
+  const char *op = "rk_attention";
+  RK_TRY(ensure(op));
   int mode = mask_mode;
-  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, "rk_attention", true));
+  RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, head_dim, &mode, window, op, true));
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
-  HostTimer tm(st);
   const size_t nq_el = (size_t)n_q * n_head * head_dim;
   const size_t nk_el = (size_t)n_kv * n_kv_heads * head_dim;
-  void *f32buf, *q16, *k16, *v16, *o16;
-  RK_TRY(scratch(cs, "at_f32", std::max(nq_el, nk_el) * 4, &f32buf));
+  float *f32;
+  void *q16, *k16, *v16, *o16;
+  int *flag;
+  RK_TRY(scratch(cs, "at_f32", (nq_el + 2 * nk_el) * 4, (void **)&f32));
   RK_TRY(scratch(cs, "at_q16", nq_el * 2, &q16));
   RK_TRY(scratch(cs, "at_k16", nk_el * 2, &k16));
   RK_TRY(scratch(cs, "at_v16", nk_el * 2, &v16));
   RK_TRY(scratch(cs, "at_o16", nq_el * 2, &o16));
-  tm.mark(0);
-  const float *srcs[3] = {q, k, v};
-  void *dsts[3] = {q16, k16, v16};
-  const size_t els[3] = {nq_el, nk_el, nk_el};
-  for (int i = 0; i < 3; ++i) {
-    HIP_TRY(hipMemcpyAsync(f32buf, srcs[i], els[i] * 4, hipMemcpyHostToDevice, st), "rk_attention");
-    HIP_TRY(rk_launch_f32_to_f16((const float *)f32buf, dsts[i], (int64_t)els[i], st), "rk_attention");
-  }
-  RK_TRY(attn_dev_impl(cs, q16, k16, v16, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap,
-                       mode, window, q0, k0, o16, "rk_attention", 0, 0, 0, 0, &tm));
-  tm.mark(2);
-  HIP_TRY(rk_launch_f16_to_f32(o16, (float *)f32buf, (int64_t)nq_el, st), "rk_attention");
-  HIP_TRY(hipMemcpyAsync(out, f32buf, nq_el * 4, hipMemcpyDeviceToHost, st), "rk_attention");
-  tm.mark(3);
-  HIP_TRY(hipStreamSynchronize(st), "rk_attention");
-  tm.finish();
+  RK_TRY(scratch(cs, "at_flag", 4, (void **)&flag));
+  float *q32 = f32, *k32 = q32 + nq_el, *v32 = k32 + nk_el;
+  auto compute = [&](int64_t, int64_t) {
+    HIP_TRY(hipMemsetAsync(flag, 0, 4, st), op);
+    HIP_TRY(rk_launch_f32_to_f16_checked(q32, q16, (int64_t)nq_el, flag, st), op);
+    HIP_TRY(rk_launch_f32_to_f16_checked(k32, k16, (int64_t)nk_el, flag, st), op);
+    HIP_TRY(rk_launch_f32_to_f16(v32, v16, (int64_t)nk_el, st), op);
+    RK_TRY(attn_dev_impl(cs, q16, k16, v16, n_q, n_kv, n_head, n_kv_heads, head_dim, scale, softcap,
+                         mode, window, q0, k0, o16, op));
+    // the output overwrites q's f32 copy, which is no longer read
+    HIP_TRY(rk_launch_f16_to_f32(o16, q32, (int64_t)nq_el, st), op);
+    return RK_OK;
+  };
+  RK_TRY(staged(cs, {{q, nullptr, q32, 0, nq_el * 4}, {k, nullptr, k32, 0, nk_el * 4}, {v, nullptr, v32, 0, nk_el * 4}},
+                {{nullptr, out, q32, 0, nq_el * 4}}, 1, 1, compute, op));
+  RK_TRY(range_flag(flag, op));
   g_eng->calls++;
   return RK_OK;
 }
 
-extern "C" int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv, int n_head,
-                                 int n_kv_heads, float scale, float softcap, int mask_mode,
-                                 int64_t window, int64_t q0, int64_t k0, const uint16_t *q,
-                                 const uint16_t *k, const uint16_t *v, uint16_t *out) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  const char *op = "rk_flash_attn_f16";
+namespace {
+int flash_impl(int64_t n_q, int64_t n_kv, int head_dim, int dv, int n_head, int n_kv_heads, float scale,
+               float softcap, int mask_mode, int64_t window, int64_t q0, int64_t k0, const uint16_t *q,
+               const uint16_t *k, const uint16_t *v, uint16_t *out, const char *op) {
   RK_TRY(ensure(op));
   if (head_dim <= 0 || dv <= 0) return fail(RK_E_SHAPE, op, "head_dim and dv must be positive");
   // The kernel runs one width D for q, k and v, the smallest kernel width at
@@ -1216,54 +1400,164 @@ extern "C" int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv
   RK_TRY(attn_check(n_q, n_kv, n_head, n_kv_heads, D, &mode, window, op));
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
-  HostTimer tm(st);
-  const size_t nq_el = (size_t)n_q * n_head * D;
-  const size_t nk_el = (size_t)n_kv * n_kv_heads * D;
-  const size_t nv_in = (size_t)n_kv_heads * dv * n_kv;
+  const size_t q_in = (size_t)n_head * n_q * head_dim, k_in = (size_t)n_kv_heads * n_kv * head_dim;
+  const size_t v_in = (size_t)n_kv_heads * dv * n_kv, o_out = (size_t)n_head * n_q * dv;
+  const size_t nq_el = (size_t)n_q * n_head * D, nk_el = (size_t)n_kv * n_kv_heads * D;
   const int dvp = rk_attn_dv_pad(D);
   const int64_t n_kv_pad = round_up_i(n_kv, rk_attn_kv_tile());
-  void *q16, *k16, *v16, *o16, *vt;
+  char *raw;
+  void *q16, *k16, *o16, *vt;
+  RK_TRY(scratch(cs, "fa_raw", (q_in + k_in + v_in + o_out) * 2, (void **)&raw));
   RK_TRY(scratch(cs, "at_q16", nq_el * 2, &q16));
   RK_TRY(scratch(cs, "at_k16", nk_el * 2, &k16));
-  RK_TRY(scratch(cs, "at_v16", nv_in * 2, &v16));
   RK_TRY(scratch(cs, "at_o16", nq_el * 2, &o16));
   RK_TRY(scratch(cs, "attn_vt", (size_t)n_kv_heads * dvp * n_kv_pad * 2, &vt));
-  tm.mark(0);
-  // q [H][n_q][head_dim] and k [KV][n_kv][head_dim] into rows of D values.
-  const struct {
-    const uint16_t *src;
-    void *dst;
-    size_t rows;
-  } qk[2] = {{q, q16, (size_t)n_head * n_q}, {k, k16, (size_t)n_kv_heads * n_kv}};
-  for (const auto &t : qk) {
-    if (head_dim < D) {
-      HIP_TRY(hipMemsetAsync(t.dst, 0, t.rows * D * 2, st), op);
-      HIP_TRY(hipMemcpy2DAsync(t.dst, (size_t)D * 2, t.src, (size_t)head_dim * 2,
-                               (size_t)head_dim * 2, t.rows, hipMemcpyHostToDevice, st),
-              op);
-    } else {
-      HIP_TRY(hipMemcpyAsync(t.dst, t.src, t.rows * D * 2, hipMemcpyHostToDevice, st), op);
+  char *q_raw = raw, *k_raw = q_raw + q_in * 2, *v_raw = k_raw + k_in * 2, *o_raw = v_raw + v_in * 2;
+  auto compute = [&](int64_t, int64_t) {
+    // q [H][n_q][head_dim] and k [KV][n_kv][head_dim] into rows of D values.
+    const struct {
+      const char *src;
+      void *dst;
+      size_t rows;
+    } qk[2] = {{q_raw, q16, (size_t)n_head * n_q}, {k_raw, k16, (size_t)n_kv_heads * n_kv}};
+    for (const auto &t : qk) {
+      if (head_dim < D) {
+        HIP_TRY(hipMemsetAsync(t.dst, 0, t.rows * D * 2, st), op);
+        HIP_TRY(hipMemcpy2DAsync(t.dst, (size_t)D * 2, t.src, (size_t)head_dim * 2, (size_t)head_dim * 2,
+                                 t.rows, hipMemcpyDeviceToDevice, st),
+                op);
+      } else {
+        HIP_TRY(hipMemcpyAsync(t.dst, t.src, t.rows * D * 2, hipMemcpyDeviceToDevice, st), op);
+      }
     }
-  }
-  HIP_TRY(hipMemcpyAsync(v16, v, nv_in * 2, hipMemcpyHostToDevice, st), op);
-  // v is [KV][dv][n_kv]: element (key, head, d) at head·dv·n_kv + d·n_kv + key;
-  // its dv rows fill Vᵀ, the rest of the D rows are zero.
-  HIP_TRY(rk_launch_v_transpose_strided(v16, 1, (int64_t)dv * n_kv, n_kv, (int)n_kv, (int)n_kv_pad,
-                                        n_kv_heads, dv, dvp, vt, st),
-          op);
-  tm.mark(1);
-  RK_TRY(attn_run(q16, k16, vt, o16, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, D, scale, softcap,
-                  mode, window, q0, k0, true, st, op, &cs));
-  tm.mark(2);
-  // out [H][n_q][dv]: the first dv columns of each output row.
-  HIP_TRY(hipMemcpy2DAsync(out, (size_t)dv * 2, o16, (size_t)D * 2, (size_t)dv * 2,
-                           (size_t)n_head * n_q, hipMemcpyDeviceToHost, st),
-          op);
-  tm.mark(3);
-  HIP_TRY(hipStreamSynchronize(st), op);
-  tm.finish();
+    // v is [KV][dv][n_kv]: element (key, head, d) at head·dv·n_kv + d·n_kv + key;
+    // its dv rows fill Vᵀ, the rest of the D rows are zero.
+    HIP_TRY(rk_launch_v_transpose_strided(v_raw, 1, (int64_t)dv * n_kv, n_kv, (int)n_kv, (int)n_kv_pad,
+                                          n_kv_heads, dv, dvp, vt, st),
+            op);
+    RK_TRY(attn_run(q16, k16, vt, o16, n_q, n_kv, n_kv_pad, n_head, n_kv_heads, D, scale, softcap, mode,
+                    window, q0, k0, true, st, op, &cs));
+    // out [H][n_q][dv]: the first dv columns of each output row.
+    HIP_TRY(hipMemcpy2DAsync(o_raw, (size_t)dv * 2, o16, (size_t)D * 2, (size_t)dv * 2, (size_t)n_head * n_q,
+                             hipMemcpyDeviceToDevice, st),
+            op);
+    return RK_OK;
+  };
+  RK_TRY(staged(cs, {{q, nullptr, q_raw, 0, q_in * 2}, {k, nullptr, k_raw, 0, k_in * 2}, {v, nullptr, v_raw, 0, v_in * 2}},
+                {{nullptr, out, o_raw, 0, o_out * 2}}, 1, 1, compute, op));
   g_eng->calls++;
   return RK_OK;
+}
+
+// The additive masks of masks.rs:11-114 (0 visible, -inf hidden) in the
+// kernel's predicate form: each row's visible keys must be one interval and
+// the rows' intervals those of one mode at one query-key offset d = q0 - k0
+// (relative query i sees relative key j as absolute t = i + d against j).
+struct MaskFit {
+  int mode = RK_MASK_NONE;
+  int64_t window = -1, q0 = 0, k0 = 0;
+};
+
+int classify_mask(const uint16_t *mask, int64_t n_q, int64_t n_kv, MaskFit *fit, const char *op) {
+  std::vector<int64_t> lo(n_q), hi(n_q);  // visible interval per row; lo > hi: none
+  bool all_full = true;
+  for (int64_t i = 0; i < n_q; ++i) {
+    const uint16_t *row = mask + i * n_kv;
+    int64_t first = -1, last = -2, count = 0;
+    for (int64_t j = 0; j < n_kv; ++j) {
+      const uint16_t m = row[j];
+      if ((m & 0x7fff) == 0) {
+        if (first < 0) first = j;
+        last = j;
+        ++count;
+      } else if (m != 0xfc00) {
+        return fail(RK_E_UNSUPPORTED, op, "an additive mask value other than 0 and -inf");
+      }
+    }
+    if (first < 0) first = 0, last = -1;
+    if (count != last - first + 1)
+      return fail(RK_E_UNSUPPORTED, op, "a mask row whose visible keys are not one interval");
+    lo[i] = first;
+    hi[i] = last;
+    all_full = all_full && first == 0 && last == n_kv - 1;
+  }
+  if (all_full) return RK_OK;
+  // Offsets of the unclipped ends: hi = i + dh (causal, window, causal window)
+  // and lo = i + dl (window, causal window).
+  bool has_h = false, has_l = false;
+  int64_t dh = 0, dl = 0, first_full = -1;
+  for (int64_t i = 0; i < n_q; ++i) {
+    if (lo[i] > hi[i]) continue;
+    if (!has_h && hi[i] < n_kv - 1) has_h = true, dh = hi[i] - i;
+    if (!has_l && lo[i] > 0) has_l = true, dl = lo[i] - i;
+    if (first_full < 0 && lo[i] == 0 && hi[i] == n_kv - 1) first_full = i;
+  }
+  const int64_t big = n_q + n_kv + 1;
+  struct Cand {
+    int mode;
+    int64_t d, w;
+  };
+  std::vector<Cand> cands;
+  if (has_h) cands.push_back({RK_MASK_CAUSAL, dh, -1});
+  if (has_h && has_l && dh - dl + 1 >= 1) cands.push_back({RK_MASK_CAUSAL_WINDOW, dh, dh - dl + 1});
+  if (has_h && has_l && (dh - dl) % 2 == 0 && dh >= dl)
+    cands.push_back({RK_MASK_WINDOW, (dh + dl) / 2, (dh - dl) / 2});
+  if (!has_h && has_l) {
+    cands.push_back({RK_MASK_WINDOW, dl + big, big});
+    cands.push_back({RK_MASK_CAUSAL_WINDOW, n_kv + big, n_kv + big - dl + 1});
+  }
+  if (!has_h && !has_l) {
+    if (first_full >= 0) cands.push_back({RK_MASK_CAUSAL, n_kv - 1 - first_full, -1});
+    cands.push_back({RK_MASK_CAUSAL, -(n_q + 1), -1});  // every row hidden
+  }
+  for (const Cand &c : cands) {
+    bool ok = true;
+    for (int64_t i = 0; i < n_q && ok; ++i) {
+      const int64_t t = i + c.d;
+      int64_t a, b;
+      if (c.mode == RK_MASK_CAUSAL)
+        a = 0, b = t;
+      else if (c.mode == RK_MASK_WINDOW)
+        a = t - c.w, b = t + c.w;
+      else
+        a = t - c.w + 1, b = t;
+      a = std::max<int64_t>(a, 0);
+      b = std::min<int64_t>(b, n_kv - 1);
+      const bool empty = a > b, row_empty = lo[i] > hi[i];
+      ok = empty ? row_empty : (!row_empty && a == lo[i] && b == hi[i]);
+    }
+    if (ok) {
+      fit->mode = c.mode;
+      fit->window = c.w;
+      fit->q0 = std::max<int64_t>(c.d, 0);
+      fit->k0 = std::max<int64_t>(-c.d, 0);
+      return RK_OK;
+    }
+  }
+  return fail(RK_E_UNSUPPORTED, op, "an additive mask that is not a causal, band or causal-window mask");
+}
+}  // namespace
+
+extern "C" int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv, int n_head,
+                                 int n_kv_heads, float scale, float softcap, int mask_mode,
+                                 int64_t window, int64_t q0, int64_t k0, const uint16_t *q,
+                                 const uint16_t *k, const uint16_t *v, uint16_t *out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return flash_impl(n_q, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, mask_mode, window, q0, k0,
+                    q, k, v, out, "rk_flash_attn_f16");
+}
+
+extern "C" int rk_flash_attn_f16_masked(int64_t n_q, int64_t n_kv, int head_dim, int dv, int n_head,
+                                        int n_kv_heads, float scale, float softcap, const uint16_t *mask,
+                                        const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                        uint16_t *out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  const char *op = "rk_flash_attn_f16_masked";
+  if (n_q <= 0 || n_kv <= 0) return fail(RK_E_SHAPE, op, "empty query or key axis");
+  MaskFit fit;
+  if (mask) RK_TRY(classify_mask(mask, n_q, n_kv, &fit, op));
+  return flash_impl(n_q, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, fit.mode, fit.window, fit.q0,
+                    fit.k0, q, k, v, out, op);
 }
 
 // =========================================================================
@@ -1452,7 +1746,7 @@ int moe_plan(const Weight &w, int64_t s, int top_k, const uint32_t *ids, const f
   const int E = w.n_experts;
   std::vector<int64_t> count(E, 0);
   for (int64_t i = 0; i < s * top_k; ++i) {
-    if (ids[i] >= (uint32_t)E) return fail(RK_E_RANGE, op, "expert id out of range");
+    if (ids[i] >= (uint32_t)E) return fail(RK_E_SHAPE, op, "expert id out of range");
     count[ids[i]]++;
   }
   std::vector<int64_t> off(E + 1, 0);
@@ -1563,7 +1857,7 @@ int plan_mark_used(const MoePlan &p, hipStream_t st) {
 
 int moe_check(uint64_t id, int64_t s, int top_k, Weight **w, const char *op) {
   *w = find(id);
-  if (!*w || !(*w)->moe) return fail(RK_E_RANGE, op, "id is not an expert stack");
+  if (!*w || !(*w)->moe) return fail(RK_E_SHAPE, op, "id is not an expert stack");
   if (s <= 0 || top_k <= 0 || top_k > (*w)->n_experts)
     return fail(RK_E_SHAPE, op, "need s > 0 and 0 < top_k <= n_experts");
   // The expert kernels address the int8 activations (x [s, hidden], the
@@ -1734,17 +2028,17 @@ int glue_host(int op, const float *a, const float *b, float *out, int64_t n, con
   if (n < 0) return fail(RK_E_SHAPE, name, "negative element count");
   if (n == 0) return RK_OK;
   if (!a || !b || !out) return fail(RK_E_SHAPE, name, "null buffer");
-  CallScope cs(g_eng->stream);
+  hipStream_t st = g_eng->stream;
+  CallScope cs(st);
   void *d = nullptr;
   RK_TRY(scratch(cs, "glue", (size_t)n * 12, &d));
   float *da = (float *)d, *db = da + n, *dout = db + n;
-  hipStream_t st = g_eng->stream;
-  HIP_TRY(hipMemcpyAsync(da, a, (size_t)n * 4, hipMemcpyHostToDevice, st), name);
-  HIP_TRY(hipMemcpyAsync(db, b, (size_t)n * 4, hipMemcpyHostToDevice, st), name);
-  HIP_TRY(rk_launch_glue(op, da, db, dout, n, RK_DTYPE_F32, st), name);
-  HIP_TRY(hipMemcpyAsync(out, dout, (size_t)n * 4, hipMemcpyDeviceToHost, st), name);
-  HIP_TRY(hipStreamSynchronize(st), name);
-  return RK_OK;
+  auto compute = [&](int64_t r0, int64_t r1) {
+    HIP_TRY(rk_launch_glue(op, da + r0, db + r0, dout + r0, r1 - r0, RK_DTYPE_F32, st), name);
+    return RK_OK;
+  };
+  return staged(cs, {{a, nullptr, da, 4, 0}, {b, nullptr, db, 4, 0}}, {{nullptr, out, dout, 4, 0}}, n,
+                stage_chunk_rows(n, 8, 4), compute, name);
 }
 }  // namespace
 
@@ -1798,18 +2092,21 @@ int rms_host(const float *x, const float *w, float *out, int64_t rows, int64_t d
   RK_TRY(rms_check(x, out, rows, d, RK_DTYPE_F32, name));
   if (rows == 0) return RK_OK;
   const size_t n = (size_t)(rows * d);
-  CallScope cs(g_eng->stream);
+  hipStream_t st = g_eng->stream;
+  CallScope cs(st);
   void *buf = nullptr;
   RK_TRY(scratch(cs, "norm", (n + (size_t)d) * 4, &buf));
   float *dx = (float *)buf, *dw = dx + n;
-  hipStream_t st = g_eng->stream;
-  HIP_TRY(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, st), name);
-  if (w) HIP_TRY(hipMemcpyAsync(dw, w, (size_t)d * 4, hipMemcpyHostToDevice, st), name);
-  HIP_TRY(rk_launch_rms_norm(dx, w ? dw : nullptr, RK_DTYPE_F32, dx, rows, (int)d, (float)eps,
-                             RK_DTYPE_F32, st), name);
-  HIP_TRY(hipMemcpyAsync(out, dx, n * 4, hipMemcpyDeviceToHost, st), name);
-  HIP_TRY(hipStreamSynchronize(st), name);
-  return RK_OK;
+  std::vector<rkstage::Xfer> ins = {{x, nullptr, dx, (size_t)d * 4, 0}};
+  if (w) ins.push_back({w, nullptr, dw, 0, (size_t)d * 4});
+  auto compute = [&](int64_t r0, int64_t r1) {
+    HIP_TRY(rk_launch_rms_norm(dx + r0 * d, w ? dw : nullptr, RK_DTYPE_F32, dx + r0 * d, r1 - r0, (int)d,
+                               (float)eps, RK_DTYPE_F32, st),
+            name);
+    return RK_OK;
+  };
+  return staged(cs, ins, {{nullptr, out, dx, (size_t)d * 4, 0}}, rows,
+                stage_chunk_rows(rows, (size_t)d * 4, (size_t)d * 4), compute, name);
 }
 }  // namespace
 
@@ -1954,19 +2251,19 @@ extern "C" int rk_rope(const float *x, const float *cos, const float *sin, float
   RK_TRY(rope_check(x, cos, sin, out, b, s, h, d, RK_DTYPE_F32, RK_DTYPE_F32, name));
   const size_t n = (size_t)(b * s * h * d), nt = (size_t)(s * (d / 2));
   if (n == 0) return RK_OK;
-  CallScope cs(g_eng->stream);
+  hipStream_t st = g_eng->stream;
+  CallScope cs(st);
   void *buf = nullptr;
   RK_TRY(scratch(cs, "rope", (n + 2 * nt) * 4, &buf));
   float *dx = (float *)buf, *dc = dx + n, *ds = dc + nt;
-  hipStream_t st = g_eng->stream;
-  HIP_TRY(hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, st), name);
-  HIP_TRY(hipMemcpyAsync(dc, cos, nt * 4, hipMemcpyHostToDevice, st), name);
-  HIP_TRY(hipMemcpyAsync(ds, sin, nt * 4, hipMemcpyHostToDevice, st), name);
-  HIP_TRY(rk_launch_rope(dx, dc, ds, RK_DTYPE_F32, dx, (int)(b * s * h), (int)s, (int)h,
-                         (int)(d / 2), RK_DTYPE_F32, st), name);
-  HIP_TRY(hipMemcpyAsync(out, dx, n * 4, hipMemcpyDeviceToHost, st), name);
-  HIP_TRY(hipStreamSynchronize(st), name);
-  return RK_OK;
+  auto compute = [&](int64_t, int64_t) {
+    HIP_TRY(rk_launch_rope(dx, dc, ds, RK_DTYPE_F32, dx, (int)(b * s * h), (int)s, (int)h, (int)(d / 2),
+                           RK_DTYPE_F32, st),
+            name);
+    return RK_OK;
+  };
+  return staged(cs, {{x, nullptr, dx, 0, n * 4}, {cos, nullptr, dc, 0, nt * 4}, {sin, nullptr, ds, 0, nt * 4}},
+                {{nullptr, out, dx, 0, n * 4}}, 1, 1, compute, name);
 }
 
 extern "C" int rk_memcpy_dtod(void *dst, const void *src, size_t bytes, rk_stream stream) {

@@ -57,6 +57,7 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st);
 
 // Element-wise conversions.
 hipError_t rk_launch_f32_to_f16(const float *x, void *y, int64_t n, hipStream_t st);
+hipError_t rk_launch_f32_to_f16_checked(const float *x, void *y, int64_t n, int *flag, hipStream_t st);
 hipError_t rk_launch_f16_to_f32(const void *x, float *y, int64_t n, hipStream_t st);
 
 // MLP glue: op 0 silu_mul, 1 gelu_mul; dtype RK_DTYPE_*.

@@ -30,6 +30,36 @@ __global__ void f16_to_f32_kernel(const f16 *__restrict__ x, float *__restrict__
   }
 }
 
+// f32 -> fp16 that also sets *flag to 1 when a converted value is not finite
+// (an input outside fp16's range, or not finite itself).
+__global__ void f32_to_f16_checked_kernel(const float *__restrict__ x, f16 *__restrict__ y, int64_t n,
+                                          int *__restrict__ flag) {
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  bool bad = false;
+  if (i + 3 < n) {
+    floatx4 v = *(const floatx4 *)(x + i);
+    half4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    *(half4 *)(y + i) = h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bad |= !isfinite((float)h[e]);
+  } else {
+    for (; i < n; ++i) {
+      const f16 h = (f16)x[i];
+      y[i] = h;
+      bad |= !isfinite((float)h);
+    }
+  }
+  if (bad) *flag = 1;
+}
+
+hipError_t rk_launch_f32_to_f16_checked(const float *x, void *y, int64_t n, int *flag, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  int64_t threads = (n + 3) / 4;
+  hipLaunchKernelGGL(f32_to_f16_checked_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, x, (f16 *)y, n, flag);
+  return hipGetLastError();
+}
+
 hipError_t rk_launch_f32_to_f16(const float *x, void *y, int64_t n, hipStream_t st) {
   if (n <= 0) return hipSuccess;
   // Vector path needs 16-byte aligned rows of 4; callers pass whole buffers.

@@ -16,6 +16,13 @@
 //! `op_failure` does (ext.rs:344-352). Weights in bf16 are packed as fp16
 //! (the bf16 streaming context of the reference is not part of this library).
 //!
+//! Beside the trait, the free functions the app calls whose reference bodies
+//! reach the RK3588 engine are replaced too: `pack_qat`, `stats`,
+//! `stats_reset`, `mem_stats`, `trim_scratch`, `trim_scratch_to` and
+//! `clear_scratch`. The driver types Clef holds directly (`RocketCtx`,
+//! `RocketFaCtx`, `npu::matmul::I8Context`) come from rocket-hip-sys
+//! (`ctx.rs`, `npu.rs`), re-exported by lib.rs in place of rocket-npu's.
+//!
 //! Not compiled in the repository that holds it (no Rust toolchain there);
 //! tests/test_rust_binding.py checks that every item it takes from
 //! rocket-hip-sys exists there, and that the crate's FFI declarations match
@@ -266,4 +273,46 @@ pub fn trim_scratch_to(budget: usize) {
 }
 pub fn clear_scratch() {
     let _ = hip::clear_scratch();
+}
+
+/// `burn_rocket::trim_scratch` (ext.rs:254-265): scratch no call used since the
+/// previous trim goes; the just-used set stays (src/util/mem.rs:99-101 calls it
+/// after each served request).
+pub fn trim_scratch() {
+    let _ = hip::trim_scratch();
+}
+
+/// `burn_rocket::mem_stats` (ext.rs:206-252): `None` before `init`, as the
+/// reference. The device scratch splits into the attention buffers
+/// (`attention_bo_bytes`) and the rest (`matmul_bo_bytes`); the page-locked
+/// staging of the host-buffer ops is `matmul_host_bytes`. The scratch is one
+/// buffer per use grown to its largest call, not a per-shape cache, so
+/// `slots` and `attn_workers` stay empty.
+pub fn mem_stats() -> Option<crate::MemStats> {
+    let s = hip::mem_stats().ok()?;
+    Some(crate::MemStats {
+        weights_bytes: s.weights_bytes as usize,
+        matmul_bo_bytes: (s.scratch_bytes - s.attention_bytes) as usize,
+        matmul_host_bytes: s.host_bytes as usize,
+        attention_bo_bytes: s.attention_bytes as usize,
+        attention_host_bytes: 0,
+        slots: Vec::new(),
+        attn_workers: Vec::new(),
+    })
+}
+
+/// `burn_rocket::pack_qat` (ext.rs:1375-1425): one pre-quantized per-channel
+/// int8 weight of a QAT checkpoint, codes `[N, K]`, `w_scale [N]`, the static
+/// activation scale (0 = per-row dynamic) and the output grid (0 = none). The
+/// Gemma 4 loader packs its QAT linears through it
+/// (src/gemma/gemma4/loader.rs:1149, 1283); `matmul` on the returned id runs
+/// the QAT path (quantizer, exact int32 product, epilogue) on the GPU.
+pub fn pack_qat(codes: &[i8], w_scale: Vec<f32>, n: usize, k: usize, in_scale: f32, out_scale: f32) -> super::WeightId {
+    assert_eq!(codes.len(), n * k, "QAT codes must be [N, K]");
+    assert_eq!(w_scale.len(), n, "one weight scale per output channel");
+    assert!(in_scale >= 0.0, "QAT input scale must not be negative");
+    assert_eq!(k % 32, 0, "the int8 path needs K % 32 == 0 (K={k})");
+    assert_eq!(n % 32, 0, "the int8 path needs N % 32 == 0 (N={n})");
+    let id = hip::pack_qat(codes, &w_scale, n, k, in_scale, out_scale).unwrap_or_else(|e| op_failure(e, 0, k, n));
+    super::WeightId(id)
 }

@@ -56,13 +56,17 @@ pub struct RkStats {
     pub calls: u64,
 }
 
-/// `rk_mem_stats_t`: live resident-weight and scratch bytes.
+/// `rk_mem_stats_t`: live resident-weight, device scratch (all / attention)
+/// and page-locked staging bytes.
 #[repr(C)]
 #[derive(Debug, Default, Clone, Copy)]
 pub struct RkMemStats {
     pub weights_bytes: u64,
     pub scratch_bytes: u64,
     pub n_weights: u64,
+    pub attention_bytes: u64,
+    pub host_bytes: u64,
+    pub n_scratch: u64,
 }
 
 #[link(name = "burn_rocket_amd")]
@@ -75,6 +79,7 @@ unsafe extern "C" {
     pub fn rk_mem_stats(out: *mut RkMemStats) -> c_int;
     pub fn rk_trim_scratch_to(budget: u64) -> c_int;
     pub fn rk_clear_scratch() -> c_int;
+    pub fn rk_trim_scratch() -> c_int;
     pub fn rk_pack(w: *const f32, n: i64, k: i64, id: *mut WeightId) -> c_int;
     pub fn rk_pack_f16(w: *const u16, n: i64, k: i64, id: *mut WeightId) -> c_int;
     pub fn rk_pack_seg(
@@ -95,6 +100,12 @@ unsafe extern "C" {
         id: WeightId, kind: *mut c_int, n: *mut i64, k: *mut i64, group: *mut i64
     ) -> c_int;
     pub fn rk_matmul(id: WeightId, x: *const f32, m: i64, k: i64, y: *mut f32) -> c_int;
+    pub fn rk_matmul_f16(id: WeightId, a: *const u16, m: i64, k: i64, c: *mut u16) -> c_int;
+    pub fn rk_matmul_i8_gw(
+        id: WeightId, a: *const i8, a_scale: *const f32, b_scale: *const f32, m: i64, k: i64,
+        cf: *mut f32
+    ) -> c_int;
+    pub fn rk_matmul_i8(id: WeightId, a: *const i8, m: i64, k: i64, c: *mut i32) -> c_int;
     pub fn rk_matmul_f16_dev(
         id: WeightId, a: *const c_void, m: i64, k: i64, c: *mut c_void, stream: Stream
     ) -> c_int;
@@ -145,6 +156,11 @@ unsafe extern "C" {
         n_q: i64, n_kv: i64, head_dim: c_int, dv: c_int, n_head: c_int, n_kv_heads: c_int,
         scale: f32, softcap: f32, mask_mode: c_int, window: i64, q0: i64, k0: i64, q: *const u16,
         k: *const u16, v: *const u16, out: *mut u16
+    ) -> c_int;
+    pub fn rk_flash_attn_f16_masked(
+        n_q: i64, n_kv: i64, head_dim: c_int, dv: c_int, n_head: c_int, n_kv_heads: c_int,
+        scale: f32, softcap: f32, mask: *const u16, q: *const u16, k: *const u16, v: *const u16,
+        out: *mut u16
     ) -> c_int;
     pub fn rk_moe_route(
         logits: *const f32, s: i64, n_experts: c_int, top_k: c_int, norm_topk: c_int,
@@ -368,7 +384,112 @@ pub fn weight_info(id: WeightId) -> Result<(i32, usize, usize, usize), Error> {
 /// `y[m, n] = x[m, k] · Wᵀ` on host f32 buffers for any weight kind (`rocket_matmul`).
 pub fn matmul(id: WeightId, x: &[f32], m: usize, k: usize, y: &mut [f32]) -> Result<(), Error> {
     assert_eq!(x.len(), m * k, "matmul: x must be [M, K]");
+    // The library writes m·N values, N from the resident weight.
+    let (_, n, wk, _) = weight_info(id)?;
+    assert_eq!(wk, k, "matmul: activation K differs from the weight's K");
+    assert_eq!(y.len(), m * n, "matmul: y must be [M, N]");
     check(unsafe { rk_matmul(id, x.as_ptr(), m as i64, k as i64, y.as_mut_ptr()) }, "rocket_matmul")
+}
+
+/// `C[m, n] = A[m, k] · Bᵀ` on host fp16 buffers (`RocketCtx::matmul_prepacked`).
+pub fn matmul_f16(id: WeightId, a: &[u16], m: usize, k: usize, c: &mut [u16]) -> Result<(), Error> {
+    let (kind, n, wk, _) = weight_info(id)?;
+    assert_eq!(kind, RK_WEIGHT_F16, "matmul_f16: not an fp16 weight");
+    assert_eq!(wk, k, "matmul_f16: activation K differs from the weight's K");
+    assert!(a.len() == m * k && c.len() == m * n, "matmul_f16: A [M, K], C [M, N]");
+    check(unsafe { rk_matmul_f16(id, a.as_ptr(), m as i64, k as i64, c.as_mut_ptr()) }, "rocket_matmul_fp16")
+}
+
+/// `cf[m, n] = Σ_g a_scale[m,g]·b_scale[n,g]·P_g` on host buffers (`I8Context::matmul_gw`);
+/// `b_scale` None uses the scales packed with the weight.
+pub fn matmul_i8_gw(
+    id: WeightId, a: &[i8], a_scale: &[f32], b_scale: Option<&[f32]>, m: usize, k: usize, cf: &mut [f32],
+) -> Result<(), Error> {
+    let (kind, n, wk, group) = weight_info(id)?;
+    assert!(kind == RK_WEIGHT_I8 && group > 0, "matmul_i8_gw: not a group-wise int8 weight");
+    assert_eq!(wk, k, "matmul_i8_gw: activation K differs from the weight's K");
+    let ng = k / group;
+    assert!(a.len() == m * k && a_scale.len() == m * ng && cf.len() == m * n, "matmul_i8_gw: buffers");
+    if let Some(b) = b_scale {
+        assert_eq!(b.len(), n * ng, "matmul_i8_gw: b_scale must be [N, K/group]");
+    }
+    let bp = b_scale.map_or(std::ptr::null(), |b| b.as_ptr());
+    check(
+        unsafe { rk_matmul_i8_gw(id, a.as_ptr(), a_scale.as_ptr(), bp, m as i64, k as i64, cf.as_mut_ptr()) },
+        "rocket_matmul_int8_prepacked_gw",
+    )
+}
+
+/// Raw int32 `c[m, n] = Σ_k a[m,k]·w[n,k]` on host buffers (`I8Context::matmul`).
+pub fn matmul_i8(id: WeightId, a: &[i8], m: usize, k: usize, c: &mut [i32]) -> Result<(), Error> {
+    let (kind, n, wk, _) = weight_info(id)?;
+    assert!(kind == RK_WEIGHT_I8 || kind == RK_WEIGHT_QAT, "matmul_i8: not an int8 weight");
+    assert_eq!(wk, k, "matmul_i8: activation K differs from the weight's K");
+    assert!(a.len() == m * k && c.len() == m * n, "matmul_i8: A [M, K], C [M, N]");
+    check(unsafe { rk_matmul_i8(id, a.as_ptr(), m as i64, k as i64, c.as_mut_ptr()) }, "rocket_matmul_int8_prepacked")
+}
+
+/// Resident fp16 weight from fp16 bits `[n, k]` (`RocketCtx::pack_weight`).
+pub fn pack_f16(w: &[u16], n: usize, k: usize) -> Result<WeightId, Error> {
+    assert_eq!(w.len(), n * k, "pack_f16: weight must be [N, K]");
+    let mut id = 0;
+    check(unsafe { rk_pack_f16(w.as_ptr(), n as i64, k as i64, &mut id) }, "rocket_weights_pack")?;
+    Ok(id)
+}
+
+/// Group-wise int8 codes `[n, k]`, with scales `[n, k/group]` or without
+/// (`I8Context::pack_weight_gw` keeps the codes alone).
+pub fn pack_i8_codes(codes: &[i8], scales: Option<&[f32]>, n: usize, k: usize, group: usize) -> Result<WeightId, Error> {
+    assert_eq!(codes.len(), n * k, "pack_i8_codes: codes must be [N, K]");
+    assert!(group > 0 && group % 32 == 0 && k % group == 0, "pack_i8_codes: group");
+    if let Some(s) = scales {
+        assert_eq!(s.len(), n * (k / group), "pack_i8_codes: scales must be [N, K/group]");
+    }
+    let sp = scales.map_or(std::ptr::null(), |s| s.as_ptr());
+    let mut id = 0;
+    check(
+        unsafe { rk_pack_i8_codes(codes.as_ptr(), sp, n as i64, k as i64, group as i64, &mut id) },
+        "rocket_i8_weights_pack_gw",
+    )?;
+    Ok(id)
+}
+
+/// New codes (and scales, or keep the resident ones) for a resident int8 weight.
+pub fn rewrite_i8(id: WeightId, codes: &[i8], scales: Option<&[f32]>) -> Result<(), Error> {
+    let (_, n, k, group) = weight_info(id)?;
+    assert_eq!(codes.len(), n * k, "rewrite_i8: codes must be [N, K]");
+    if let Some(s) = scales {
+        assert_eq!(s.len(), n * (k / group), "rewrite_i8: scales must be [N, K/group]");
+    }
+    let sp = scales.map_or(std::ptr::null(), |s| s.as_ptr());
+    check(unsafe { rk_rewrite_i8(id, codes.as_ptr(), sp) }, "rocket_i8_rewrite_gw")
+}
+
+/// Head-major fp16 attention with an optional additive 0 / -inf mask
+/// (`RocketFaCtx::flash_attn`): q `[H][n_q][head_dim]`, k `[KV][n_kv][head_dim]`,
+/// v `[KV][dv][n_kv]`, out `[H][n_q][dv]`, mask `[n_q][n_kv]`.
+#[allow(clippy::too_many_arguments)]
+pub fn flash_attn_f16(
+    n_q: usize, n_kv: usize, head_dim: usize, dv: usize, n_head: usize, n_kv_heads: usize, scale: f32,
+    softcap: f32, q: &[u16], k: &[u16], v: &[u16], mask: Option<&[u16]>, out: &mut [u16],
+) -> Result<(), Error> {
+    assert_eq!(q.len(), n_head * n_q * head_dim, "flash_attn: q must be [H][n_q][head_dim]");
+    assert_eq!(k.len(), n_kv_heads * n_kv * head_dim, "flash_attn: k must be [KV][n_kv][head_dim]");
+    assert_eq!(v.len(), n_kv_heads * dv * n_kv, "flash_attn: v must be [KV][dv][n_kv]");
+    assert_eq!(out.len(), n_head * n_q * dv, "flash_attn: out must be [H][n_q][dv]");
+    if let Some(m) = mask {
+        assert_eq!(m.len(), n_q * n_kv, "flash_attn: mask must be [n_q][n_kv]");
+    }
+    let mp = mask.map_or(std::ptr::null(), |m| m.as_ptr());
+    check(
+        unsafe {
+            rk_flash_attn_f16_masked(
+                n_q as i64, n_kv as i64, head_dim as c_int, dv as c_int, n_head as c_int, n_kv_heads as c_int,
+                scale, softcap, mp, q.as_ptr(), k.as_ptr(), v.as_ptr(), out.as_mut_ptr(),
+            )
+        },
+        "rocket_flash_attn_fp16_ctx",
+    )
 }
 
 /// The mask of one attention call: mode, window and the block offsets.
@@ -437,6 +558,7 @@ pub fn rope(
     x: &[f32], cos: &[f32], sin: &[f32], b: usize, s: usize, h: usize, d: usize, out: &mut [f32],
 ) -> Result<(), Error> {
     assert_eq!(x.len(), b * s * h * d, "rope: x must be [B, S, H, D]");
+    assert_eq!(out.len(), x.len(), "rope: out must be [B, S, H, D]");
     assert!(cos.len() == s * d / 2 && sin.len() == s * d / 2, "rope: tables must be [S, D/2]");
     check(
         unsafe {
@@ -466,3 +588,10 @@ pub fn trim_scratch_to(budget: u64) -> Result<(), Error> {
 pub fn clear_scratch() -> Result<(), Error> {
     check(unsafe { rk_clear_scratch() }, "clear_scratch")
 }
+pub fn trim_scratch() -> Result<(), Error> {
+    check(unsafe { rk_trim_scratch() }, "trim_scratch")
+}
+
+pub mod ctx;
+pub mod npu;
+pub use ctx::{RocketCtx, RocketFaCtx, RocketWeight};

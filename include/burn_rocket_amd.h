@@ -44,7 +44,7 @@ extern "C" {
 #define RK_E_NOMEM (-3)       /* device or host allocation failed */
 #define RK_E_DEVICE (-4)      /* HIP runtime / device failure */
 #define RK_E_UNSUPPORTED (-5) /* feature not supported */
-#define RK_E_RANGE (-6)       /* value out of range (fp16 overflow, id unknown) */
+#define RK_E_RANGE (-6)       /* an fp16 value left its range (error.rs:22-24) */
 #define RK_E_IO (-7)          /* I/O failure */
 
 /* ---- weight kinds (ext.rs:1156-1161 `WeightKind`) ------------------------ */
@@ -96,12 +96,12 @@ const char *rk_last_error(void);
 int rk_is_fallback(int rc);
 
 /* Op time counters: `burn_rocket::stats()` / `stats_reset()` (ext.rs:165-200).
- * The host-buffer entries (rk_matmul, rk_attention, rk_flash_attn_f16) are
- * timed with events on their stream: convert_s is their host<->device copies,
- * format conversions and layout passes (the reference's T_CONVERT_US), device_s
- * the op's own kernels (T_NPU_US). calls counts matmul, attention and MoE calls,
- * host-buffer and `_dev` alike; the `_dev` entries return before their kernels
- * finish and add no time. */
+ * For the host-buffer entries device_s is the time of the op's kernels on the
+ * device (events around each row chunk's kernels; the reference's T_NPU_US)
+ * and convert_s the rest of the call's wall time: the host<->device copies
+ * and waits that the kernels did not hide (its T_CONVERT_US). calls counts
+ * matmul, attention and MoE calls, host-buffer and `_dev` alike; the `_dev`
+ * entries return before their kernels finish and add no time. */
 typedef struct {
   double convert_s;
   double device_s;
@@ -110,17 +110,30 @@ typedef struct {
 int rk_stats(rk_stats_t *out);
 int rk_stats_reset(void);
 
-/* Live memory held by the engine: `burn_rocket::mem_stats()` (ext.rs:206-252).*/
+/* Live memory held by the engine: `burn_rocket::mem_stats()` (ext.rs:206-252;
+ * `MemStats`, lib.rs:44-84). The device scratch is per named buffer, grown to
+ * the largest call that used it; attention_bytes is the part the attention
+ * entries use (the reference's attention_bo_bytes, the rest its
+ * matmul_bo_bytes); host_bytes is the page-locked staging of the host-buffer
+ * entries (its *_host_bytes). */
 typedef struct {
-  uint64_t weights_bytes; /* resident weights */
-  uint64_t scratch_bytes; /* per-shape device scratch */
+  uint64_t weights_bytes;   /* resident weights */
+  uint64_t scratch_bytes;   /* device scratch, all buffers */
   uint64_t n_weights;
+  uint64_t attention_bytes; /* device scratch of the attention entries */
+  uint64_t host_bytes;      /* page-locked host staging */
+  uint64_t n_scratch;       /* scratch buffers */
 } rk_mem_stats_t;
 int rk_mem_stats(rk_mem_stats_t *out);
 /* Drop scratch above `budget` bytes / all scratch: `trim_scratch_to`,
- * `clear_scratch` (ext.rs:256-308). */
+ * `clear_scratch` (ext.rs:256-308). A zero budget also frees the page-locked
+ * staging (allocated again by the next host-buffer call). */
 int rk_trim_scratch_to(uint64_t budget);
 int rk_clear_scratch(void);
+/* `trim_scratch` (ext.rs:254-265): frees the scratch buffers that no call has
+ * used since the previous rk_trim_scratch; what the calls in between used
+ * stays, as the reference keeps the just-used shape set. */
+int rk_trim_scratch(void);
 
 /* ======================================================================== *
  * Resident weights                                                          *
@@ -143,11 +156,16 @@ int rk_pack_seg(const float *const *parts, const int64_t *ns, int nparts,
 int rk_pack_i8(const float *w, int64_t n, int64_t k, int64_t group,
                rk_weight_id *id);
 /* Pre-quantized group-wise weight: codes [N, K], scales [N, K/group]
- * (`RocketI8Ctx::pack_weight_gw`, lib.rs:363; int8.rs:458). */
+ * (`RocketI8Ctx::pack_weight_gw`, lib.rs:363; int8.rs:458). scales may be
+ * NULL: the codes alone, as `I8Context::pack_weight_gw` keeps them (the
+ * scales then come with each rk_matmul_i8_gw call, int8.rs:644-676); group K
+ * with NULL scales is the per-channel `I8Context::pack_weight` (int8.rs:452),
+ * whose product is rk_matmul_i8. */
 int rk_pack_i8_codes(const int8_t *codes, const float *scales, int64_t n,
                      int64_t k, int64_t group, rk_weight_id *id);
 /* Replace the codes/scales of a resident group-wise weight in place
- * (`I8Context::rewrite_weight_gw`, int8.rs:521). */
+ * (`I8Context::rewrite_weight_gw`, int8.rs:521). NULL scales keep the
+ * resident scales (the reference rewrites codes only, int8.rs:482-526). */
 int rk_rewrite_i8(rk_weight_id id, const int8_t *codes, const float *scales);
 /* GGUF Q8_0 weight: [N, K/32] blocks of 34 bytes {f16 d, int8 q[32]}
  * (src/util/gguf.rs:125-200), e.g. a pointer into an mmapped GGUF tensor. The
@@ -173,6 +191,13 @@ int rk_weight_info(rk_weight_id id, int *kind, int64_t *n, int64_t *k,
  * Matmul                                                                    *
  * ======================================================================== */
 
+/* Host-buffer entries (rk_matmul, rk_matmul_i8_gw, rk_matmul_i8, rk_attention,
+ * rk_flash_attn_f16, rk_silu_mul, rk_gelu_mul, rk_rms_norm*, rk_rope) move
+ * their buffers through page-locked staging slots (hipHostMalloc) with a
+ * pool of CPU copy threads; row-separable ops run in row chunks so that the
+ * upload of one chunk, the kernels of the previous one and the download of
+ * the one before overlap. They return when the outputs are in host memory. */
+
 /* y[M, N] = x[M, K] · Wᵀ for any resident weight, host f32 in and out
  * (`rocket_matmul` → matmul_impl, ext.rs:627, ext.rs:1208-1232):
  *   F16: x → fp16 (RNE), fp16 GEMM with f32 accumulation, fp16 result widened
@@ -184,6 +209,25 @@ int rk_weight_info(rk_weight_id id, int *kind, int64_t *n, int64_t *k,
  *        row dynamically, exact int32 C, epilogue acc·(in_scale·w_scale[n])
  *        and optional output-grid rounding (matmul_qat, ext.rs:1236-1373). */
 int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, float *y);
+
+/* fp16 GEMM on host buffers (`RocketCtx::matmul_prepacked`, lib.rs:244-254;
+ * Context::matmul_prepacked, context.rs:497-513): a fp16 [M, K], c fp16
+ * [M, N], f32 accumulation. The reference's M % 4 padding
+ * (lib.rs:500-511) is not needed: any M >= 1. */
+int rk_matmul_f16(rk_weight_id id, const uint16_t *a, int64_t m, int64_t k, uint16_t *c);
+/* `I8Context::matmul_gw` (int8.rs:644-676) on host buffers, as Clef's expert
+ * workers call it (src/clef/engine_npu.rs:75-110): a int8 codes [M, K]
+ * already quantized per row per group, a_scale [M, K/group], b_scale
+ * [N, K/group] the weight scales of this call (NULL: those packed with the
+ * weight); cf f32 [M, N] = Σ_g (a_scale[m,g]·b_scale[n,g])·P_g, groups
+ * ascending, the product of each group's scales rounded first as the
+ * reference does (int8.rs:663-667, src/clef/int8.rs:101-158). The weight is a
+ * group-wise int8 weight. */
+int rk_matmul_i8_gw(rk_weight_id id, const int8_t *a, const float *a_scale,
+                    const float *b_scale, int64_t m, int64_t k, float *cf);
+/* `I8Context::matmul` (int8.rs:606-640) on host buffers: c int32 [M, N] =
+ * Σ_k a[m,k]·w[n,k], exact, for an int8 weight of any group. */
+int rk_matmul_i8(rk_weight_id id, const int8_t *a, int64_t m, int64_t k, int32_t *c);
 
 /* fp16 GEMM on device buffers: a fp16 [M, K], c fp16 [M, N]
  * (`RocketCtx::matmul_prepacked`, lib.rs:244-254). K % 8 == 0. */
@@ -253,7 +297,9 @@ int rk_matmul_i8_partials_dev(rk_weight_id id, const int8_t *a, int64_t m,
  * the window modes into NONE / CAUSAL (ext.rs:99-126). head_dim: 32, 48, 64,
  * 72, 80, 96, 112, 128 or 256, and 160, 192, 224 (run zero-padded to 256, on
  * packed rows; the reference's contract is head_dim % 32, attn/mod.rs:1443);
- * others return RK_E_UNSUPPORTED. */
+ * others return RK_E_UNSUPPORTED. A q or k value that fp16 cannot represent
+ * returns RK_E_RANGE (the reference answers Status::Range when its fp16 score
+ * surface saturates, attn/softmax.rs:462-475; scores are f32 here). */
 int rk_attention(const float *q, const float *k, const float *v, int64_t n_q,
                  int64_t n_kv, int n_head, int n_kv_heads, int head_dim,
                  float scale, float softcap, int mask_mode, int64_t window,
@@ -275,12 +321,13 @@ int rk_attention_dev(const void *q, const void *k, const void *v, int64_t n_q,
  * RK_NOALLOC_SCRATCH_BYTES per GPU (held from rk_init until the process ends)
  * instead of library scratch. Shapes whose Vᵀ, n_kv_heads · dv_pad ·
  * round_up(n_kv, 64) · 2 bytes with dv_pad = head_dim rounded up to 16, is
- * larger return RK_E_RANGE. All calls on one GPU share that array and each
+ * larger return RK_E_NOMEM. All calls on one GPU share that array and each
  * call rewrites it: calls whose work overlaps on the device (different streams
  * with no ordering between them) race and give wrong results. It never
- * splits a query tile's keys (that needs a workspace); otherwise the same
- * arguments and results as rk_attention_dev (bit for bit when that split is
- * off, RK_ATTN_SPLIT=1). */
+ * splits a query tile's keys (that needs a workspace), and it refuses head
+ * dims 160, 192 and 224 with RK_E_UNSUPPORTED (rk_attention_dev runs those
+ * zero-padded to 256 in scratch); otherwise the same arguments and results as
+ * rk_attention_dev (bit for bit when that split is off, RK_ATTN_SPLIT=1). */
 #define RK_NOALLOC_SCRATCH_BYTES (32u << 20)
 int rk_attention_dev_noalloc(const void *q, const void *k, const void *v, int64_t n_q,
                              int64_t n_kv, int n_head, int n_kv_heads, int head_dim, float scale,
@@ -313,6 +360,17 @@ int rk_flash_attn_f16(int64_t n_q, int64_t n_kv, int head_dim, int dv,
                       int mask_mode, int64_t window, int64_t q0, int64_t k0,
                       const uint16_t *q, const uint16_t *k, const uint16_t *v,
                       uint16_t *out);
+/* `RocketFaCtx::flash_attn` (lib.rs:294-323; Attention::flash,
+ * attn/mod.rs:1541-1600) with its optional additive mask: mask fp16
+ * [n_q, n_kv] of 0 (visible) and -inf (hidden), or NULL for none. Masks of
+ * the reference's builders (masks.rs:11-114: causal, band and causal window,
+ * full-sequence or block forms) run as the kernel's predicates, found by one
+ * pass over the mask on the host; any other mask (other values, or visible
+ * keys that are not one interval per row, or rows that follow no one mode)
+ * returns RK_E_UNSUPPORTED. Layouts and padding as rk_flash_attn_f16. */
+int rk_flash_attn_f16_masked(int64_t n_q, int64_t n_kv, int head_dim, int dv, int n_head,
+                             int n_kv_heads, float scale, float softcap, const uint16_t *mask,
+                             const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *out);
 
 /* ======================================================================== *
  * MoE experts                                                               *

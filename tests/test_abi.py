@@ -74,3 +74,43 @@ def test_router_rejects_bad_top_k():
     with pytest.raises(burn_rocket.RocketError) as e:
         burn_rocket.moe_route(np.zeros((2, 4), np.float32), 5)
     assert e.value.rc == burn_rocket.RK_E_SHAPE
+
+
+def _mask(n_q, n_kv, keep):
+    i = np.arange(n_q)[:, None]
+    j = np.arange(n_kv)[None, :]
+    return np.ascontiguousarray(np.where(np.broadcast_to(keep(i, j), (n_q, n_kv)), np.float16(0), np.float16(-np.inf)).astype(np.float16))
+
+
+def test_additive_mask_classification_without_a_device():
+    # rk_flash_attn_f16_masked reads the mask on the host before it touches the
+    # device: the reference builders' masks (masks.rs:11-114) pass to the
+    # device stage (RK_E_DEVICE here, no engine), other masks are refused.
+    import burn_rocket
+    lib = burn_rocket.load_library()
+    s = burn_rocket.Stats()
+    if lib.rk_stats(ctypes.byref(s)) == 0:
+        pytest.skip("engine already initialised in this process")
+    z = np.zeros(4096, np.uint16)
+
+    def rc(mask, n_q, n_kv):
+        return lib.rk_flash_attn_f16_masked(n_q, n_kv, 64, 64, 1, 1, 0.125, 0.0, mask.view(np.uint16).ctypes.data,
+                                            z.ctypes.data, z.ctypes.data, z.ctypes.data, z.ctypes.data)
+
+    good = [(_mask(40, 40, lambda i, j: j <= i), 40, 40),
+            (_mask(40, 40, lambda i, j: np.abs(i - j) <= 3), 40, 40),
+            (_mask(40, 40, lambda i, j: (j <= i) & (j > i - 5)), 40, 40),
+            (_mask(24, 64, lambda i, j: j <= i + 30), 24, 64),                       # causal block
+            (_mask(24, 64, lambda i, j: np.abs((50 + i) - (20 + j)) <= 9), 24, 64),   # band block
+            (_mask(24, 64, lambda i, j: (j <= i + 30) & (j > i + 30 - 12)), 24, 64),  # causal window block
+            (_mask(16, 64, lambda i, j: j < 0), 16, 64),                              # every row hidden
+            (_mask(16, 64, lambda i, j: j >= 0), 16, 64)]                             # nothing hidden
+    for m, n_q, n_kv in good:
+        assert rc(m, n_q, n_kv) == burn_rocket.RK_E_DEVICE, lib.rk_last_error()
+    bad = [(np.full((40, 40), -2.0, np.float16), 40, 40),                  # a finite bias
+           (_mask(40, 40, lambda i, j: (j % 3) != 1), 40, 40),              # several intervals per row
+           (_mask(40, 40, lambda i, j: (i % 2 == 0) | (j < 0)), 40, 40),    # full and empty rows alternate
+           (_mask(40, 40, lambda i, j: j <= i // 2), 40, 40)]               # a band that widens
+    for m, n_q, n_kv in bad:
+        assert rc(m, n_q, n_kv) == burn_rocket.RK_E_UNSUPPORTED
+        assert b"mask" in lib.rk_last_error()

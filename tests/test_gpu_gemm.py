@@ -130,7 +130,8 @@ def test_shape_errors_are_reported(rk):
         rk.pack(np.ones((16, 12), np.float32))  # K % 8 != 0
     assert e.value.rc == rk.RK_E_SHAPE
     lib = rk.lib()
-    assert lib.rk_matmul(987654321, None, 1, 64, None) == rk.RK_E_RANGE
+    # an unknown id is a bad argument (RK_E_RANGE is kept for fp16 range, error.rs:22-24)
+    assert lib.rk_matmul(987654321, None, 1, 64, None) == rk.RK_E_SHAPE
     assert b"not packed" in lib.rk_last_error()
     ms = rk.mem_stats()
     assert ms.n_weights >= 1 and ms.weights_bytes >= 16 * 64 * 2

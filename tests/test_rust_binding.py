@@ -87,3 +87,90 @@ def test_wrappers_and_the_flex_impl_use_declared_items():
                "rocket_attention", "rocket_attention_window", "rocket_attention_causal_window",
                "rocket_attention_window_block", "rocket_attention_causal_block"):
         assert re.search(rf"fn {op}\(", ext), op
+
+
+CTX = os.path.join(ROOT, "burn-rocket_amd", "rust", "rocket-hip-sys", "src", "ctx.rs")
+NPU = os.path.join(ROOT, "burn-rocket_amd", "rust", "rocket-hip-sys", "src", "npu.rs")
+
+
+def _split_params(params):
+    out, depth, cur = [], 0, ""
+    for ch in params:
+        if ch in "<([":
+            depth += 1
+        elif ch in ">)]":
+            depth -= 1
+        if ch == "," and depth == 0:
+            out.append(cur.strip())
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip():
+        out.append(cur.strip())
+    return [p for p in out if p not in ("&self", "&mut self", "self", "mut self")]
+
+
+def _methods(path, type_name=None):
+    """name -> number of parameters (self excluded) of the `pub fn`s of `impl
+    type_name` (or of the file's free functions when type_name is None)."""
+    src = re.sub(r"//.*", "", open(path).read())
+    if type_name is not None:
+        start = src.index(f"impl {type_name} {{")
+        depth, i = 0, src.index("{", start)
+        for j in range(i, len(src)):
+            depth += {"{": 1, "}": -1}.get(src[j], 0)
+            if depth == 0:
+                break
+        src = src[i:j]
+    out = {}
+    for m in re.finditer(r"pub (?:const )?fn (\w+)\s*\((.*?)\)\s*(->|\{)", src, flags=re.S):
+        out[m.group(1)] = len(_split_params(" ".join(m.group(2).split())))
+    return out
+
+
+# The signatures a drop-in must keep (the Rust API the app calls), with the
+# reference's parameter counts, self excluded.
+KEEP = [
+    # free functions of crates/burn-rocket/src/ext.rs whose bodies reach the engine
+    (EXT, None, {"init": 1,            # ext.rs:561
+                 "pack_qat": 6,        # ext.rs:1382-1389
+                 "stats": 0, "stats_reset": 0,            # ext.rs:186-200
+                 "mem_stats": 0,       # ext.rs:206
+                 "trim_scratch": 0,    # ext.rs:254
+                 "trim_scratch_to": 1,  # ext.rs:281
+                 "clear_scratch": 0}),  # ext.rs:266
+    # RocketCtx / RocketFaCtx, crates/burn-rocket/src/lib.rs:203-330
+    (CTX, "RocketCtx", {"new": 1, "pack_weight": 4, "pack_weight_seg": 3, "matmul_prepacked": 6,
+                        "trim_scratch": 0, "trim_to_budget": 1, "scratch_bytes": 0, "clear_scratch": 0,
+                        "mem_stats": 0}),
+    (CTX, "RocketFaCtx", {"new": 1, "flash_attn": 13, "mem_stats": 0}),
+    (CTX, "RocketWeight", {"bytes": 0}),
+    # I8Context / I8Weight, crates/rocket-npu/src/matmul/int8.rs:126-676
+    (NPU, "I8Context", {"new": 1, "new_at": 2, "pack_weight": 4, "pack_weight_gw": 5, "rewrite_weight": 2,
+                        "rewrite_weight_gw": 2, "matmul": 6, "matmul_gw": 8, "scratch_bytes": 0,
+                        "clear_scratch": 0}),
+    (NPU, "I8Weight", {"shape": 0, "bytes": 0}),
+    # rocket_npu::Error accessors used by Clef (src/clef/engine_npu.rs:63-71), error.rs:69-150
+    (NPU, "Error", {"op": 0, "status": 0, "errno": 0, "c_code": 0}),
+    (NPU, "Status", {"code": 0, "from_code": 1}),
+]
+
+
+def test_the_reference_signatures_are_kept():
+    for path, ty, want in KEEP:
+        got = _methods(path, ty)
+        for name, arity in want.items():
+            assert name in got, f"{os.path.basename(path)} {ty or ''}::{name} missing"
+            assert got[name] == arity, f"{ty or ''}::{name}: {got[name]} parameters, the reference has {arity}"
+
+
+def test_safe_wrappers_check_output_lengths():
+    # Every safe wrapper that hands a mutable slice to the library checks its
+    # length first (a short slice would be written past its end).
+    src = open(SYS).read()
+    body = src[src.index("/// A failed call"):]
+    for m in re.finditer(r"pub fn (\w+)\s*(?:<[^>]*>)?\((.*?)\)\s*->[^{]*\{(.*?)\n\}", body, flags=re.S):
+        name, params, fn_body = m.groups()
+        outs = re.findall(r"(\w+): &mut \[", params)
+        for o in outs:
+            assert re.search(rf"\b{o}\.len\(\)", fn_body), f"{name}: no length check on {o}"

@@ -71,5 +71,24 @@ def test_noalloc_attention_rejects_shapes_beyond_its_scratch(rk):
     out = rk.DeviceBuffer(n_q * h * d * 2)
     rc = lib.rk_attention_dev_noalloc(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, n_q, n_kv, h, kv, d, 0.1, 0.0, 0, -1,
                                       0, 0, out.ptr, None)
-    assert rc == rk.RK_E_RANGE
+    assert rc == rk.RK_E_NOMEM
     assert b"static scratch" in lib.rk_last_error()
+
+
+def test_noalloc_attention_refuses_the_padded_head_dims(rk):
+    # rk_attention_dev runs head dims 160, 192 and 224 zero-padded to 256 in
+    # scratch; the no-allocation entry has no scratch for that and refuses them.
+    note("noalloc attention padded head dims")
+    lib = rk.lib()
+    n, h, kv = 64, 2, 1
+    for d in (160, 192, 224):
+        q = rk.DeviceBuffer(n * h * d * 2)
+        k = rk.DeviceBuffer(n * kv * d * 2)
+        out = rk.DeviceBuffer(n * h * d * 2)
+        q.zero()
+        k.zero()
+        rc = lib.rk_attention_dev_noalloc(q.ptr, k.ptr, k.ptr, n, n, h, kv, d, 0.1, 0.0, 0, -1, 0, 0, out.ptr, None)
+        assert rc == rk.RK_E_UNSUPPORTED, d
+        # the allocating entry accepts the same call
+        assert lib.rk_attention_dev(q.ptr, k.ptr, k.ptr, n, n, h, kv, d, 0.1, 0.0, 0, -1, 0, 0, out.ptr, None) == 0
+    rk.synchronize()
