@@ -247,6 +247,26 @@ uint64_t insert(Weight w) {
   return id;
 }
 
+// The device buffers of a weight being packed, freed if the pack fails before
+// the weight is registered (register() hands them to the registry).
+struct PackGuard {
+  Weight &w;
+  bool kept = false;
+  explicit PackGuard(Weight &w_) : w(w_) {}
+  PackGuard(const PackGuard &) = delete;
+  PackGuard &operator=(const PackGuard &) = delete;
+  uint64_t register_weight() {
+    kept = true;
+    return insert(w);
+  }
+  ~PackGuard() {
+    if (kept) return;
+    void *bufs[] = {w.codes, w.scales, w.gu_codes, w.dn_codes, w.gu_scales, w.dn_scales};
+    for (void *b : bufs)
+      if (b) (void)hipFree(b);
+  }
+};
+
 int ws_stride_for(int64_t k) { return (int)round_up_i(k / 32, 4); }
 
 }  // namespace
@@ -269,6 +289,7 @@ int upload_block_scales(const std::vector<float> &blk, int64_t n, int64_t kb, fl
 
 int pack_f16_dev(const void *src_f16_dev, int64_t n, int64_t k, uint64_t *id) {
   Weight w;
+  PackGuard guard(w);
   w.kind = RK_WEIGHT_F16;
   w.n = n;
   w.k = k;
@@ -277,7 +298,7 @@ int pack_f16_dev(const void *src_f16_dev, int64_t n, int64_t k, uint64_t *id) {
   HIP_TRY(hipMemcpyAsync(w.codes, src_f16_dev, w.bytes, hipMemcpyDeviceToDevice, g_eng->stream),
           "rk_pack");
   HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack");
-  *id = insert(w);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -474,6 +495,7 @@ namespace {
 int pack_i8_host(const int8_t *codes, const std::vector<float> &block_scales, int64_t n,
                  int64_t k, int64_t group, rk_weight_id *id, const char *op) {
   Weight w;
+  PackGuard guard(w);
   w.kind = RK_WEIGHT_I8;
   w.n = n;
   w.k = k;
@@ -484,7 +506,7 @@ int pack_i8_host(const int8_t *codes, const std::vector<float> &block_scales, in
   w.ws_f16 = std::all_of(block_scales.begin(), block_scales.end(),
                          [](float d) { return (float)(_Float16)d == d; });
   w.bytes = (size_t)n * k + (size_t)n * w.ws_stride * 4;
-  *id = insert(w);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -595,9 +617,10 @@ extern "C" int rk_pack_q8_0(const uint8_t *blocks, int64_t n, int64_t k, rk_weig
   RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0"));
   CallScope cs(g_eng->stream);
   Weight wt;
+  PackGuard guard(wt);
   const int off = 0;
   RK_TRY(pack_q8_0_blocks(cs, &blocks, &off, 1, n, k, n, 16, wt, "rk_pack_q8_0"));
-  *id = insert(wt);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -607,6 +630,7 @@ extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_
   RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_f32"));
   CallScope cs(g_eng->stream);
   Weight wt;
+  PackGuard guard(wt);
   wt.kind = RK_WEIGHT_I8;
   wt.ws_f16 = true;  // GGUF Q8_0: fp16 d per block
   wt.n = n;
@@ -625,7 +649,7 @@ extern "C" int rk_pack_q8_0_f32(const float *w, int64_t n, int64_t k, rk_weight_
           "rk_pack_q8_0_f32");
   HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack_q8_0_f32");
   wt.bytes = (size_t)n * k + (size_t)n * wt.ws_stride * 4;
-  *id = insert(wt);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -644,11 +668,12 @@ extern "C" int rk_pack_q8_0_glu(const uint8_t *gate_blocks, const uint8_t *up_bl
   RK_TRY(check_i8_shape(n, k, 32, "rk_pack_q8_0_glu"));
   CallScope cs(g_eng->stream);
   Weight wt;
+  PackGuard guard(wt);
   const uint8_t *srcs[2] = {gate_blocks, up_blocks};
   const int offs[2] = {0, 16};  // gate rows at 32t + j, up rows at 32t + 16 + j
   RK_TRY(pack_q8_0_blocks(cs, srcs, offs, 2, n, k, glu_rows(n), 32, wt, "rk_pack_q8_0_glu"));
   wt.glu_n = n;
-  *id = insert(wt);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -660,6 +685,7 @@ extern "C" int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t 
   CallScope cs(g_eng->stream);
   const int64_t rows = glu_rows(n);
   Weight wt;
+  PackGuard guard(wt);
   wt.kind = RK_WEIGHT_I8;
   wt.ws_f16 = true;  // GGUF Q8_0: fp16 d per block
   wt.n = rows;
@@ -685,7 +711,7 @@ extern "C" int rk_pack_q8_0_glu_f32(const float *gate, const float *up, int64_t 
   }
   HIP_TRY(hipStreamSynchronize(g_eng->stream), "rk_pack_q8_0_glu_f32");
   wt.bytes = (size_t)rows * k + (size_t)rows * wt.ws_stride * 4;
-  *id = insert(wt);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -701,6 +727,7 @@ extern "C" int rk_pack_f16_glu(const float *gate, const float *up, int64_t n, in
   CallScope cs(g_eng->stream);
   const int64_t rows = glu_rows(n);
   Weight w;
+  PackGuard guard(w);
   w.kind = RK_WEIGHT_F16;
   w.n = rows;
   w.k = k;
@@ -715,7 +742,7 @@ extern "C" int rk_pack_f16_glu(const float *gate, const float *up, int64_t n, in
     HIP_TRY(rk_launch_f32_to_f16_rows((const float *)x32, n, k, 32, 16 * part, w.codes, cs.st), op);
   }
   HIP_TRY(hipStreamSynchronize(cs.st), op);
-  *id = insert(w);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -727,6 +754,7 @@ extern "C" int rk_pack_qat(const int8_t *codes, const float *w_scale, int64_t n,
     return fail(RK_E_SHAPE, "rk_pack_qat", "the int8 path needs K % 32 == 0");
   if (!(in_scale >= 0.f)) return fail(RK_E_SHAPE, "rk_pack_qat", "input scale must not be negative");
   Weight w;
+  PackGuard guard(w);
   w.kind = RK_WEIGHT_QAT;
   w.n = n;
   w.k = k;
@@ -738,7 +766,7 @@ extern "C" int rk_pack_qat(const int8_t *codes, const float *w_scale, int64_t n,
   HIP_TRY(hipMalloc((void **)&w.scales, (size_t)n * 4), "rk_pack_qat");
   HIP_TRY(hipMemcpy(w.scales, w_scale, (size_t)n * 4, hipMemcpyHostToDevice), "rk_pack_qat");
   w.bytes = (size_t)n * k + (size_t)n * 4;
-  *id = insert(w);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -1641,6 +1669,7 @@ extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const ui
     return fail(RK_E_SHAPE, op, "hidden and inter must be multiples of 32");
   const int64_t H = hidden, I = inter, E = n_experts;
   Weight w;
+  PackGuard guard(w);
   RK_TRY(moe_alloc(w, n_experts, H, I, op));
   CallScope cs(g_eng->stream);
   hipStream_t st = cs.st;
@@ -1664,7 +1693,7 @@ extern "C" int rk_pack_moe_q8_0(const uint8_t *gate, const uint8_t *up, const ui
             op);
   }
   HIP_TRY(hipStreamSynchronize(st), op);
-  *id = insert(w);
+  *id = guard.register_weight();
   return RK_OK;
 }
 
@@ -1676,6 +1705,7 @@ extern "C" int rk_pack_moe_f32(const float *gate, const float *up, const float *
     return fail(RK_E_SHAPE, "rk_pack_moe_f32", "hidden and inter must be multiples of 32");
   const int64_t H = hidden, I = inter, E = n_experts;
   Weight w;
+  PackGuard guard(w);
   RK_TRY(moe_alloc(w, n_experts, H, I, "rk_pack_moe_f32"));
   CallScope cs(g_eng->stream);
   void *x32;
@@ -1701,7 +1731,7 @@ extern "C" int rk_pack_moe_f32(const float *gate, const float *up, const float *
     }
   }
   HIP_TRY(hipStreamSynchronize(st), "rk_pack_moe_f32");
-  *id = insert(w);
+  *id = guard.register_weight();
   return RK_OK;
 }
 

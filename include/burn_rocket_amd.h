@@ -258,9 +258,14 @@ int rk_quantize_rows_dev(const float *x, int64_t m, int64_t k, int64_t group,
 
 /* W8A8 GEMM on device buffers against a resident I8 weight
  * (`I8Context::matmul_gw`, int8.rs:644-676): a int8 [M, K] with scales
- * a_scale [M, K/a_group]; a_group is the weight's group (reference formula
+ * a_scale [M, K/a_group]; a_group is the weight's group (the reference's
  * Σ_g (a_s·w_s)·P_g) or K (per-token: a_s[m]·Σ_g w_s[n,g]·P_g).
- * c f32 [M, N]. */
+ * c f32 [M, N]. Groups are summed in ascending order in f32 with exact int32
+ * P_g; the rounding inside each term is not the reference's two-step
+ * acc + fl(fl(a_s·w_s)·P_g): weights whose every scale is an fp16 value (GGUF
+ * Q8_0 d) fold fma(fl(P_g·d), a_s, acc), others fma(P_g, fl(a_s·w_s), acc).
+ * Both stay within 1e-5 of the largest output against the reference formula
+ * at the config-2 shapes. rk_matmul_i8_gw folds every weight the second way. */
 int rk_matmul_w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale,
                        int64_t a_group, int64_t m, int64_t k, float *c,
                        rk_stream stream);
@@ -406,7 +411,10 @@ int rk_pack_moe_f32(const float *gate, const float *up, const float *down,
  * [s, hidden] and the silu·up rows are each quantized per row per 32-value
  * group (scale max(amax/127, 1e-12), round-half-away, ±127), and every
  * product is Σ_b (a_s[m,b]·w_s[n,b])·P_b over the Q8_0 blocks b with exact
- * int32 P_b, accumulated in f32. silu(v) = v / (1 + e^-v) (src/clef/model.rs:
+ * int32 P_b, accumulated in f32 in ascending b. The gate|up product rounds
+ * each term as the reference does, acc + fl(fl(a_s·w_s)·P_b) (its results are
+ * quantized again); the down product folds fma(fl(P_b·w_s), a_s, acc), within
+ * 1e-5 of the largest value of the reference's order. silu(v) = v / (1 + e^-v) (src/clef/model.rs:
  * 491-493). ids/wts are host arrays (bucketing runs on the host,
  * engine.rs:284-313); y f32 [s, hidden] is overwritten with the sum. The
  * combine runs inside the down-projection launch: the workgroup that
