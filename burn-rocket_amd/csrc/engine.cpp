@@ -810,6 +810,29 @@ int launch_i8(const Weight &w, const int8_t *a, const float *as, int as_stride, 
   return RK_OK;
 }
 
+// One fp16 GEMM launch (glu: the gate|up epilogue form) with its split-K
+// workspace from the call's scratch: partial tiles, and arrival counters
+// zeroed when first allocated (every launch leaves them at zero).
+int gemm_f16_run(CallScope &cs, const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
+                 const char *op, int glu = 0, int64_t n_out = 0, bool out_f16 = true) {
+  const F16Plan p = rk_gemm_f16_plan((int)m, (int)n, (int)k, g_eng->num_cus, glu != 0);
+  float *part = nullptr;
+  unsigned *cnt = nullptr;
+  if (p.ksplit > 1) {
+    bool fresh = false;
+    const size_t cnt_bytes = std::max<size_t>((size_t)p.n_cnt * 4, 256);
+    RK_TRY(scratch(cs, "f16_part", (size_t)p.part_floats * 4, (void **)&part));
+    RK_TRY(scratch(cs, "f16_cnt", cnt_bytes, (void **)&cnt, &fresh));
+    if (fresh) HIP_TRY(hipMemsetAsync(cnt, 0, cnt_bytes, cs.st), op);
+  }
+  if (glu)
+    HIP_TRY(rk_launch_gemm_f16_glu(p, a, b, c, (int)m, (int)n, (int)k, (int)n_out, glu, out_f16, part, cnt, cs.st),
+            op);
+  else
+    HIP_TRY(rk_launch_gemm_f16(p, a, b, c, (int)m, (int)n, (int)k, part, cnt, cs.st), op);
+  return RK_OK;
+}
+
 int check_m(int64_t m, int64_t k, const Weight *w, const char *op) {
   if (!w) return fail(RK_E_SHAPE, op, "weight id is not packed");
   if (m <= 0) return fail(RK_E_SHAPE, op, "M must be positive");
@@ -842,12 +865,10 @@ extern "C" int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, 
     uint16_t *a16, *c16;
     RK_TRY(scratch(cs, "mm_a16", (size_t)m * k * 2, (void **)&a16));
     RK_TRY(scratch(cs, "mm_c16", (size_t)m * n * 2, (void **)&c16));
-    compute = [=](int64_t r0, int64_t r1) {
+    compute = [=, &cs](int64_t r0, int64_t r1) {
       const int64_t rows = r1 - r0;
       HIP_TRY(rk_launch_f32_to_f16(x32 + r0 * k, a16 + r0 * k, rows * k, st), "rk_matmul");
-      HIP_TRY(rk_launch_gemm_f16(a16 + r0 * k, w->codes, c16 + r0 * n, (int)rows, (int)n, (int)k,
-                                 g_eng->num_cus, st),
-              "rk_matmul_fp16");
+      RK_TRY(gemm_f16_run(cs, a16 + r0 * k, w->codes, c16 + r0 * n, rows, n, k, "rk_matmul_fp16"));
       HIP_TRY(rk_launch_f16_to_f32(c16 + r0 * n, y32 + r0 * n, rows * n, st), "rk_matmul");
       return RK_OK;
     };
@@ -906,9 +927,7 @@ extern "C" int rk_matmul_f16(rk_weight_id id, const uint16_t *a, int64_t m, int6
   RK_TRY(scratch(cs, "mm_a16", (size_t)m * k * 2, (void **)&a16));
   RK_TRY(scratch(cs, "mm_c16", (size_t)m * n * 2, (void **)&c16));
   auto compute = [&](int64_t r0, int64_t r1) {
-    HIP_TRY(rk_launch_gemm_f16(a16 + r0 * k, w->codes, c16 + r0 * n, (int)(r1 - r0), (int)n, (int)k,
-                               g_eng->num_cus, st),
-            "rocket_matmul_fp16");
+    RK_TRY(gemm_f16_run(cs, a16 + r0 * k, w->codes, c16 + r0 * n, r1 - r0, n, k, "rocket_matmul_fp16"));
     return RK_OK;
   };
   RK_TRY(staged(cs, {{a, nullptr, a16, (size_t)k * 2, 0}}, {{nullptr, c, c16, (size_t)n * 2, 0}}, m,
@@ -1002,9 +1021,8 @@ extern "C" int rk_matmul_f16_dev(rk_weight_id id, const void *a, int64_t m, int6
     return fail(RK_E_UNSUPPORTED, "rk_matmul_f16_dev", "weight is not fp16");
   if (w->glu_n > 0)
     return fail(RK_E_UNSUPPORTED, "rk_matmul_f16_dev", "gate|up weight: use rk_matmul_f16_glu_dev");
-  HIP_TRY(rk_launch_gemm_f16(a, w->codes, c, (int)m, (int)w->n, (int)k, g_eng->num_cus,
-                             pick(stream)),
-          "rk_matmul_f16_dev");
+  CallScope cs(pick(stream));
+  RK_TRY(gemm_f16_run(cs, a, w->codes, c, m, w->n, k, "rk_matmul_f16_dev"));
   g_eng->calls++;
   return RK_OK;
 }
@@ -1019,9 +1037,8 @@ extern "C" int rk_matmul_f16_glu_dev(rk_weight_id id, const void *a, int64_t m, 
   if (w->kind != RK_WEIGHT_F16 || w->moe || w->glu_n <= 0)
     return fail(RK_E_UNSUPPORTED, op, "weight was not packed by rk_pack_f16_glu");
   if (glu != RK_GLU_SILU && glu != RK_GLU_GELU) return fail(RK_E_SHAPE, op, "unknown glu kind");
-  HIP_TRY(rk_launch_gemm_f16_glu(a, w->codes, out, (int)m, (int)w->n, (int)k, (int)w->glu_n, glu,
-                                 out_f16 != 0, g_eng->num_cus, pick(stream)),
-          op);
+  CallScope cs(pick(stream));
+  RK_TRY(gemm_f16_run(cs, a, w->codes, out, m, w->n, k, op, glu, w->glu_n, out_f16 != 0));
   g_eng->calls++;
   return RK_OK;
 }

@@ -28,6 +28,14 @@
 //     register sets).
 //   * The MFMA computes Cᵀ tiles (B fragment as the A operand), so a lane
 //     holds four consecutive columns of one row of C: 8-byte stores.
+//   * Split-K (ksplit > 1): the K stages of a tile are divided between
+//     ksplit workgroups. Each stores its f32 partial tile with device-coherent
+//     (sc1) 16-byte stores and counts its arrival; the workgroup that arrives
+//     last sums the partials in split order (0, 1, ...: the result does not
+//     depend on which finishes last), resets the count and runs the epilogue.
+//     No workgroup waits for another. Grids that fill less than a round of
+//     the CUs, or whose tiles are too small to keep the MFMAs fed from LDS,
+//     trade the partials' traffic for more and larger tiles.
 #include <algorithm>
 
 #include "common.hpp"
@@ -61,7 +69,8 @@ __device__ __forceinline__ float f16_glu(float g, float u) {
 template <int BM, int BN, int WM, int WN, int ST, int MINW, int GLU = 0, bool OUT_F16 = true>
 __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
     const f16 *__restrict__ A, const f16 *__restrict__ B, void *__restrict__ Cv, int M, int N, int K,
-    int tiles_m, int tiles_n, int group_m, int n_out) {
+    int tiles_m, int tiles_n, int group_m, int n_out, int ksplit, float *__restrict__ part,
+    unsigned *__restrict__ cnt) {
   constexpr int NW = WM * WN;
   constexpr int STAGE = (BM + BN) * ROWB;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -82,9 +91,16 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int tm, tn;
-  tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, group_m, tm, tn);
+  // Split kj of tile `tile`: consecutive workgroup ids (one XCD's run) take
+  // consecutive tiles of one split, so an XCD's L2 holds one K range of them.
+  const int n_tiles = tiles_m * tiles_n;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int kj = bid / n_tiles, tile = bid - kj * n_tiles;
+  tile_coords(tile, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = (K + KS - 1) / KS;  // stages
+  const int KT_ALL = (K + KS - 1) / KS;
+  const int s_begin = (int)((int64_t)KT_ALL * kj / ksplit);
+  const int KT = (int)((int64_t)KT_ALL * (kj + 1) / ksplit) - s_begin;  // stages of this split
 
   const rsrc_t ra = make_rsrc(A + (size_t)m0 * K, (int64_t)min(M - m0, BM) * K * 2);
   const rsrc_t rb = make_rsrc(B + (size_t)n0 * K, (int64_t)min(N - n0, BN) * K * 2);
@@ -101,7 +117,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   // stage reads), which keeps the loop body free of branches.
   auto issue = [&](int s) {
     uint8_t *sb = smem + (s % ST) * STAGE;
-    const int k0 = s * KS;
+    const int k0 = (s_begin + s) * KS;
     const bool past = s >= KT;
     const uint32_t v0 = (past || (ktail && k0 + lch * 8 >= K)) ? OOB_OFFSET : voff0;
     static_for<L>([&](auto i_c) {
@@ -194,6 +210,59 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   }
   WAIT_VMCNT(0);  // no copy may still be writing LDS when the workgroup ends
 
+  if (ksplit > 1) {
+    // Partial slot of split j: [wave][tile u][lane] 16-byte entries.
+    constexpr int SC1 = 16;  // cache policy bit: device scope
+    constexpr uint32_t SLOT = (uint32_t)BM * BN * 4;
+    const rsrc_t rp = make_rsrc(part + (size_t)tile * ksplit * BM * BN, (int64_t)ksplit * SLOT);
+    const uint32_t lane_off = (uint32_t)((wave * T * 64 + lane) * 16);
+    static_for<T>([&](auto u_c) {
+      constexpr int U = decltype(u_c)::value, I = U / TN, J = U % TN;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, acc[I][J]), rp,
+                                             lane_off + (uint32_t)kj * SLOT + U * 1024, 0, SC1);
+    });
+    WAIT_VMCNT(0);  // the partial is stored before the arrival count
+    WAIT_LGKMCNT0();
+    BARRIER();  // every LDS read of the stages is done: the first word is free
+    unsigned *flag = (unsigned *)smem;
+    if (threadIdx.x == 0) {
+      const unsigned prev = atomicAdd(cnt + tile, 1u);
+      const unsigned last = prev == (unsigned)(ksplit - 1);
+      if (last) atomicExch(cnt + tile, 0u);  // every split is in: reset for the next launch
+      *flag = last;
+      WAIT_LGKMCNT0();
+    }
+    BARRIER();
+    if (!*flag) return;
+    // The sum runs in split order: sum = p0 + p1 + ... (this split's own
+    // partial from its registers); each split's loads are all issued before
+    // the first add.
+    floatx4 sum[TM][TN];
+    for (int i = 0; i < ksplit; ++i) {
+      floatx4 v[TM][TN];
+      if (i == kj) {
+        static_for<T>([&](auto u_c) {
+          constexpr int U = decltype(u_c)::value, I = U / TN, J = U % TN;
+          v[I][J] = acc[I][J];
+        });
+      } else {
+        static_for<T>([&](auto u_c) {
+          constexpr int U = decltype(u_c)::value, I = U / TN, J = U % TN;
+          v[I][J] = __builtin_bit_cast(
+              floatx4, __builtin_amdgcn_raw_buffer_load_b128(rp, lane_off + (uint32_t)i * SLOT + U * 1024, 0, SC1));
+        });
+      }
+      static_for<T>([&](auto u_c) {
+        constexpr int U = decltype(u_c)::value, I = U / TN, J = U % TN;
+        sum[I][J] = i == 0 ? v[I][J] : sum[I][J] + v[I][J];
+      });
+    }
+    static_for<T>([&](auto u_c) {
+      constexpr int U = decltype(u_c)::value, I = U / TN, J = U % TN;
+      acc[I][J] = sum[I][J];
+    });
+  }
+
   // Epilogue: lane holds C[row lane%16][cols 4·(lane/16) + 0..3] of each tile.
   if constexpr (GLU != 0) {
     static_assert(TN % 2 == 0 && WTN % 32 == 0, "gate/up tile pairs start at 32-row groups");
@@ -258,7 +327,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
 
 template <int BM, int BN, int WM, int WN, int ST, int MINW, int GLU = 0, bool OUT_F16 = true>
 static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, void *C, int M, int N, int K,
-                                  hipStream_t st, int n_out = 0) {
+                                  int ksplit, float *part, unsigned *cnt, hipStream_t st, int n_out = 0) {
   constexpr int smem = ST * (BM + BN) * ROWB;
   static_assert(smem <= 160 * 1024, "LDS per workgroup");
   auto kern = gemm_f16_kernel<BM, BN, WM, WN, ST, MINW, GLU, OUT_F16>;
@@ -274,8 +343,8 @@ static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, void *C, int M, in
   // run of consecutive tiles then shares a few A row-blocks instead of
   // streaming all of A (vision fc2 2394x4304x1152: 40.6 -> 37.3 us on MI355X,
   // 185 MB fetched per launch row-fastest over the whole grid).
-  hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, A, B, C, M, N, K, tm, tn,
-                     rk_knob("RK_TILE_GROUP_M", 3), n_out);
+  hipLaunchKernelGGL(kern, dim3(tm * tn * ksplit), dim3(WM * WN * 64), smem, st, A, B, C, M, N, K, tm, tn,
+                     rk_knob("RK_TILE_GROUP_M", 3), n_out, ksplit, part, cnt);
   return hipGetLastError();
 }
 
@@ -293,31 +362,36 @@ constexpr F16Cfg F16_CFGS[] = {
     {256, 128, 1, .40f}, {192, 192, 1, .38f}, {128, 128, 1, .32f}, {128, 64, 2, .26f},
     {64, 64, 2, .27f},   {128, 256, 1, .41f}, {96, 128, 1, .27f},  {128, 192, 1, .34f},
     {192, 128, 1, .35f}, {64, 128, 2, .25f},  {192, 192, 1, .41f}, {192, 192, 1, .42f},
-    {128, 128, 1, .33f}, {128, 192, 1, .36f}, {192, 128, 1, .37f}, {128, 192, 2, .44f},
-    {192, 128, 2, .44f},
+    {128, 128, 1, .33f}, {128, 192, 1, .36f}, {192, 128, 1, .42f}, {128, 192, 2, .36f},
+    {192, 128, 2, .36f}, {128, 96, 1, .27f},  {128, 96, 2, .22f},  {128, 128, 2, .30f},
+    {96, 128, 2, .22f},
 };
 constexpr int N_F16_CFGS = sizeof(F16_CFGS) / sizeof(F16_CFGS[0]);
 
-hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, int K,
-                      hipStream_t st) {
+hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, int K, int ks, float *part,
+                      unsigned *cnt, hipStream_t st) {
   switch (c) {
-    case 0: return launch_gemm_f16<256, 128, 4, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 1: return launch_gemm_f16<192, 192, 2, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 2: return launch_gemm_f16<128, 128, 2, 2, 4, 2>(a, b, d, M, N, K, st);
-    case 3: return launch_gemm_f16<128, 64, 2, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 4: return launch_gemm_f16<64, 64, 2, 2, 4, 2>(a, b, d, M, N, K, st);
-    case 5: return launch_gemm_f16<128, 256, 2, 4, 3, 2>(a, b, d, M, N, K, st);
-    case 6: return launch_gemm_f16<96, 128, 2, 2, 4, 2>(a, b, d, M, N, K, st);
-    case 7: return launch_gemm_f16<128, 192, 2, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 8: return launch_gemm_f16<192, 128, 2, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 9: return launch_gemm_f16<64, 128, 2, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 10: return launch_gemm_f16<192, 192, 2, 4, 3, 2>(a, b, d, M, N, K, st);
-    case 11: return launch_gemm_f16<192, 192, 4, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 12: return launch_gemm_f16<128, 128, 2, 4, 4, 2>(a, b, d, M, N, K, st);
-    case 13: return launch_gemm_f16<128, 192, 2, 4, 3, 2>(a, b, d, M, N, K, st);
-    case 14: return launch_gemm_f16<192, 128, 4, 2, 3, 2>(a, b, d, M, N, K, st);
-    case 15: return launch_gemm_f16<128, 192, 2, 4, 2, 2>(a, b, d, M, N, K, st);
-    case 16: return launch_gemm_f16<192, 128, 4, 2, 2, 2>(a, b, d, M, N, K, st);
+    case 0: return launch_gemm_f16<256, 128, 4, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 1: return launch_gemm_f16<192, 192, 2, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 2: return launch_gemm_f16<128, 128, 2, 2, 4, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 3: return launch_gemm_f16<128, 64, 2, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 4: return launch_gemm_f16<64, 64, 2, 2, 4, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 5: return launch_gemm_f16<128, 256, 2, 4, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 6: return launch_gemm_f16<96, 128, 2, 2, 4, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 7: return launch_gemm_f16<128, 192, 2, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 8: return launch_gemm_f16<192, 128, 2, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 9: return launch_gemm_f16<64, 128, 2, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 10: return launch_gemm_f16<192, 192, 2, 4, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 11: return launch_gemm_f16<192, 192, 4, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 12: return launch_gemm_f16<128, 128, 2, 4, 4, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 13: return launch_gemm_f16<128, 192, 2, 4, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 14: return launch_gemm_f16<192, 128, 4, 2, 3, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 15: return launch_gemm_f16<128, 192, 2, 4, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 16: return launch_gemm_f16<192, 128, 4, 2, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 17: return launch_gemm_f16<128, 96, 2, 2, 4, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 18: return launch_gemm_f16<128, 96, 2, 2, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 19: return launch_gemm_f16<128, 128, 2, 2, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 20: return launch_gemm_f16<96, 128, 2, 2, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
   }
   return hipErrorInvalidValue;
 }
@@ -326,65 +400,91 @@ hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, i
 // multiple of 32), the ones the glue epilogue is instantiated for.
 constexpr int F16_GLU_CFGS[] = {0, 1, 2, 3, 4, 8};
 
-// Choose the configuration with the least estimated time: rounds of
-// workgroups over the CUs, each round a fixed ~3 us (launch, pipeline fill,
-// output store) plus the work of the tiles one CU holds at that tile's
-// sustained MFMA efficiency. glu: only the glue-epilogue configurations.
-int choose_cfg(int M, int N, int K, int num_cus, bool glu = false) {
-  int best = 4;
-  double best_t = 1e300;
-  for (int c = 0; c < N_F16_CFGS; ++c) {
-    if (glu && std::find(std::begin(F16_GLU_CFGS), std::end(F16_GLU_CFGS), c) == std::end(F16_GLU_CFGS))
-      continue;
-    const F16Cfg &f = F16_CFGS[c];
-    const long tiles = ((M + f.bm - 1) / f.bm) * (long)((N + f.bn - 1) / f.bn);
-    const long slots = (long)num_cus * f.per_cu;
-    const long rounds = (tiles + slots - 1) / slots;
-    const long held = std::min<long>(f.per_cu, (tiles + num_cus - 1) / num_cus);
-    const double t = rounds * (3e-6 + held * 2.0 * f.bm * f.bn * K / (9.83e12 * f.eff));
-    if (t < best_t) {
-      best_t = t;
-      best = c;
-    }
-  }
-  return best;
+// Estimated time of configuration c with its K stages split over ks
+// workgroups: rounds of workgroups over the CUs, each round a fixed ~3 us
+// (launch, pipeline fill, output store) plus the work of the tiles one CU
+// holds at that tile's sustained MFMA efficiency; a split adds its partial
+// tiles' store and load (~1 us plus their bytes at ~10 TB/s). The split
+// term is optimistic: measured on MI355X, splits cost 5-20 us more than this
+// on the 512x1024x3072 and vision-layer shapes and won only on fc2
+// (2394x4304x1152: 36.7 us split in two against 37.9 us), so the chooser
+// only considers them when RK_F16_KSPLIT asks for one.
+double cfg_time(int c, int ks, int M, int N, int K, int num_cus) {
+  const F16Cfg &f = F16_CFGS[c];
+  const long tiles = ((M + f.bm - 1) / f.bm) * (long)((N + f.bn - 1) / f.bn);
+  const long wgs = tiles * ks;
+  const long slots = (long)num_cus * f.per_cu;
+  const long rounds = (wgs + slots - 1) / slots;
+  const long held = std::min<long>(f.per_cu, (wgs + num_cus - 1) / num_cus);
+  double t = rounds * (3e-6 + held * 2.0 * f.bm * f.bn * ((double)K / ks) / (9.83e12 * f.eff));
+  if (ks > 1) t += 1e-6 + (double)wgs * f.bm * f.bn * 4 * 2 / 10e12;
+  return t;
 }
 }  // namespace
 
-hipError_t rk_launch_gemm_f16(const void *A, const void *B, void *C, int M, int N, int K,
-                              int num_cus, hipStream_t st) {
-  const int c = rk_knob("RK_F16_TILE", -1);
-  return launch_cfg(c >= 0 && c < N_F16_CFGS ? c : choose_cfg(M, N, K, num_cus), (const f16 *)A,
-                    (const f16 *)B, (f16 *)C, M, N, K, st);
+F16Plan rk_gemm_f16_plan(int M, int N, int K, int num_cus, bool glu) {
+  const int stages = (K + KS - 1) / KS;
+  int cfg = rk_knob("RK_F16_TILE", -1);
+  const bool cfg_ok = cfg >= 0 && cfg < N_F16_CFGS &&
+                      (!glu || std::find(std::begin(F16_GLU_CFGS), std::end(F16_GLU_CFGS), cfg) !=
+                                   std::end(F16_GLU_CFGS));
+  int ks = rk_knob("RK_F16_KSPLIT", 1);
+  if (ks > stages) ks = stages;
+  F16Plan p;
+  double best = 1e300;
+  for (int c = 0; c < N_F16_CFGS; ++c) {
+    if (cfg_ok && c != cfg) continue;
+    if (glu && std::find(std::begin(F16_GLU_CFGS), std::end(F16_GLU_CFGS), c) == std::end(F16_GLU_CFGS))
+      continue;
+    for (int s = 1; s <= 4 && s <= stages; ++s) {
+      if (ks >= 1 && s != ks) continue;
+      const double t = cfg_time(c, s, M, N, K, num_cus);
+      if (t < best) {
+        best = t;
+        p.cfg = c;
+        p.ksplit = s;
+      }
+    }
+  }
+  if (p.ksplit > 1) {
+    const F16Cfg &f = F16_CFGS[p.cfg];
+    const int64_t tiles = (int64_t)((M + f.bm - 1) / f.bm) * ((N + f.bn - 1) / f.bn);
+    p.part_floats = tiles * p.ksplit * f.bm * f.bn;
+    p.n_cnt = tiles;
+  }
+  return p;
+}
+
+hipError_t rk_launch_gemm_f16(const F16Plan &p, const void *A, const void *B, void *C, int M, int N, int K,
+                              float *part, unsigned *cnt, hipStream_t st) {
+  return launch_cfg(p.cfg, (const f16 *)A, (const f16 *)B, (f16 *)C, M, N, K, p.ksplit, part, cnt, st);
 }
 
 namespace {
 template <int GLU, bool OUT_F16>
-hipError_t launch_glu_cfg(int c, const f16 *a, const f16 *b, void *d, int M, int N, int K, int n_out,
-                          hipStream_t st) {
+hipError_t launch_glu_cfg(int c, const f16 *a, const f16 *b, void *d, int M, int N, int K, int n_out, int ks,
+                          float *part, unsigned *cnt, hipStream_t st) {
   switch (c) {
-    case 0: return launch_gemm_f16<256, 128, 4, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
-    case 1: return launch_gemm_f16<192, 192, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
-    case 2: return launch_gemm_f16<128, 128, 2, 2, 4, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
-    case 3: return launch_gemm_f16<128, 64, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
-    case 4: return launch_gemm_f16<64, 64, 2, 2, 4, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
-    case 8: return launch_gemm_f16<192, 128, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, st, n_out);
+    case 0: return launch_gemm_f16<256, 128, 4, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
+    case 1: return launch_gemm_f16<192, 192, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
+    case 2: return launch_gemm_f16<128, 128, 2, 2, 4, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
+    case 3: return launch_gemm_f16<128, 64, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
+    case 4: return launch_gemm_f16<64, 64, 2, 2, 4, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
+    case 8: return launch_gemm_f16<192, 128, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
   }
   return hipErrorInvalidValue;
 }
 }  // namespace
 
-hipError_t rk_launch_gemm_f16_glu(const void *A, const void *B, void *C, int M, int N, int K,
-                                  int n_out, int glu, bool out_f16, int num_cus, hipStream_t st) {
-  int c = rk_knob("RK_F16_TILE", -1);
-  if (std::find(std::begin(F16_GLU_CFGS), std::end(F16_GLU_CFGS), c) == std::end(F16_GLU_CFGS))
-    c = choose_cfg(M, N, K, num_cus, true);
+hipError_t rk_launch_gemm_f16_glu(const F16Plan &p, const void *A, const void *B, void *C, int M, int N, int K,
+                                  int n_out, int glu, bool out_f16, float *part, unsigned *cnt, hipStream_t st) {
   const f16 *a = (const f16 *)A, *b = (const f16 *)B;
+  const int c = p.cfg, ks = p.ksplit;
   if (glu == 1)
-    return out_f16 ? launch_glu_cfg<1, true>(c, a, b, C, M, N, K, n_out, st)
-                   : launch_glu_cfg<1, false>(c, a, b, C, M, N, K, n_out, st);
+    return out_f16 ? launch_glu_cfg<1, true>(c, a, b, C, M, N, K, n_out, ks, part, cnt, st)
+                   : launch_glu_cfg<1, false>(c, a, b, C, M, N, K, n_out, ks, part, cnt, st);
   if (glu == 2)
-    return out_f16 ? launch_glu_cfg<2, true>(c, a, b, C, M, N, K, n_out, st)
-                   : launch_glu_cfg<2, false>(c, a, b, C, M, N, K, n_out, st);
+    return out_f16 ? launch_glu_cfg<2, true>(c, a, b, C, M, N, K, n_out, ks, part, cnt, st)
+                   : launch_glu_cfg<2, false>(c, a, b, C, M, N, K, n_out, ks, part, cnt, st);
   return hipErrorInvalidValue;
 }

@@ -322,17 +322,23 @@ __device__ __forceinline__ float glu_apply(float g, float u) {
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2,
-          int GLU = GLU_NONE, bool WSF16 = false>
-__global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
+          int GLU = GLU_NONE, bool WSF16 = false, int KG = 1>
+__global__ __launch_bounds__(KG *WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     const int8_t *__restrict__ A, const float *__restrict__ AS, const int8_t *__restrict__ W,
     const float *__restrict__ WS, int ws_stride, void *__restrict__ Cout, int M, int N, int K,
     int tiles_m, int tiles_n, int group_m, int n_out, int as_stride) {
   static_assert(MODE == MODE_PER_TOKEN || MODE == MODE_PER_GROUP || MODE == MODE_RAW,
                 "per-token, per-group or raw");
-  constexpr int NW = WM * WN;
-  constexpr int NT = NW * 64;
+  constexpr int NW = WM * WN;  // waves of one K-group
+  constexpr int NT = KG * NW * 64;
   constexpr int ROWB = 128;  // K bytes of one stage row
   constexpr bool GROUPED = (MODE == MODE_PER_GROUP);
+  // KG K-groups of NW waves each: group k walks stages [k·KT, (k+1)·KT) of the
+  // tile's K range with its own LDS ring, and the groups' partial sums meet
+  // in LDS at the end (group 0's first). A tile then keeps 4·KG waves per
+  // SIMD busy on its own, which is what a lone workgroup (a grid of about
+  // one tile per CU, or the last round of a larger one) lacks.
+  static_assert(KG == 1 || !GROUPED, "K-groups: per-token and raw modes");
   constexpr bool SCALED = (MODE == MODE_PER_TOKEN) || GROUPED;
   constexpr int CODE_BYTES = (BM + BN) * ROWB;
   constexpr int WS_BYTES = SCALED ? BN * 16 : 0;
@@ -359,17 +365,23 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   static_assert(!GROUPED || TM == 1, "per-group mode: one row of 32x32 tiles per wave");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  float *s_as = (float *)(smem + STAGES * STAGE_BYTES);  // [BM] per-token activation scales
-  uint8_t *s_asg = smem + STAGES * STAGE_BYTES;          // per-group ring (GROUPED)
+  float *s_as = (float *)(smem + KG * STAGES * STAGE_BYTES);  // [BM] per-token activation scales
+  uint8_t *s_asg = smem + STAGES * STAGE_BYTES;               // per-group ring (GROUPED)
 
   const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave_all / NW;    // K-group
+  const int wave = wave_all % NW;   // wave within its K-group
+  uint8_t *const gsm = smem + grp * STAGES * STAGE_BYTES;  // the group's LDS ring
   int tm, tn;
   tile_coords(xcd_remap(blockIdx.x, gridDim.x), tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = (K + 127) / 128;
+  // Stages (128 K-values) of this group; with KG > 1 the host guarantees
+  // K % (128·KG) == 0, so each group has KT whole stages.
+  const int KT = ((K + 127) / 128) / KG;
+  const int kt0 = grp * KT;  // the group's first stage
   const int KB = K / 32;
-  const int NBLK = KB;  // blocks the main loop steps through
+  const int NBLK = KG == 1 ? KB : 4 * KT;  // blocks the main loop steps through
 
   const rsrc_t ra = make_rsrc(A + (size_t)m0 * K, (int64_t)(M - m0) * K);
   const rsrc_t rw = make_rsrc(W + (size_t)n0 * K, (int64_t)(N - n0) * K);
@@ -396,8 +408,8 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
 
   auto issue = [&](auto slot_c, int kt) {
     constexpr int slot = decltype(slot_c)::value;
-    uint8_t *sb = smem + slot * STAGE_BYTES;
-    const uint32_t k0 = kt * 128;
+    uint8_t *sb = gsm + slot * STAGE_BYTES;
+    const uint32_t k0 = (kt0 + kt) * 128;
 #pragma unroll
     for (int i = 0; i < CP; ++i) {
       const int q = wave + i * NW;  // wave-uniform
@@ -411,7 +423,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
     }
     if constexpr (WS_INS > 0) {
       if (wave < WS_INS)
-        bdma16(rs, sb + CODE_BYTES + wave * 1024, voff_ws, wave * 64 * ws_stride * 4 + kt * 16);
+        bdma16(rs, sb + CODE_BYTES + wave * 1024, voff_ws, wave * 64 * ws_stride * 4 + (kt0 + kt) * 16);
     }
     if constexpr (AS_INS > 0) {
       // from the last wave down, away from the waves that copy weight scales
@@ -475,7 +487,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
   auto load_frags = [&](auto buf_c, auto slot_c, auto b_c) {
     constexpr int buf = decltype(buf_c)::value, slot = decltype(slot_c)::value,
                   b = decltype(b_c)::value;
-    const uint8_t *base = smem + slot * STAGE_BYTES;
+    const uint8_t *base = gsm + slot * STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < TM; ++i) af[buf][i] = *(const intx4 *)(base + a_off[b] + i * 32 * ROWB);
 #pragma unroll
@@ -629,6 +641,47 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
       fold(ic<0>{}, ic<TM - 1>{}, ic<TN - 1>{}, dpend, as_pend);
   }
 
+  if constexpr (KG > 1) {
+    // Group 1 hands its partial sums to group 0 through LDS ([wave][tile]
+    // [element][lane], lane-contiguous 4-byte words: conflict-free), and
+    // group 0 adds them to its own: (first half of K) + (second half).
+    static_assert(KG == 2, "two K-groups");
+    static_assert(NW * T * 16 * 64 * 4 <= KG * STAGES * STAGE_BYTES, "exchange fits the rings");
+    WAIT_VMCNT(0);
+    WAIT_LGKMCNT0();
+    BARRIER();  // every wave is past its last read of the rings
+    float *xf = (float *)smem + wave * (T * 16 * 64) + lane;
+    if (grp == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int u = (i * TN + j) * 16 + r;
+            if constexpr (MODE == MODE_RAW)
+              xf[u * 64] = __int_as_float(iacc[i][j][r]);
+            else
+              xf[u * 64] = facc[i][j][r];
+          }
+    }
+    WAIT_LGKMCNT0();
+    BARRIER();
+    if (grp == 1) return;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int u = (i * TN + j) * 16 + r;
+          if constexpr (MODE == MODE_RAW)
+            iacc[i][j][r] += __float_as_int(xf[u * 64]);
+          else
+            facc[i][j][r] = facc[i][j][r] + xf[u * 64];
+        }
+  }
+
   // Epilogue: lane holds rows 8·(r/4) + 4·(lane/32) + r%4 of column lane%32.
   // f32 and int32 outputs use non-temporal stores: written through rather than left
   // dirty in L2 for the end-of-kernel write-back (MI355X, M=3633 up / down
@@ -684,13 +737,14 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_i8_q8_kernel(
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES, int MODE, bool OUT_F16, int MINW = 2,
-          int GLU = GLU_NONE, bool WSF16 = false>
+          int GLU = GLU_NONE, bool WSF16 = false, int KG = 1>
 static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   constexpr bool SCALED = MODE == MODE_PER_TOKEN || MODE == MODE_PER_GROUP;
-  constexpr int smem = STAGES * ((BM + BN) * 128 + (SCALED ? BN * 16 : 0)) +
+  constexpr int smem = KG * STAGES * ((BM + BN) * 128 + (SCALED ? BN * 16 : 0)) +
                        (MODE == MODE_PER_GROUP ? (STAGES + 1) * BM * 16 : BM * 4);
   static_assert(smem <= 160 * 1024, "LDS");
-  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16, MINW, GLU, WSF16>;
+  if (KG > 1 && g.K % (128 * KG) != 0) return hipErrorInvalidValue;
+  auto kern = gemm_i8_q8_kernel<BM, BN, WM, WN, STAGES, MODE, OUT_F16, MINW, GLU, WSF16, KG>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -703,7 +757,7 @@ static hipError_t launch_q8(const I8GemmArgs &g, hipStream_t st) {
   // of consecutive tiles re-reads a few A row blocks from its L2 instead of
   // streaming all of A (M=3633 down-projection: 108 MB fetched per launch
   // row-fastest over the whole grid; 3-4 % faster on both projections).
-  hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(WM * WN * 64), smem, st, g.A, g.AS, g.W, g.WS,
+  hipLaunchKernelGGL(kern, dim3(tm * tn), dim3(KG * WM * WN * 64), smem, st, g.A, g.AS, g.W, g.WS,
                      g.ws_stride, g.C, g.M, g.N, g.K, tm, tn, rk_knob("RK_TILE_GROUP_M", 8),
                      GLU != GLU_NONE ? g.n_out : g.N, g.as_stride);
   return hipGetLastError();
@@ -779,6 +833,15 @@ static hipError_t launch_q8_cfg(const I8GemmArgs &g, hipStream_t st) {
       return launch_q8<128, 256, 4, 4, 2, MODE_PER_TOKEN, OUT_F16, 4>(g, st);
     case 23:
       return launch_q8<128, 128, 2, 4, 3, MODE_PER_TOKEN, OUT_F16, 2>(g, st);
+    // two K-groups per workgroup (K % 256 == 0)
+    case 24:
+      return launch_q8<128, 128, 2, 4, 2, MODE_PER_TOKEN, OUT_F16, 4, GLU_NONE, false, 2>(g, st);
+    case 25:
+      return launch_q8<128, 128, 2, 2, 2, MODE_PER_TOKEN, OUT_F16, 2, GLU_NONE, false, 2>(g, st);
+    case 26:
+      return launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, OUT_F16, 2, GLU_NONE, false, 2>(g, st);
+    case 27:
+      return launch_q8<64, 128, 2, 2, 2, MODE_PER_TOKEN, OUT_F16, 2, GLU_NONE, false, 2>(g, st);
     default:
       return launch_q8<128, 64, 2, 2, 2, MODE_PER_TOKEN, OUT_F16>(g, st);
   }
@@ -847,6 +910,8 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
       }
       return dispatch_scaled<MODE_PER_GROUP>(g, st);
     case I8_RAW:
+      if (rk_knob("RK_Q8_RAW_TILE", 0) == 1 && g.K % 256 == 0)
+        return launch_q8<128, 128, 2, 2, 2, MODE_RAW, false, 2, GLU_NONE, false, 2>(g, st);
       return launch_q8<128, 128, 2, 2, 2, MODE_RAW, false>(g, st);
     case I8_PARTIALS:
       return launch_i8<64, 64, 2, 2, 4, MODE_PARTIALS, false, true>(g, st);

@@ -15,16 +15,25 @@ static inline int rk_knob(const char *name, int dflt) {
   return (end && *end == 0) ? (int)x : dflt;
 }
 
+// fp16 GEMM launch plan: tile configuration, K split and the split's
+// workspace (f32 partial tiles, arrival counters that start at zero and are
+// left at zero by every launch).
+struct F16Plan {
+  int cfg = 4, ksplit = 1;
+  int64_t part_floats = 0;
+  int64_t n_cnt = 0;
+};
+F16Plan rk_gemm_f16_plan(int M, int N, int K, int num_cus, bool glu);
 // fp16 GEMM, C[M,N] = A[M,K]·B[N,K]ᵀ, K % 8 == 0.
-hipError_t rk_launch_gemm_f16(const void *A, const void *B, void *C, int M, int N, int K,
-                              int num_cus, hipStream_t st);
+hipError_t rk_launch_gemm_f16(const F16Plan &p, const void *A, const void *B, void *C, int M, int N, int K,
+                              float *part, unsigned *cnt, hipStream_t st);
 
 // fp16 GEMM with a gate|up glue epilogue: B [N, K] holds gate and up rows
 // interleaved per 16 (N = 32·ceil(n_out/16)); C [M, n_out] = glue(gate·a,
 // up·a) with both products rounded to fp16 first; glu 1 silu·up, 2 gelu·up;
-// C f32 or (out_f16) fp16.
-hipError_t rk_launch_gemm_f16_glu(const void *A, const void *B, void *C, int M, int N, int K,
-                                  int n_out, int glu, bool out_f16, int num_cus, hipStream_t st);
+// C f32 or (out_f16) fp16. p from rk_gemm_f16_plan(.., glu = true).
+hipError_t rk_launch_gemm_f16_glu(const F16Plan &p, const void *A, const void *B, void *C, int M, int N, int K,
+                                  int n_out, int glu, bool out_f16, float *part, unsigned *cnt, hipStream_t st);
 // Element type conversion (RK_DTYPE_* src → dst), round to nearest even.
 hipError_t rk_launch_cast(const void *x, int src, void *y, int dst, int64_t n, hipStream_t st);
 // f32 rows [n, k] → fp16 (RNE) rows (r/16)·grp_stride + grp_off + r%16 of out.

@@ -140,12 +140,13 @@ def test_shape_errors_are_reported(rk):
 # Every tile configuration of the fp16 kernel (RK_F16_TILE): ragged M and N,
 # a K tail inside a 64-value stage, and K of one and two stages (fewer stages
 # than the pipeline prologue issues).
-F16_TILES = list(range(17))
+F16_TILES = list(range(21))
 
 
 @pytest.mark.parametrize("tile", F16_TILES)
 def test_gemm_f16_every_tile_config(rk, orc, tile, monkeypatch):
     monkeypatch.setenv("RK_F16_TILE", str(tile))
+    monkeypatch.setenv("RK_F16_KSPLIT", "1")
     for m, k, n in ((300, 424, 200), (257, 1024, 392), (70, 64, 130), (129, 128, 260)):
         note(f"fp16 GEMM RK_F16_TILE={tile} m={m} k={k} n={n}")
         r = np.random.default_rng(tile * 13 + m + k + n)
@@ -153,3 +154,50 @@ def test_gemm_f16_every_tile_config(rk, orc, tile, monkeypatch):
         b = (r.standard_normal((n, k)) * 0.05).astype(np.float16)
         got = run_f16(rk, rk.pack(b), a, n)
         check(orc, got, orc.gemm_f16(a, b))
+
+
+# Split-K: a tile's K stages over 2, 3 or 4 workgroups whose f32 partials the
+# last to arrive sums in split order. Every split of a shape gives the same
+# bits from call to call (the order does not depend on which finishes last),
+# and the partials' counters are left at zero (a second call is correct).
+@pytest.mark.parametrize("tile", [2, 4, 17, 18, 19, 20, 6])
+@pytest.mark.parametrize("ksplit", [2, 3, 4])
+def test_gemm_f16_split_k(rk, orc, tile, ksplit, monkeypatch):
+    monkeypatch.setenv("RK_F16_TILE", str(tile))
+    monkeypatch.setenv("RK_F16_KSPLIT", str(ksplit))
+    for m, k, n in ((300, 424, 200), (512, 1024, 3072), (70, 256, 130)):
+        note(f"fp16 GEMM split-K RK_F16_TILE={tile} ksplit={ksplit} m={m} k={k} n={n}")
+        r = np.random.default_rng(tile * 7 + ksplit + m + k + n)
+        a = r.standard_normal((m, k)).astype(np.float16)
+        b = (r.standard_normal((n, k)) * 0.05).astype(np.float16)
+        wid = rk.pack(b)
+        got = run_f16(rk, wid, a, n)
+        check(orc, got, orc.gemm_f16(a, b))
+        again = run_f16(rk, wid, a, n)
+        assert (again == got).all()
+
+
+def test_gemm_f16_split_k_glu(rk, orc, monkeypatch):
+    # The gate|up glue epilogue after a split-K sum equals the unsplit launch.
+    m, k, n = 300, 512, 200
+    r = np.random.default_rng(21)
+    x = r.standard_normal((m, k)).astype(np.float16)
+    gate = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    up = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    wid = rk.pack_f16_glu(gate, up)
+    lib = rk.lib()
+    da = rk.DeviceBuffer.from_array(x.view(np.uint16))
+    outs = []
+    for ks in ("1", "3"):
+        note(f"fp16 glu GEMM ksplit={ks}")
+        monkeypatch.setenv("RK_F16_TILE", "2")
+        monkeypatch.setenv("RK_F16_KSPLIT", ks)
+        do = rk.DeviceBuffer(m * n * 4)
+        assert lib.rk_matmul_f16_glu_dev(int(wid), da.ptr, m, k, rk.GLU_SILU, do.ptr, 0, None) == 0, lib.rk_last_error()
+        rk.synchronize()
+        outs.append(do.download((m, n), np.float32))
+    g = orc.gemm_f16(x, gate.astype(np.float16)).astype(np.float16).astype(np.float32)
+    u = orc.gemm_f16(x, up.astype(np.float16)).astype(np.float16).astype(np.float32)
+    ref = orc.silu_mul(g, u)
+    for got in outs:
+        check(orc, got, ref)

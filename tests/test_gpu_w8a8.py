@@ -236,6 +236,34 @@ def test_w8a8_every_tile_config(rk, orc, tile, monkeypatch):
                 assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
+# Two K-groups per workgroup (RK_Q8_TILE 24-27; K % 256 == 0): each group
+# folds half of K in its own LDS ring and the halves meet in LDS. Ragged M and
+# N, K of two, four and twelve 128-value stages per group; the raw int32 form
+# (RK_Q8_RAW_TILE=1) stays bit-exact.
+@pytest.mark.parametrize("tile", [24, 25, 26, 27])
+def test_w8a8_k_groups(rk, orc, tile, monkeypatch):
+    monkeypatch.setenv("RK_Q8_TILE", str(tile))
+    monkeypatch.setenv("RK_Q8_RAW_TILE", "1")
+    for m, k, n in ((300, 512, 200), (257, 1024, 392), (70, 3072, 130)):
+        note(f"W8A8 K-groups RK_Q8_TILE={tile} m={m} k={k} n={n}")
+        r = np.random.default_rng(tile * 11 + m + k + n)
+        x = r.standard_normal((m, k)).astype(np.float32)
+        w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+        wq, wd = orc.q8_0_quantize(w)
+        wid = rk.pack_q8_0(orc.q8_0_blocks(wq, wd), n, k)
+        aq, a_s = orc.quantize_rows(x, k)
+        dq, ds = quantize_dev(rk, x, k)
+        ref = orc.emu_matmul_gw(aq, a_s, k, wq, wd.view(np.float16).astype(np.float32), 32)
+        for f16out in (False, True):
+            got = w8a8_dev(rk, wid, dq, ds, k, m, k, f16out)
+            check(orc, got, ref)
+            if not f16out:
+                assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+                again = w8a8_dev(rk, wid, dq, ds, k, m, k, f16out)
+                assert (again == got).all()
+        assert (raw_dev(rk, wid, aq).astype(np.int64) == orc.matmul_i8_raw(aq, wq)).all()
+
+
 @pytest.mark.parametrize("in_scale,out_scale", [(0.02, 0.0), (0.0, 0.0), (0.02, 0.05)])
 def test_qat_matmul_is_bit_exact(rk, orc, in_scale, out_scale):
     note(f"QAT in_scale={in_scale} out_scale={out_scale}")
