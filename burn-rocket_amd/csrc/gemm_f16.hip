@@ -66,7 +66,10 @@ __device__ __forceinline__ float f16_glu(float g, float u) {
 // rows), so tiles j (even) and j+1 of a lane hold gate and up of the same
 // outputs; each is rounded to fp16 as the plain GEMM's output would be, the
 // glue runs in f32, and C is [M, n_out] f32 (OUT_F16: fp16).
-template <int BM, int BN, int WM, int WN, int ST, int MINW, int GLU = 0, bool OUT_F16 = true>
+// SPLIT = false is the unsplit kernel (ksplit must be 1): the partial
+// exchange is compiled out, and with it the registers it holds.
+template <int BM, int BN, int WM, int WN, int ST, int MINW, int GLU = 0, bool OUT_F16 = true,
+          bool SPLIT = false>
 __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
     const f16 *__restrict__ A, const f16 *__restrict__ B, void *__restrict__ Cv, int M, int N, int K,
     int tiles_m, int tiles_n, int group_m, int n_out, int ksplit, float *__restrict__ part,
@@ -95,12 +98,13 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   // consecutive tiles of one split, so an XCD's L2 holds one K range of them.
   const int n_tiles = tiles_m * tiles_n;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int kj = bid / n_tiles, tile = bid - kj * n_tiles;
+  const int ks = SPLIT ? ksplit : 1;
+  const int kj = SPLIT ? bid / n_tiles : 0, tile = bid - kj * n_tiles;
   tile_coords(tile, tiles_m, tiles_n, group_m, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int KT_ALL = (K + KS - 1) / KS;
-  const int s_begin = (int)((int64_t)KT_ALL * kj / ksplit);
-  const int KT = (int)((int64_t)KT_ALL * (kj + 1) / ksplit) - s_begin;  // stages of this split
+  const int s_begin = SPLIT ? (int)((int64_t)KT_ALL * kj / ks) : 0;
+  const int KT = SPLIT ? (int)((int64_t)KT_ALL * (kj + 1) / ks) - s_begin : KT_ALL;  // stages of this split
 
   const rsrc_t ra = make_rsrc(A + (size_t)m0 * K, (int64_t)min(M - m0, BM) * K * 2);
   const rsrc_t rb = make_rsrc(B + (size_t)n0 * K, (int64_t)min(N - n0, BN) * K * 2);
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(WM *WN * 64, MINW) void gemm_f16_kernel(
   }
   WAIT_VMCNT(0);  // no copy may still be writing LDS when the workgroup ends
 
-  if (ksplit > 1) {
+  if constexpr (SPLIT) {
     // Partial slot of split j: [wave][tile u][lane] 16-byte entries.
     constexpr int SC1 = 16;  // cache policy bit: device scope
     constexpr uint32_t SLOT = (uint32_t)BM * BN * 4;
@@ -330,13 +334,14 @@ static hipError_t launch_gemm_f16(const f16 *A, const f16 *B, void *C, int M, in
                                   int ksplit, float *part, unsigned *cnt, hipStream_t st, int n_out = 0) {
   constexpr int smem = ST * (BM + BN) * ROWB;
   static_assert(smem <= 160 * 1024, "LDS per workgroup");
-  auto kern = gemm_f16_kernel<BM, BN, WM, WN, ST, MINW, GLU, OUT_F16>;
-  static bool attr_set = false;
-  if (!attr_set) {
+  auto kern = ksplit > 1 ? gemm_f16_kernel<BM, BN, WM, WN, ST, MINW, GLU, OUT_F16, true>
+                         : gemm_f16_kernel<BM, BN, WM, WN, ST, MINW, GLU, OUT_F16, false>;
+  static bool attr_set[2] = {false, false};
+  if (!attr_set[ksplit > 1]) {
     hipError_t e = hipFuncSetAttribute((const void *)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set[ksplit > 1] = true;
   }
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   // Tiles in groups of 3 tile rows (row-fastest inside a group): one XCD's

@@ -909,10 +909,18 @@ hipError_t rk_launch_gemm_i8(const I8GemmArgs &g, hipStream_t st) {
                         : (g.out_f16 ? launch_q8g<true, false>(c, g, st) : launch_q8g<false, false>(c, g, st));
       }
       return dispatch_scaled<MODE_PER_GROUP>(g, st);
-    case I8_RAW:
-      if (rk_knob("RK_Q8_RAW_TILE", 0) == 1 && g.K % 256 == 0)
+    case I8_RAW: {
+      // Two K-groups of waves per workgroup where the grid leaves a CU with
+      // one workgroup (down-projection 3633x3072->1024: 18.6 against 19.3 us);
+      // with two or more per CU the single group is faster (up-projection
+      // 3633x1024->3072: 22.0 against 24.0 us). RK_Q8_RAW_TILE: 1 forces two
+      // groups, 2 forces one.
+      const int knob = rk_knob("RK_Q8_RAW_TILE", 0);
+      const long t128 = ((g.M + 127) / 128) * (long)((g.N + 127) / 128);
+      if (g.K % 256 == 0 && (knob == 1 || (knob == 0 && t128 < g.num_cus)))
         return launch_q8<128, 128, 2, 2, 2, MODE_RAW, false, 2, GLU_NONE, false, 2>(g, st);
       return launch_q8<128, 128, 2, 2, 2, MODE_RAW, false>(g, st);
+    }
     case I8_PARTIALS:
       return launch_i8<64, 64, 2, 2, 4, MODE_PARTIALS, false, true>(g, st);
   }
