@@ -374,6 +374,121 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     const int nj_max = (n_tiles + 1) / 2;
     floatx4 sacc[NKB][2];
     half8 phi[2][NC2], plo[2][NC2];
+    const bool mix_on = a.mix != 0;
+    // Steady-state MFMA slot of 64-key tiles (MIX): the PV products of the
+    // second 32-key chunk run interleaved with the Sᵀ products of the first
+    // two 16-key blocks. Sᵀ alone reads a 1 KB K fragment per two MFMAs, which
+    // on four waves is the LDS read rate of a CU; PV reads one per four. The
+    // registers of P chunk 0 die before those of Sᵀ blocks 0-1 are born, so
+    // the mix adds no live registers. Built for head dims 72 and 80 only: on
+    // MI355X it took vision attention (S=2394, 16 heads, d72) 70.9 -> 68.7 us
+    // and made d64 and d128 5-7 % slower (causal S=3633 d128 85 -> 90 us).
+    constexpr bool MIX = NC2 == 2 && D > 64 && D <= 80;
+    constexpr int NSQ = NQC + (TAIL16 ? 1 : 0);  // K fragments per 16-key block
+    auto s_step = [&](const uint8_t *kbuf, auto c_c, auto kb_c) {
+      constexpr int c = decltype(c_c)::value, kb = decltype(kb_c)::value;
+      if constexpr (c < NQC) {
+        const half8 kfr = *(const half8 *)(kbuf + k_off[c] + kb * 16 * KROW);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr, qf[qb][c], sacc[kb][qb], 0, 0, 0);
+      } else if constexpr (TAIL16) {
+        const half4 kfr = *(const half4 *)(kbuf + k_off16 + kb * 16 * KROW);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+          sacc[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x16f16(kfr, qt16[qb], sacc[kb][qb], 0, 0, 0);
+      }
+    };
+    auto mixed_slot = [&](int j) {
+      // (1 <= j < nj) the slot's copies, as in mfma_slot
+      issue(j + 1 < nj ? kt_begin + 2 * (j + 1) + grp : -1, (j + 1) & 1, kt_begin + 2 * j + grp, j & 1);
+      const uint8_t *vb = smem + (grp * 2 + ((j - 1) & 1)) * BUF_BYTES;
+      const uint8_t *kbuf = smem + (grp * 2 + (j & 1)) * BUF_BYTES;
+      // (a) PV of chunk 0: hi of fragment f, lo of fragment f-1.
+      {
+        half8 vprev = half8{};
+        static_for<NDB + 1>([&](auto f_c) {
+          constexpr int F = decltype(f_c)::value;
+          half8 vcur = half8{};
+          if constexpr (F < NDB) {
+            vcur = *(const half8 *)(vb + v_off[0] + F * 16 * VRB);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+              o[F][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vcur, phi[qb][0], o[F][qb], 0, 0, 0);
+          }
+          if constexpr (F > 0) {
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+              o[F - 1][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vprev, plo[qb][0], o[F - 1][qb], 0, 0, 0);
+          }
+          vprev = vcur;
+        });
+        constexpr int LA_A = LAWV < NDB ? LAWV : NDB;
+        __builtin_amdgcn_sched_group_barrier(0x100, LA_A, 0);
+        static_for<NDB - LA_A>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        });
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * LA_A, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // (b) PV of chunk 1 interleaved with Sᵀ of blocks 0 and 1.
+      {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) sacc[kb][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        constexpr int NS = 2 * NSQ;                       // Sᵀ steps: (c, kb), c-major
+        constexpr int NB = (NDB + 1 > NS) ? NDB + 1 : NS;  // interleaved steps
+        half8 vprev = half8{};
+        static_for<NB>([&](auto i_c) {
+          constexpr int I = decltype(i_c)::value;
+          half8 vcur = half8{};
+          if constexpr (I < NDB) {
+            vcur = *(const half8 *)(vb + v_off[1] + I * 16 * VRB);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+              o[I][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vcur, phi[qb][1], o[I][qb], 0, 0, 0);
+          }
+          if constexpr (I > 0 && I <= NDB) {
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+              o[I - 1][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vprev, plo[qb][1], o[I - 1][qb], 0, 0, 0);
+          }
+          vprev = vcur;
+          if constexpr (I < NS) s_step(kbuf, ic<I / 2>{}, ic<I % 2>{});
+        });
+        constexpr int NRB = NDB + NS, NMB = 4 * NDB + 2 * NS;
+        constexpr int LA_B = LAW < NRB ? LAW : NRB;
+        constexpr int STEPS = (NMB / 3 < NRB - LA_B) ? NMB / 3 : NRB - LA_B;
+        __builtin_amdgcn_sched_group_barrier(0x100, LA_B, 0);
+        static_for<STEPS>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        });
+        __builtin_amdgcn_sched_group_barrier(0x008, NMB - 3 * STEPS, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // (c) Sᵀ of blocks 2 and 3.
+      {
+#pragma unroll
+        for (int kb = 2; kb < 4; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) sacc[kb][qb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        static_for<2 * NSQ>([&](auto i_c) {
+          constexpr int I = decltype(i_c)::value;
+          s_step(kbuf, ic<I / 2>{}, ic<2 + I % 2>{});
+        });
+        constexpr int NR = 2 * NSQ;
+        constexpr int LA_C = LAWK < NR ? LAWK : NR;
+        __builtin_amdgcn_sched_group_barrier(0x100, LA_C, 0);
+        static_for<NR - LA_C>([&](auto) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        });
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * LA_C, 0);
+      }
+    };
     // MFMA slot j: PV of tile j-1, Sᵀ of tile j.
     auto mfma_slot = [&](int j) {
     if (j < nj) issue(j + 1 < nj ? kt_begin + 2 * (j + 1) + grp : -1, (j + 1) & 1, kt_begin + 2 * j + grp, j & 1);
@@ -550,8 +665,25 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
     BARRIER();
     // One loop per group, so that only S (group 1) or only P (group 0) is
     // live across a loop iteration; both make 2·nj_max + 2 barriers.
+    // With MIX the slots that hold both products (1 ≤ j < nj) run in a loop
+    // of their own, so that no loop body joins two schedules of them.
     if (grp == 0) {
-      for (int j = 0; j <= nj_max; ++j) {
+      int j = 0;
+      if constexpr (MIX) {
+        if (mix_on && nj >= 2) {
+          mfma_slot(0);
+          BARRIER();
+          valu_slot(0);
+          BARRIER();
+          for (j = 1; j < nj; ++j) {
+            mixed_slot(j);
+            BARRIER();
+            valu_slot(j);
+            BARRIER();
+          }
+        }
+      }
+      for (; j <= nj_max; ++j) {
         mfma_slot(j);
         BARRIER();
         valu_slot(j);
@@ -561,7 +693,18 @@ __global__ __launch_bounds__(2 * NWG * 64, NWG == 4 ? 2 : 1) void attn_fa_kernel
       BARRIER();
       mfma_slot(0);
       BARRIER();
-      for (int j = 0; j < nj_max; ++j) {
+      int j = 0;
+      if constexpr (MIX) {
+        if (mix_on && nj >= 2) {
+          for (; j + 1 < nj; ++j) {
+            valu_slot(j);
+            BARRIER();
+            mixed_slot(j + 1);
+            BARRIER();
+          }
+        }
+      }
+      for (; j < nj_max; ++j) {
         valu_slot(j);
         BARRIER();
         mfma_slot(j + 1);
@@ -771,11 +914,15 @@ static hipError_t launch_attn_nwg(const AttnArgs &a, hipStream_t st) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
+  // RK_ATTN_MIX = 0 keeps the PV and Sᵀ products of a slot apart (kernels
+  // that have the mixed slot: head dims 72 and 80).
+  AttnArgs b = a;
+  b.mix = rk_knob("RK_ATTN_MIX", 1) != 0;
   if (a.softcap != 0.f)
-    hipLaunchKernelGGL(kern1, dim3((unsigned)grid), dim3(2 * NWG * 64), smem, st, a, G, BQ,
+    hipLaunchKernelGGL(kern1, dim3((unsigned)grid), dim3(2 * NWG * 64), smem, st, b, G, BQ,
                        n_qtiles);
   else
-    hipLaunchKernelGGL(kern0, dim3((unsigned)grid), dim3(2 * NWG * 64), smem, st, a, G, BQ,
+    hipLaunchKernelGGL(kern0, dim3((unsigned)grid), dim3(2 * NWG * 64), smem, st, b, G, BQ,
                        n_qtiles);
   return hipGetLastError();
 }

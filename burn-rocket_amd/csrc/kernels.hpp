@@ -170,6 +170,7 @@ struct AttnArgs {
   float *part;
   unsigned *cnt;
   int n_split;  // query tiles split (the first ones in dispatch order, the longest)
+  int mix;      // set by the launcher: interleave the PV and Sᵀ products of a slot
 };
 // V [n_kv, tok stride] (kv head g at column g·D) → Vt [KV][Dv_pad][n_kv_pad].
 hipError_t rk_launch_v_transpose(const void *v, int64_t v_tok_stride, int64_t v_head_stride,

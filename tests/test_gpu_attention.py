@@ -120,6 +120,33 @@ def test_192_row_tiles(rk, orc, d, h, kv, monkeypatch):
         check(orc, got, orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, softcap, mode, window))
 
 
+@pytest.mark.parametrize("d", [72, 80])
+@pytest.mark.parametrize("rows,split", [("128", "1"), ("192", "1"), ("128", "2")])
+def test_mixed_slot_equals_separate_slots(rk, orc, d, rows, split, monkeypatch):
+    """Head dims 72 and 80 run the steady-state MFMA slots with the PV and
+    Sᵀ products interleaved (RK_ATTN_MIX, default on); the sums are the same
+    MFMAs in the same order per accumulator, so the output equals the separate
+    slots bit for bit: 128- and 192-row tiles, the key split, every mask
+    mode, key ranges of one to many tiles per group (the mixed loop runs only
+    from the second tile of a group on)."""
+    monkeypatch.setenv("RK_ATTN_ROWS", rows)
+    monkeypatch.setenv("RK_ATTN_SPLIT", split)
+    r = np.random.default_rng(d + int(rows) + int(split))
+    h, kv = 8, 4
+    for n_q, n_kv, mode, window in ((300, 450, 0, -1), (300, 300, 1, -1), (200, 200, 3, 70), (130, 60, 0, -1),
+                                    (90, 130, 2, 40)):
+        note(f"mixed slot d={d} rows={rows} split={split} n_q={n_q} n_kv={n_kv} mode={mode}")
+        q = r.standard_normal((n_q, h * d)).astype(np.float16)
+        k = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+        v = r.standard_normal((n_kv, kv * d)).astype(np.float16)
+        outs = []
+        for mix in ("1", "0"):
+            monkeypatch.setenv("RK_ATTN_MIX", mix)
+            outs.append(attn_dev(rk, q, k, v, h, kv, d, d ** -0.5, mode=mode, window=window))
+        assert (outs[0] == outs[1]).all()
+        check(orc, outs[0], orc.attention_ref(q, k, v, h, kv, d, d ** -0.5, 0.0, mode, window))
+
+
 @pytest.mark.parametrize("mode,window,n_q,n_kv,q0,k0", [
     (2, 17, 200, 200, 0, 0),      # band
     (3, 33, 200, 200, 0, 0),      # causal sliding window
