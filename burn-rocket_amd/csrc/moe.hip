@@ -489,21 +489,17 @@ __global__ __launch_bounds__(NW * 64, 2) void moe_q8_kernel(
     int64_t ws_stride_e, int ws_stride, int N, int K, const float *__restrict__ row_w,
     float *__restrict__ out, int out_ld, MoeCombine cmb) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  // The column slices of one tile run on one XCD and share the tile's token
-  // rows in its L2. gate|up: consecutive tiles on one XCD. down: tile t on
-  // XCD t mod 8 (the dispatcher hands workgroup b to XCD b mod 8), so the
-  // last tiles, whose workgroups complete most tokens and run the combine's
-  // reads, are spread over all XCDs; the grid is padded to whole rounds of 8
-  // tiles and the padding workgroups exit at once.
-  int L;
-  if constexpr (GU) {
-    L = xcd_remap(blockIdx.x, gridDim.x);
-  } else {
-    const int j = blockIdx.x / 8;
-    const int t = blockIdx.x % 8 + 8 * (j / n_col_tiles);
-    if (t >= cmb.n_tiles) return;
-    L = t * n_col_tiles + j % n_col_tiles;
-  }
+  // Tile t runs on XCD t mod 8 (the dispatcher hands workgroup b to XCD
+  // b mod 8), all its column slices there, sharing the tile's token rows in
+  // that XCD's L2; each XCD takes its tiles in list order, longest first (the
+  // plan sorts them). For down this also spreads the last tiles, whose
+  // workgroups complete most tokens and run the combine's reads, over all
+  // XCDs. The grid is padded to whole rounds of 8 tiles and the padding
+  // workgroups exit at once.
+  const int jb = blockIdx.x / 8;
+  const int t = blockIdx.x % 8 + 8 * (jb / n_col_tiles);
+  if (t >= cmb.n_tiles) return;
+  const int L = t * n_col_tiles + jb % n_col_tiles;
   const MoeTile tile = tiles[L / n_col_tiles];
   const int n0 = (L % n_col_tiles) * 32 * NW;
   const int8_t *We = W + (int64_t)tile.expert * w_stride_e;
@@ -537,7 +533,7 @@ static hipError_t launch_moe_cfg(const int8_t *A, const float *AS, int as_stride
     attr_set = true;
   }
   const int n_col = (N + 32 * NW - 1) / (32 * NW);
-  const int grid = GU ? n_tiles * n_col : (n_tiles + 7) / 8 * 8 * n_col;
+  const int grid = (n_tiles + 7) / 8 * 8 * n_col;
   MoeCombine c = cmb;
   c.n_tiles = n_tiles;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * 64), smem, st, A, AS, as_stride,
