@@ -369,7 +369,7 @@ constexpr F16Cfg F16_CFGS[] = {
     {192, 128, 1, .35f}, {64, 128, 2, .25f},  {192, 192, 1, .41f}, {192, 192, 1, .42f},
     {128, 128, 1, .33f}, {128, 192, 1, .36f}, {192, 128, 1, .42f}, {128, 192, 2, .36f},
     {192, 128, 2, .36f}, {128, 96, 1, .27f},  {128, 96, 2, .22f},  {128, 128, 2, .30f},
-    {96, 128, 2, .22f},
+    {96, 128, 2, .22f},  {256, 192, 1, .42f}, {256, 192, 1, .425f},
 };
 constexpr int N_F16_CFGS = sizeof(F16_CFGS) / sizeof(F16_CFGS[0]);
 
@@ -397,6 +397,8 @@ hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, i
     case 18: return launch_gemm_f16<128, 96, 2, 2, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
     case 19: return launch_gemm_f16<128, 128, 2, 2, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
     case 20: return launch_gemm_f16<96, 128, 2, 2, 2, 2>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 21: return launch_gemm_f16<256, 192, 2, 4, 2, 1>(a, b, d, M, N, K, ks, part, cnt, st);
+    case 22: return launch_gemm_f16<256, 192, 4, 2, 2, 1>(a, b, d, M, N, K, ks, part, cnt, st);
   }
   return hipErrorInvalidValue;
 }
