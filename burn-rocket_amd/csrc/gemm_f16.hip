@@ -405,7 +405,7 @@ hipError_t launch_cfg(int c, const f16 *a, const f16 *b, f16 *d, int M, int N, i
 
 // The configurations whose waves hold whole 32-row gate|up groups (BN/WN a
 // multiple of 32), the ones the glue epilogue is instantiated for.
-constexpr int F16_GLU_CFGS[] = {0, 1, 2, 3, 4, 8};
+constexpr int F16_GLU_CFGS[] = {0, 1, 2, 3, 4, 8, 22};
 
 // Estimated time of configuration c with its K stages split over ks
 // workgroups: rounds of workgroups over the CUs, each round a fixed ~3 us
@@ -478,6 +478,7 @@ hipError_t launch_glu_cfg(int c, const f16 *a, const f16 *b, void *d, int M, int
     case 3: return launch_gemm_f16<128, 64, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
     case 4: return launch_gemm_f16<64, 64, 2, 2, 4, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
     case 8: return launch_gemm_f16<192, 128, 2, 2, 3, 2, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
+    case 22: return launch_gemm_f16<256, 192, 4, 2, 2, 1, GLU, OUT_F16>(a, b, d, M, N, K, ks, part, cnt, st, n_out);
   }
   return hipErrorInvalidValue;
 }

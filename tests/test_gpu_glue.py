@@ -168,6 +168,40 @@ def test_f16_glu_gemm(rk, orc, m, k, n, glu):
     assert lib.rk_matmul_f16_dev(int(wid), dx.ptr, m, k, rk.DeviceBuffer(m * 2 * n * 2).ptr, None) == rk.RK_E_UNSUPPORTED
 
 
+# Every tile configuration the fp16 GLU epilogue runs on (RK_F16_TILE; gate and
+# up tiles pair inside one wave, so the wave tile is a multiple of 32 columns):
+# ragged M and N, a K tail, equal bit for bit to the unfused products and glue.
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 8, 22])
+def test_f16_glu_gemm_every_tile(rk, orc, tile, monkeypatch):
+    lib = rk.lib()
+    for m, k, n in ((300, 520, 200), (257, 192, 100)):
+        note(f"fp16 gate|up GEMM + silu RK_F16_TILE={tile} m={m} k={k} n={n}")
+        r = np.random.default_rng(tile * 31 + m + n)
+        x = r.standard_normal((m, k)).astype(np.float16)
+        gate = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+        up = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+        wid = rk.pack_f16_glu(gate, up)
+        dx = rk.DeviceBuffer.from_array(x.view(np.uint16))
+        do = rk.DeviceBuffer(m * n * 4)
+        monkeypatch.setenv("RK_F16_TILE", str(tile))
+        assert lib.rk_matmul_f16_glu_dev(int(wid), dx.ptr, m, k, rk.GLU_SILU, do.ptr, 0, None) == 0, \
+            lib.rk_last_error()
+        rk.synchronize()
+        got = do.download((m, n), np.float32)
+        monkeypatch.delenv("RK_F16_TILE")
+        prods = []
+        for w in (gate, up):
+            dc = rk.DeviceBuffer(m * n * 2)
+            assert lib.rk_matmul_f16_dev(int(rk.pack(w)), dx.ptr, m, k, dc.ptr, None) == 0
+            rk.synchronize()
+            prods.append(dc.download((m, n), np.uint16).view(np.float16).astype(np.float32))
+        assert (got == rk.silu_mul(prods[0], prods[1])).all()
+        g16 = orc.f16_to_f32(orc.f32_to_f16(orc.gemm_f16(x, orc.f32_to_f16(gate))))
+        u16 = orc.f16_to_f32(orc.f32_to_f16(orc.gemm_f16(x, orc.f32_to_f16(up))))
+        ref = orc.silu_mul(g16, u16)
+        assert orc.cosine(got, ref) >= 0.9999 and orc.max_rel(got, ref) <= 1e-2
+
+
 def test_cast_dev_every_type_pair_rounds_to_nearest_even(rk, orc):
     # rk_cast_dev: the f32 <-> f16 / bf16 conversions either side of every op
     # (ext.rs:2144-2170), bit for bit against the oracle's RNE conversions
