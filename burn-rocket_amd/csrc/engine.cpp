@@ -835,7 +835,7 @@ int gemm_f16_run(CallScope &cs, const void *a, const void *b, void *c, int64_t m
 
 int check_m(int64_t m, int64_t k, const Weight *w, const char *op) {
   if (!w) return fail(RK_E_SHAPE, op, "weight id is not packed");
-  if (m <= 0) return fail(RK_E_SHAPE, op, "M must be positive");
+  if (m < 0) return fail(RK_E_SHAPE, op, "M must not be negative");
   if (m > INT32_MAX) return fail(RK_E_SHAPE, op, "M too large");
   if (k != w->k)
     return fail(RK_E_SHAPE, op, "activation K " + std::to_string(k) + " != weight K " +
@@ -852,6 +852,7 @@ extern "C" int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, 
   if (w->moe) return fail(RK_E_UNSUPPORTED, "rk_matmul", "an expert stack is not a matmul weight");
   if (w->glu_n > 0)
     return fail(RK_E_UNSUPPORTED, "rk_matmul", "gate|up weight: use rk_matmul_w8a8_glu_dev");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
   const int64_t n = w->n;
@@ -919,6 +920,7 @@ extern "C" int rk_matmul_f16(rk_weight_id id, const uint16_t *a, int64_t m, int6
   RK_TRY(check_m(m, k, w, op));
   if (w->kind != RK_WEIGHT_F16 || w->moe || w->glu_n > 0)
     return fail(RK_E_UNSUPPORTED, op, "weight is not a plain fp16 weight");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   if (!a || !c) return fail(RK_E_SHAPE, op, "null buffer");
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
@@ -947,6 +949,7 @@ extern "C" int rk_matmul_i8_gw(rk_weight_id id, const int8_t *a, const float *a_
   RK_TRY(check_m(m, k, w, op));
   if (w->kind != RK_WEIGHT_I8 || w->moe || w->glu_n > 0)
     return fail(RK_E_UNSUPPORTED, op, "weight is not a group-wise int8 weight");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   if (!a || !a_scale || !cf) return fail(RK_E_SHAPE, op, "null buffer");
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
@@ -994,6 +997,7 @@ extern "C" int rk_matmul_i8(rk_weight_id id, const int8_t *a, int64_t m, int64_t
   RK_TRY(check_m(m, k, w, op));
   if ((w->kind != RK_WEIGHT_I8 && w->kind != RK_WEIGHT_QAT) || w->moe || w->glu_n > 0)
     return fail(RK_E_UNSUPPORTED, op, "weight is not int8");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   if (!a || !c) return fail(RK_E_SHAPE, op, "null buffer");
   hipStream_t st = g_eng->stream;
   CallScope cs(st);
@@ -1021,6 +1025,7 @@ extern "C" int rk_matmul_f16_dev(rk_weight_id id, const void *a, int64_t m, int6
     return fail(RK_E_UNSUPPORTED, "rk_matmul_f16_dev", "weight is not fp16");
   if (w->glu_n > 0)
     return fail(RK_E_UNSUPPORTED, "rk_matmul_f16_dev", "gate|up weight: use rk_matmul_f16_glu_dev");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   CallScope cs(pick(stream));
   RK_TRY(gemm_f16_run(cs, a, w->codes, c, m, w->n, k, "rk_matmul_f16_dev"));
   g_eng->calls++;
@@ -1037,6 +1042,7 @@ extern "C" int rk_matmul_f16_glu_dev(rk_weight_id id, const void *a, int64_t m, 
   if (w->kind != RK_WEIGHT_F16 || w->moe || w->glu_n <= 0)
     return fail(RK_E_UNSUPPORTED, op, "weight was not packed by rk_pack_f16_glu");
   if (glu != RK_GLU_SILU && glu != RK_GLU_GELU) return fail(RK_E_SHAPE, op, "unknown glu kind");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   CallScope cs(pick(stream));
   RK_TRY(gemm_f16_run(cs, a, w->codes, out, m, w->n, k, op, glu, w->glu_n, out_f16 != 0));
   g_eng->calls++;
@@ -1050,6 +1056,7 @@ extern "C" int rk_quantize_rows_dev(const float *x, int64_t m, int64_t k, int64_
   if (m < 0 || k <= 0 || group <= 0 || k % group != 0)
     return fail(RK_E_SHAPE, "rk_quantize_rows_dev", "group must divide K");
   if (k / group > 1024) return fail(RK_E_SHAPE, "rk_quantize_rows_dev", "more than 1024 groups per row");
+  if (m == 0) return RK_OK;
   HIP_TRY(rk_launch_quantize_rows(x, m, k, group, q, scale, pick(stream)), "rk_quantize_rows_dev");
   return RK_OK;
 }
@@ -1069,6 +1076,7 @@ int w8a8_dev(rk_weight_id id, const int8_t *a, const float *a_scale, int64_t a_g
     mode = I8_PER_GROUP;
   else
     return fail(RK_E_SHAPE, op, "activation group must be K (per token) or the weight group");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   RK_TRY(launch_i8(*w, a, a_scale, (int)(k / a_group), (int)(a_group / 32), mode, out_f16, m, c,
                    pick(stream), op));
   g_eng->calls++;
@@ -1086,6 +1094,7 @@ extern "C" int rk_matmul_w8a8_glu_dev(rk_weight_id id, const int8_t *a, const fl
   RK_TRY(check_m(m, k, w, op));
   if (w->glu_n <= 0) return fail(RK_E_UNSUPPORTED, op, "weight was not packed by rk_pack_q8_0_glu");
   if (glu != RK_GLU_SILU && glu != RK_GLU_GELU) return fail(RK_E_SHAPE, op, "unknown glu kind");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   I8GemmArgs g;
   g.A = a;
   g.AS = a_scale;
@@ -1131,6 +1140,7 @@ extern "C" int rk_matmul_i8_raw_dev(rk_weight_id id, const int8_t *a, int64_t m,
   RK_TRY(check_m(m, k, w, "rk_matmul_i8_raw_dev"));
   if ((w->kind != RK_WEIGHT_I8 && w->kind != RK_WEIGHT_QAT) || w->moe)
     return fail(RK_E_UNSUPPORTED, "rk_matmul_i8_raw_dev", "weight is not int8");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   RK_TRY(launch_i8(*w, a, nullptr, 0, 1, I8_RAW, false, m, c, pick(stream), "rk_matmul_i8_raw_dev"));
   g_eng->calls++;
   return RK_OK;
@@ -1144,6 +1154,7 @@ extern "C" int rk_matmul_i8_partials_dev(rk_weight_id id, const int8_t *a, int64
   RK_TRY(check_m(m, k, w, "rk_matmul_i8_partials_dev"));
   if ((w->kind != RK_WEIGHT_I8 && w->kind != RK_WEIGHT_QAT) || w->moe)
     return fail(RK_E_UNSUPPORTED, "rk_matmul_i8_partials_dev", "weight is not int8");
+  if (m == 0) return RK_OK;  // an empty batch: nothing to compute (the reference returns [.., 0, N])
   RK_TRY(launch_i8(*w, a, nullptr, 0, 1, I8_PARTIALS, false, m, p, pick(stream),
                    "rk_matmul_i8_partials_dev"));
   g_eng->calls++;

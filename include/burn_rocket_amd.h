@@ -196,7 +196,12 @@ int rk_weight_info(rk_weight_id id, int *kind, int64_t *n, int64_t *k,
  * their buffers through page-locked staging slots (hipHostMalloc) with a
  * pool of CPU copy threads; row-separable ops run in row chunks so that the
  * upload of one chunk, the kernels of the previous one and the download of
- * the one before overlap. They return when the outputs are in host memory. */
+ * the one before overlap. They return when the outputs are in host memory.
+ *
+ * Every matmul entry accepts M = 0 (an empty batch): the arguments are
+ * checked as for any M, nothing is launched and RK_OK is returned, as the
+ * reference's row-chunk loop (`while off < m`, ext.rs:1457) runs no chunk and
+ * returns an empty [.., 0, N] tensor. */
 
 /* y[M, N] = x[M, K] · Wᵀ for any resident weight, host f32 in and out
  * (`rocket_matmul` → matmul_impl, ext.rs:627, ext.rs:1208-1232):
@@ -213,7 +218,7 @@ int rk_matmul(rk_weight_id id, const float *x, int64_t m, int64_t k, float *y);
 /* fp16 GEMM on host buffers (`RocketCtx::matmul_prepacked`, lib.rs:244-254;
  * Context::matmul_prepacked, context.rs:497-513): a fp16 [M, K], c fp16
  * [M, N], f32 accumulation. The reference's M % 4 padding
- * (lib.rs:500-511) is not needed: any M >= 1. */
+ * (lib.rs:500-511) is not needed: any M >= 0. */
 int rk_matmul_f16(rk_weight_id id, const uint16_t *a, int64_t m, int64_t k, uint16_t *c);
 /* `I8Context::matmul_gw` (int8.rs:644-676) on host buffers, as Clef's expert
  * workers call it (src/clef/engine_npu.rs:75-110): a int8 codes [M, K]

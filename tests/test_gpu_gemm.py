@@ -137,6 +137,50 @@ def test_shape_errors_are_reported(rk):
     assert ms.n_weights >= 1 and ms.weights_bytes >= 16 * 64 * 2
 
 
+def test_empty_batch_is_a_no_op(rk, orc):
+    # The reference's row-chunk loop (ext.rs:1457) runs no chunk for M = 0 and
+    # returns an empty [.., 0, N]; every matmul entry returns RK_OK with no
+    # launch, while a bad id, K or mode is still reported.
+    note("M = 0 on every matmul entry")
+    lib = rk.lib()
+    k, n = 64, 48
+    r = np.random.default_rng(3)
+    w = (r.standard_normal((n, k)) * 0.1).astype(np.float32)
+    f16, i8 = rk.pack(w), rk.pack_i8(w, 32)
+    wq, wd = orc.q8_0_quantize(w)
+    q8 = rk.pack_q8_0(orc.q8_0_blocks(wq, wd), n, k)
+    f16_glu, q8_glu = rk.pack_f16_glu(w, w), rk.pack_q8_0_glu_f32(w, w)
+    for wid in (f16, i8, q8):
+        assert rk.matmul(np.zeros((0, k), np.float32), wid).shape == (0, n)
+        assert rk.matmul(np.zeros((3, 0, k), np.float32), wid).shape == (3, 0, n)
+    calls = [
+        ("rk_matmul_f16", lambda kk: lib.rk_matmul_f16(int(f16), None, 0, kk, None)),
+        ("rk_matmul_i8_gw", lambda kk: lib.rk_matmul_i8_gw(int(i8), None, None, None, 0, kk, None)),
+        ("rk_matmul_i8", lambda kk: lib.rk_matmul_i8(int(i8), None, 0, kk, None)),
+        ("rk_matmul_f16_dev", lambda kk: lib.rk_matmul_f16_dev(int(f16), None, 0, kk, None, None)),
+        ("rk_matmul_f16_glu_dev",
+         lambda kk: lib.rk_matmul_f16_glu_dev(int(f16_glu), None, 0, kk, rk.GLU_SILU, None, 0, None)),
+        ("rk_matmul_w8a8_dev", lambda kk: lib.rk_matmul_w8a8_dev(int(q8), None, None, 32, 0, kk, None, None)),
+        ("rk_matmul_w8a8_f16out_dev",
+         lambda kk: lib.rk_matmul_w8a8_f16out_dev(int(q8), None, None, kk, 0, kk, None, None)),
+        ("rk_matmul_w8a8_glu_dev",
+         lambda kk: lib.rk_matmul_w8a8_glu_dev(int(q8_glu), None, None, 0, kk, rk.GLU_GELU, None, 1, None)),
+        ("rk_matmul_i8_raw_dev", lambda kk: lib.rk_matmul_i8_raw_dev(int(q8), None, 0, kk, None, None)),
+        ("rk_matmul_i8_partials_dev", lambda kk: lib.rk_matmul_i8_partials_dev(int(q8), None, 0, kk, None, None)),
+        ("rk_quantize_rows_dev", lambda kk: lib.rk_quantize_rows_dev(None, 0, kk, 32, None, None, None)),
+    ]
+    for name, call in calls:
+        assert call(k) == rk.RK_OK, (name, lib.rk_last_error())
+        if name != "rk_quantize_rows_dev":
+            assert call(k + 32) == rk.RK_E_SHAPE, name  # K still checked
+    assert lib.rk_matmul_f16_dev(987654321, None, 0, k, None, None) == rk.RK_E_SHAPE
+    assert lib.rk_matmul_f16_glu_dev(int(f16_glu), None, 0, k, 7, None, 0, None) == rk.RK_E_SHAPE
+    assert lib.rk_matmul_w8a8_dev(int(q8), None, None, 48, 0, k, None, None) == rk.RK_E_SHAPE
+    assert lib.rk_matmul_f16_dev(int(q8), None, 0, k, None, None) == rk.RK_E_UNSUPPORTED
+    assert lib.rk_matmul_f16_dev(int(f16), None, -1, k, None, None) == rk.RK_E_SHAPE
+    rk.synchronize()
+
+
 # Every tile configuration of the fp16 kernel (RK_F16_TILE): ragged M and N,
 # a K tail inside a 64-value stage, and K of one and two stages (fewer stages
 # than the pipeline prologue issues).
