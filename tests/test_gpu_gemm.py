@@ -184,7 +184,7 @@ def test_empty_batch_is_a_no_op(rk, orc):
 # Every tile configuration of the fp16 kernel (RK_F16_TILE): ragged M and N,
 # a K tail inside a 64-value stage, and K of one and two stages (fewer stages
 # than the pipeline prologue issues).
-F16_TILES = list(range(23))
+F16_TILES = list(range(24))
 
 
 @pytest.mark.parametrize("tile", F16_TILES)
