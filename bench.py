@@ -11,8 +11,10 @@ timed steps (2·M·K·N per GEMM), measured with HIP events on the library
 stream around the whole timed region. `roofline` is the up-projection
 kernel's average launch time (K back-to-back launches between two events on
 the same stream, right after the timed region) against the MI355X dense int8
-MFMA peak. `extras` times the other four workloads the same way;
-`cpu_baseline` times the oracle's C restatement of the reference's W8A8 path
+MFMA peak. `extras` times the other four workloads the same way, before the
+headline (the card's clocks then have settled when its steps are timed), except
+the host-buffer pass, which runs after it; `cpu_baseline` times the oracle's C
+restatement of the reference's W8A8 path
 on the host cores (all of them, and one core) over a bounded sample; every
 `extras` entry carries its own `cpu_baseline` of the same kind.
 """
@@ -722,14 +724,14 @@ def main():
     if a.traffic_probe:
         traffic_probe(layers, TRAFFIC_LAUNCHES)
         return
-    log("W8A8 config ready; timing")
-    ms, up_ms, wall = run_headline(layers, a.steps, a.warmup)
-    m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]
-    ops_gemm = 2.0 * m * h * i
-    value = 2 * ops_gemm / ms / 1e9
-    achieved = ops_gemm / up_ms / 1e9
-    log(f"step {ms:.4f} ms, up-proj {up_ms:.4f} ms, {value:.1f} TOP/s")
-
+    # The other device-resident workloads run first, then the headline: the
+    # card's clocks take ~10 ms of sustained work to settle after the
+    # host-side set-up, so a headline timed first after a few warm-up steps
+    # (five are 0.3 ms of work) reads the power-state ramp rather than the
+    # kernels. The headline's own W warm-up and K timed steps are unchanged;
+    # they only come later. The extras that use the headline's buffers
+    # re-quantize the same activations (per token, identical codes) and
+    # overwrite only its output.
     extras = {}
     if not a.no_extras:
         for key, fn in (("w8a8_forms_3633", lambda: extra_w8a8_forms(layers, 50)),
@@ -740,10 +742,21 @@ def main():
                         ("vision_layer_2394", lambda: extra_vision(50)),
                         ("gemma_attention_d256_2587", lambda: extra_gemma_attention(50)),
                         ("moe_30b_a3b_1024", lambda: extra_moe(20)),
-                        ("glue_qwen3_3633", lambda: extra_glue(50)),
-                        ("host_path_w8a8_pair_3633", lambda: extra_host_path(layers, 10))):
+                        ("glue_qwen3_3633", lambda: extra_glue(50))):
             log(f"extra {key}")
             extras[key] = fn()
+
+    log("W8A8 config ready; timing")
+    ms, up_ms, wall = run_headline(layers, a.steps, a.warmup)
+    m, h, i = synth.W8A8["m"], synth.W8A8["hidden"], synth.W8A8["inter"]
+    ops_gemm = 2.0 * m * h * i
+    value = 2 * ops_gemm / ms / 1e9
+    achieved = ops_gemm / up_ms / 1e9
+    log(f"step {ms:.4f} ms, up-proj {up_ms:.4f} ms, {value:.1f} TOP/s")
+    if not a.no_extras:
+        # after the headline: its PCIe copies leave the card mostly idle
+        log("extra host_path_w8a8_pair_3633")
+        extras["host_path_w8a8_pair_3633"] = extra_host_path(layers, 10)
 
     cpu = None
     if not a.no_cpu_baseline:
